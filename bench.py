@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Benchmark of the INT4 KV-cache data plane on one MI355X.
+
+Headline ("config 2"): one decode step of paged
+attention over INT4 KV pages — batch 16, 32 heads, head_dim 128, context
+4096 per sequence, 16-token pages (group-64 codes + fp16 scales), block
+tables a seeded random permutation of the page pool, retain_ratio 1.0.
+A "step" is one ``dynamic_sparse_attention`` call over the whole batch with
+inputs resident in HBM. ``value`` = effective KV bytes (codes + fp16 scales,
+285,212,672 B) / seconds per step, in GB/s.
+
+The pool holds two disjoint page sets and steps alternate between them, so a
+step never re-reads what the previous step left in the 256 MB last-level
+cache. The JSON line also carries the roofline of the decode kernel (timed
+with HIP events on the stream it runs on), a CPU baseline (the reference's
+torch CPU path, restated in oracle/, on a bounded sample), and secondary
+figures (KV-quant write path GB/s).
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "memopt-transformer-runtime_amd"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+CFG2 = dict(batch=16, heads=32, head_dim=128, ctx=4096, block=16, outlier_frac=0.005, outlier_mult=10.0, seed=0)
+
+
+def effective_kv_bytes(batch, heads, head_dim, tokens):
+    """Codes (D/2 bytes per token-head, K and V) + fp16 scales (D/64 per token-head, K and V)."""
+    return 2 * batch * heads * tokens * (head_dim // 2 + 2 * (head_dim // 64))
+
+
+def profile_traffic(name):
+    """HBM bytes per launch recorded from rocprofv3 --pmc runs (profiles/), if present."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def setup_decode(torch, memopt_C, cfg, copies=2):
+    """INT4 page pool with `copies` disjoint page sets for config 2."""
+    B, H, D, ctx, bs = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
+    nbps = ctx // bs
+    nb = copies * B * nbps
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    dev = torch.device("cuda", 0)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(cfg["seed"])).to(torch.int32)
+    tables = [perm[c * B * nbps:(c + 1) * B * nbps].reshape(B, nbps).to(dev) for c in range(copies)]
+    g = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    for bt in tables:
+        slots = (bt.long()[:, :, None] * bs + torch.arange(bs, device=dev)).reshape(-1).to(torch.int32)
+        for b0 in range(0, B, 4):
+            n = min(4, B - b0) * ctx
+            kv = []
+            for _ in range(2):
+                x = torch.randn(n, H, D, device=dev, generator=g)
+                m = torch.rand(n, H, D, device=dev, generator=g) < cfg["outlier_frac"]
+                kv.append(torch.where(m, x * cfg["outlier_mult"], x).half())
+            memopt_C.write_cache(kv[0], kv[1], bt, slots[b0 * ctx:b0 * ctx + n].contiguous())
+            del kv
+    q = torch.randn(B, 1, H, D, device=dev, generator=g).half()
+    cl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    kc, vc = memopt_C.get_pool_tensors()
+    calls = [memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, ctx) for bt in tables]
+    torch.cuda.synchronize()
+    return calls, tables, q, cl
+
+
+def time_steps(torch, fn_list, steps, warmup):
+    """Returns (ms per step over the timed region, mean per-launch ms from event pairs)."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn_list[i % len(fn_list)]()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        fn_list[i % len(fn_list)]()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    launch_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
+    region_ms = starts[0].elapsed_time(ends[-1]) / steps
+    return region_ms, launch_ms, wall_ms
+
+
+def cpu_baseline_decode(torch, O, memopt_C, tables, q, cl, cfg, budget_s=15.0):
+    """Reference CPU path (dequantize + gather + fp32 SDPA) on a bounded sample of config 2."""
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    kc, vc = memopt_C.get_pool_tensors()
+    ks, vs = memopt_C.get_pool_scales()
+    bt = tables[0]
+    nseq = 2
+    pages = bt[:nseq].reshape(-1).long()
+    # Copy only the sampled sequences' pages to host memory.
+    sub = lambda t: t[pages].cpu()
+    ck, sk, cv, sv = sub(kc), sub(ks), sub(vc), sub(vs)
+    local_bt = torch.arange(pages.numel(), dtype=torch.int32).reshape(nseq, -1)
+    qc, clc = q[:nseq].cpu(), cl[:nseq].cpu()
+    ctx = cfg["ctx"]
+    times = []
+    O.decode_int4_torch(qc, ck, sk, cv, sv, local_bt, clc, ctx, 0)  # warm-up
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 and time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        O.decode_int4_torch(qc, ck, sk, cv, sv, local_bt, clc, ctx, 0)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    nbytes = effective_kv_bytes(nseq, cfg["heads"], cfg["head_dim"], ctx)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{nseq} of {cfg['batch']} sequences of config 2 (dequantize + gather + fp32 SDPA, torch CPU), "
+                      f"median of {len(times)} after 1 warm-up"}
+
+
+def bench_kv_quant(torch, memopt_C, cfg, steps=20):
+    """Fused write + quantize of config 2's K and V into INT4 pages (write_cache), GB/s."""
+    B, H, D, ctx, bs = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
+    dev = torch.device("cuda", 0)
+    T = 4 * ctx  # 4 sequences per launch
+    g = torch.Generator(device=dev).manual_seed(1)
+    k = torch.randn(T, H, D, device=dev, generator=g).half()
+    v = torch.randn(T, H, D, device=dev, generator=g).half()
+    slots = torch.arange(T, dtype=torch.int32, device=dev)
+    bt = torch.zeros(1, 1, dtype=torch.int32, device=dev)
+    region_ms, launch_ms, _ = time_steps(torch, [lambda: memopt_C.write_cache(k, v, bt, slots, validate_slots=False)], steps, 3)
+    elems = 2 * T * H * D
+    nbytes = elems * 2.53125
+    return {"workload": "write_cache fused quantize, 2 x [16384, 32, 128] fp16 -> INT4 pages",
+            "GB/s": round(nbytes / (launch_ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_elem": 2.53125}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="skip secondary figures")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the path is single-GPU; multi-GPU sharding is "
+              "design-only, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import memopt_C  # noqa: E402  (fails loudly if the HIP library is missing)
+
+    cfg = CFG2
+    calls, tables, q, cl = setup_decode(torch, memopt_C, cfg)
+    region_ms, launch_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup)
+    nbytes = effective_kv_bytes(cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"])
+    value = nbytes / (region_ms * 1e-3) / 1e9
+    achieved = nbytes / (launch_ms * 1e-3) / 1e9
+    line = {
+        "metric": "INT4 paged decode-attn HBM GB/s (% peak); prefill MFMA util; KV-quant GB/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(region_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes, fp16 x fp16 -> fp32",
+        "data": "synthetic (seeded N(0,1) K/V with 0.5% x10 outliers, quantized on device)",
+        "config": {"workload": "BASELINE configs[1] decode: batch 16, 32 heads, head_dim 128, context 4096, "
+                               "INT4 16-token pages (group 64, fp16 scales), random-permutation block tables, "
+                               "retain_ratio 1.0",
+                   "effective_kv_bytes": nbytes, "page_sets_rotated": len(calls)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profile_traffic("decode_int4_config2_pmc.txt"),
+                     "kernel": "decode_int4_kernel<128, half>", "kernel_ms": round(launch_ms, 5)},
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O  # CPU baseline leg only
+        line["cpu_baseline"] = cpu_baseline_decode(torch, O, memopt_C, tables, q, cl, cfg)
+    if not args.no_secondary:  # overwrites pool pages: runs last
+        line["secondary"] = {"kv_quant": bench_kv_quant(torch, memopt_C, cfg)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

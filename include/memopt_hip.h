@@ -1,0 +1,202 @@
+/*
+ * memopt_hip.h — C ABI of the MI355X (gfx950) INT4 KV-cache data plane.
+ *
+ * Every entry point takes plain device pointers, 64-bit sizes and a
+ * hipStream_t (passed as void*), returns an int status (MEMOPT_OK == 0) and
+ * records a human-readable message retrievable with memopt_last_error()
+ * (thread-local). No libtorch types cross this boundary: callers allocate
+ * device memory themselves (the Python `memopt_C` shim uses torch tensors)
+ * and keep it alive while the library uses it.
+ *
+ * Each declaration names the reference interface it replaces:
+ * TheRadDani/memopt-transformer-runtime, pybind11 module `memopt_C`
+ * (src/csrc/extension.cpp) and the C++ functions it binds.
+ *
+ * Kernel entry points are asynchronous on `stream`; launch errors are
+ * reported through the status code.
+ */
+#ifndef MEMOPT_HIP_H
+#define MEMOPT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Status codes                                                             */
+/* ------------------------------------------------------------------------ */
+#define MEMOPT_OK               0
+#define MEMOPT_ERR_INVALID      1  /* contract violation (shape/dtype/range) */
+#define MEMOPT_ERR_STATE        2  /* pool not initialized                    */
+#define MEMOPT_ERR_HIP          3  /* HIP runtime / launch error              */
+#define MEMOPT_ERR_UNSUPPORTED  4  /* configuration not compiled in           */
+
+/* KV pool storage formats (memopt_init_pool `kv_format`). */
+#define MEMOPT_KV_FP16  0  /* fp16 [num_blocks, block_size, H, D] (reference layout)     */
+#define MEMOPT_KV_INT4  1  /* INT4 pages: codes u8 [num_blocks, H, block_size, D/2],     *
+                            * fp16 scales [num_blocks, H, block_size, D/64]              */
+
+/* Scale element types for INT4 caches passed to attention. */
+#define MEMOPT_SCALE_F32 0
+#define MEMOPT_SCALE_F16 1
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *memopt_last_error(void);
+
+/* Replaces get_hello() — src/csrc/extension.cpp:6-8. */
+const char *memopt_get_hello(void);
+
+/* ------------------------------------------------------------------------ */
+/* Paged pool (host free list + registered device storage)                 */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces init_pool(num_blocks, block_size, num_heads, head_dim) —
+ * src/csrc/kv_cache.cu:112-153, bound at src/csrc/extension.cpp:20-26.
+ * The caller allocates zero-filled storage and passes it in:
+ *   MEMOPT_KV_FP16: key/value = fp16 [nb, bs, H, D]; key_scales/value_scales unused.
+ *   MEMOPT_KV_INT4: key/value = u8 codes [nb, H, bs, D/2];
+ *                   key_scales/value_scales = fp16 [nb, H, bs, D/64].
+ * The free list is reseeded FIFO 0..nb-1. Invalid parameters tear the pool
+ * down and return MEMOPT_ERR_INVALID. */
+int memopt_init_pool(int64_t num_blocks, int32_t block_size, int32_t num_heads,
+                     int32_t head_dim, int32_t kv_format, void *key_pool,
+                     void *value_pool, void *key_scales, void *value_scales);
+
+/* Reports the live pool's parameters; returns 1 if a pool is initialized,
+ * 0 otherwise (outputs untouched). Used for init_pool's idempotency
+ * (src/csrc/kv_cache.cu:115-122). */
+int memopt_pool_info(int64_t *num_blocks, int32_t *block_size, int32_t *num_heads,
+                     int32_t *head_dim, int32_t *kv_format);
+
+/* Drops the pool (storage pointers are forgotten; the caller frees them). */
+int memopt_reset_pool(void);
+
+/* Replaces allocate_block() — src/csrc/kv_cache.cu:163-172. *block_idx = -1
+ * when exhausted (not an error). */
+int memopt_allocate_block(int64_t *block_idx);
+
+/* Replaces free_block(block_idx) — src/csrc/kv_cache.cu:179-185. */
+int memopt_free_block(int64_t block_idx);
+
+/* Replaces free_blocks_count() — src/csrc/kv_cache.cu:198-201. */
+int memopt_free_blocks_count(int64_t *count);
+
+/* Replaces write_cache(keys, values, block_tables, slot_mapping) —
+ * src/csrc/kv_cache.cu:282-348. keys/values: fp16 [num_tokens, H, D]
+ * contiguous; slot_mapping: int32 [num_tokens], slot = block*bs + pos.
+ * FP16 pools get a scatter copy; INT4 pools get a fused group-64 quantize
+ * into the page (codes bit-exact with memopt_quantize_kv_cache_int4, scales
+ * stored as RNE fp16 of the fp32 scale). Slots outside the pool are skipped
+ * on device; the caller validates them beforehand. */
+int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
+                       int32_t num_heads, int32_t head_dim,
+                       const int32_t *slot_mapping, void *stream);
+
+/* Replaces evict_cache(block_tables, attention_scores, retain_ratio,
+ * num_sink_tokens) — src/csrc/kv_cache.cu:379-559. scores: f32
+ * [num_blocks, block_size, H]. Per (block, head): keep = max(1,
+ * floor(r*bs)) largest scores, zero rows scoring below the keep-th
+ * largest (sinks ignored, as in the reference). */
+int memopt_evict_cache(const float *attention_scores, int64_t num_blocks,
+                       float retain_ratio, int32_t num_sink_tokens, void *stream);
+
+/* Replaces evict_tokens(attention_scores, block_tables, is_block_free,
+ * retain_ratio, num_sink_tokens) — src/csrc/kv_cache.cu:640-1156.
+ * scores f32 [num_seqs, H, seq_len]; block_tables i32 [num_seqs, max_blocks]
+ * (mutated); is_block_free i32 [total_pool_blocks] (mutated, caller zeroes).
+ * Per (seq, head): sinks t < num_sink_tokens always kept; keep =
+ * clamp(ceilf(r*L), 1, L); tokens scoring below the exact keep-th largest
+ * (sink-boosted) score are evicted; their (token, head) rows are zeroed
+ * (INT4: codes 0x88, scale 1.0). A logical block with all block_size
+ * positions evicted votes is_block_free[phys] += 1; the vote reaching H
+ * unlinks block_tables[seq, lb] = -1. No seq_len cap. */
+int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs,
+                        int32_t num_heads, int32_t seq_len, int32_t *block_tables,
+                        int32_t max_blocks_per_seq, int32_t *is_block_free,
+                        int64_t total_pool_blocks, float retain_ratio,
+                        int32_t num_sink_tokens, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Quantization (surface, whole-tensor)                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces quantize_kv_cache_int4(cache, group_size) —
+ * src/csrc/quantization.cu:104-203, :294-353. cache: fp16, numel elements,
+ * contiguous; packed_out: u8 [numel/2]; scales_out: f32 [numel/64].
+ * scale = absmax>0 ? absmax/7 : 1 (IEEE fp32); code = clamp(roundf(v/scale)
+ * + 8, 0, 15); byte = code[2i] | code[2i+1] << 4. */
+int memopt_quantize_kv_cache_int4(const void *cache, int64_t numel, int64_t last_dim,
+                                  int32_t group_size, uint8_t *packed_out,
+                                  float *scales_out, void *stream);
+
+/* Replaces dequantize_kv_cache_int4(q_cache, scales, group_size) —
+ * src/csrc/quantization.cu:232-270, :371-428. out: fp16 [2*packed_numel],
+ * value = fp16(RNE(float(code-8) * scale)). */
+int memopt_dequantize_kv_cache_int4(const uint8_t *packed, int64_t packed_numel,
+                                    const float *scales, int64_t num_scales,
+                                    int32_t group_size, void *out, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Paged attention                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces dynamic_sparse_attention(query, key_cache, value_cache,
+ * block_tables, context_lens, max_seq_len, window_size) —
+ * src/csrc/attention.cu:98-339, :371-521 — with reference semantics:
+ * non-causal, keys j in [max(0, ctx-W), ctx) for every query, pages with
+ * block_tables < 0 skipped, W <= 0 or W > max_seq_len -> max_seq_len,
+ * scale 1/sqrtf(D), empty key set -> 0. fp16 pool [nb, bs, H, D]. */
+int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_len,
+                                    int32_t num_heads, int32_t head_dim,
+                                    const void *key_cache, const void *value_cache,
+                                    int64_t num_kv_blocks, int32_t block_size,
+                                    const int32_t *block_tables,
+                                    int32_t max_blocks_per_seq,
+                                    const int32_t *context_lens, int32_t max_seq_len,
+                                    int32_t window_size, void *out, void *stream);
+
+/* Extended paged attention: the reference semantics above plus
+ *   - INT4 caches (codes + f32/f16 group-64 scales, arbitrary page/head/token
+ *     strides, dequantized just in time) — replaces the reference's
+ *     dequantize_kv_cache_int4 -> dynamic_sparse_attention composition;
+ *   - attention sinks (keys j < num_sink_tokens always visible, the token
+ *     rule of src/memopt/triton_attention.py:523-532);
+ *   - causal mode (query i at absolute position ctx-q_len+i sees
+ *     j <= pos && (j < sinks || j >= pos-W+1), scripts/bench_accuracy.py:253-280).
+ * With num_sink_tokens == 0, causal == 0 and an fp16 cache it computes the
+ * same function as memopt_dynamic_sparse_attention.
+ * `workspace` (device, >= memopt_attention_workspace_size bytes) holds
+ * split-K partials; it may be NULL when that size is 0. */
+typedef struct memopt_attn_desc {
+  const void *query;          /* fp16 [batch, q_len, H, D] contiguous        */
+  void *out;                  /* fp16 [batch, q_len, H, D] contiguous        */
+  int32_t batch, q_len, num_heads, head_dim;
+  int32_t kv_is_int4;         /* 0: fp16 cache, 1: INT4 codes + scales       */
+  const void *key_cache;      /* fp16 elements or u8 codes                   */
+  const void *value_cache;
+  const void *key_scales;     /* INT4 only                                   */
+  const void *value_scales;
+  int32_t scale_dtype;        /* MEMOPT_SCALE_F32 / MEMOPT_SCALE_F16         */
+  int32_t block_size;         /* tokens per page                             */
+  int64_t num_kv_blocks;
+  /* Strides: fp16 cache in elements; INT4 codes in bytes; scales in elements. */
+  int64_t kv_page_stride, kv_head_stride, kv_token_stride;
+  int64_t sc_page_stride, sc_head_stride, sc_token_stride;
+  const int32_t *block_tables; /* [batch, max_blocks_per_seq]                */
+  int32_t max_blocks_per_seq;
+  const int32_t *context_lens; /* [batch]                                    */
+  int32_t max_seq_len, window_size, num_sink_tokens, causal;
+  void *workspace;
+  int64_t workspace_bytes;
+} memopt_attn_desc;
+
+int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes);
+int memopt_paged_attention(const memopt_attn_desc *desc, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEMOPT_HIP_H */

@@ -1,0 +1,282 @@
+// attention.hip — paged attention entry points and the generic kernel.
+//
+// Reference: TheRadDani/memopt-transformer-runtime src/csrc/attention.cu:371-521
+// (dynamic_sparse_attention host checks, window clamp :453-455, scale
+// 1/sqrtf(D) :460, kernel semantics :158-186 and :333-338).
+//
+// Dispatch:
+//   * INT4 cache, q_len == 1, 16-token pages, D in {64, 128}, aligned
+//     strides -> decode_int4 (split-K, HBM-streaming; decode_int4.hip);
+//   * fp16 or INT4 cache, q_len >= 16, D in {64, 128}, 16-token pages ->
+//     prefill (fp16 MFMA; prefill.hip);
+//   * anything else -> generic_attention_kernel below: one wave per
+//     (b, query, head), lanes over head dims, keys visited in order with an
+//     online softmax. INT4 elements are dequantized to fp16 exactly as the
+//     reference's dequantize kernel would (fp16(RNE((code-8)*scale))) before
+//     use, so it computes the reference composition.
+#include "attention.hpp"
+
+namespace memopt {
+
+struct GenericParams {
+  const half_t *q;
+  half_t *out;
+  int32_t B, Lq, H, D;
+  int32_t int4, scale_f16;
+  const void *kc, *vc, *ks, *vs;
+  int64_t kv_ps, kv_hs, kv_ts, sc_ps, sc_hs, sc_ts;
+  int32_t bs;
+  int64_t nb;
+  const int32_t *bt;
+  int32_t M;
+  const int32_t *ctx;
+  int32_t W, sinks, causal;
+  float scale;
+};
+
+__device__ __forceinline__ float kv_elem(const GenericParams &p, const void *cache, const void *scales,
+                                         int64_t page, int32_t pos, int32_t head, int32_t d) {
+  if (!p.int4) {
+    const half_t *c = (const half_t *)cache;
+    return (float)c[page * p.kv_ps + (int64_t)pos * p.kv_ts + (int64_t)head * p.kv_hs + d];
+  }
+  const uint8_t *c = (const uint8_t *)cache;
+  const uint8_t byte = c[page * p.kv_ps + (int64_t)pos * p.kv_ts + (int64_t)head * p.kv_hs + (d >> 1)];
+  const int code = (d & 1) ? (byte >> 4) : (byte & 0xF);
+  const int64_t si = page * p.sc_ps + (int64_t)pos * p.sc_ts + (int64_t)head * p.sc_hs + (d >> 6);
+  const float s = p.scale_f16 ? (float)((const half_t *)scales)[si] : ((const float *)scales)[si];
+  return (float)(half_t)((float)(code - 8) * s);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += shfl_xor(v, off);
+  return v;
+}
+
+constexpr int kMaxDimPerLane = 4;  // D <= 256
+
+__global__ __launch_bounds__(64) void generic_attention_kernel(const GenericParams p) {
+  const int32_t h = blockIdx.x, qi = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+  const int32_t ctx = p.ctx[b];
+  const int32_t pos = ctx - p.Lq + qi;
+  const KeyRange kr = key_range(ctx, pos, p.W, p.sinks, p.causal != 0);
+  float qv[kMaxDimPerLane], acc[kMaxDimPerLane];
+  const half_t *qrow = p.q + (((int64_t)b * p.Lq + qi) * p.H + h) * p.D;
+#pragma unroll
+  for (int i = 0; i < kMaxDimPerLane; ++i) {
+    const int d = lane + 64 * i;
+    qv[i] = d < p.D ? (float)qrow[d] : 0.0f;
+    acc[i] = 0.0f;
+  }
+  float m = -INFINITY, l = 0.0f;
+  const int32_t lim = min(kr.hi, p.M * p.bs);
+  const int32_t w0 = max(kr.win_lo, kr.sink_end);
+  for (int pass = 0; pass < 2; ++pass) {
+    const int32_t j0 = pass == 0 ? 0 : w0;
+    const int32_t j1 = pass == 0 ? min(kr.sink_end, lim) : lim;
+    for (int32_t j = j0; j < j1; ++j) {
+      const int32_t page = p.bt[(int64_t)b * p.M + j / p.bs];
+      if (page < 0 || page >= p.nb) continue;
+      const int32_t ps = j % p.bs;
+      float part = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kMaxDimPerLane; ++i) {
+        const int d = lane + 64 * i;
+        if (d < p.D) part += qv[i] * kv_elem(p, p.kc, p.ks, page, ps, h, d);
+      }
+      const float s = wave_sum(part) * p.scale;
+      const float mn = fmaxf(m, s);
+      const float alpha = (mn == m) ? 1.0f : __expf(m - mn);
+      const float pw = __expf(s - mn);
+      l = l * alpha + pw;
+#pragma unroll
+      for (int i = 0; i < kMaxDimPerLane; ++i) {
+        const int d = lane + 64 * i;
+        if (d < p.D) acc[i] = acc[i] * alpha + pw * kv_elem(p, p.vc, p.vs, page, ps, h, d);
+      }
+      m = mn;
+    }
+  }
+  half_t *orow = p.out + (((int64_t)b * p.Lq + qi) * p.H + h) * p.D;
+#pragma unroll
+  for (int i = 0; i < kMaxDimPerLane; ++i) {
+    const int d = lane + 64 * i;
+    if (d < p.D) orow[d] = (half_t)(l > 0.0f ? acc[i] / l : 0.0f);
+  }
+}
+
+static bool aligned_to(const void *p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+static int32_t effective_window(int32_t window, int32_t max_seq_len) {
+  return (window <= 0 || window > max_seq_len) ? max_seq_len : window;
+}
+
+// Upper bound of pages one sequence visits (sizes the split count).
+static int32_t max_pages_visited(const memopt_attn_desc &d) {
+  const int32_t W = effective_window(d.window_size, d.max_seq_len);
+  int64_t win = (int64_t)W / d.block_size + 2;
+  int64_t sink = (int64_t)(d.num_sink_tokens + d.block_size - 1) / d.block_size;
+  int64_t v = win + sink;
+  if (v > d.max_blocks_per_seq) v = d.max_blocks_per_seq;
+  return (int32_t)v;
+}
+
+static bool use_decode_int4(const memopt_attn_desc &d) {
+  if (!d.kv_is_int4 || d.q_len != 1 || d.block_size != 16) return false;
+  if (d.head_dim != 64 && d.head_dim != 128) return false;
+  const int64_t bpl = d.head_dim / 8;
+  if (!aligned_to(d.key_cache, bpl) || !aligned_to(d.value_cache, bpl)) return false;
+  if (d.kv_page_stride % bpl || d.kv_head_stride % bpl || d.kv_token_stride % bpl) return false;
+  if (!aligned_to(d.query, 16)) return false;
+  return true;
+}
+
+static int validate(const memopt_attn_desc &d) {
+  MEMOPT_REQUIRE(d.batch >= 0 && d.q_len >= 0 && d.num_heads >= 0 && d.head_dim >= 0, MEMOPT_ERR_INVALID,
+                 "paged_attention: negative dimension");
+  MEMOPT_REQUIRE(d.head_dim % 2 == 0 && d.head_dim <= 64 * kMaxDimPerLane, MEMOPT_ERR_INVALID,
+                 "paged_attention: head_dim must be even and <= 256");
+  MEMOPT_REQUIRE(d.block_size > 0, MEMOPT_ERR_INVALID, "paged_attention: block_size must be > 0");
+  MEMOPT_REQUIRE(d.max_blocks_per_seq >= 0, MEMOPT_ERR_INVALID, "paged_attention: bad max_blocks_per_seq");
+  if (d.kv_is_int4) {
+    MEMOPT_REQUIRE(d.head_dim % 64 == 0, MEMOPT_ERR_INVALID,
+                   "paged_attention: INT4 caches need head_dim % 64 == 0");
+    MEMOPT_REQUIRE(d.key_scales && d.value_scales, MEMOPT_ERR_INVALID, "paged_attention: INT4 needs scales");
+    MEMOPT_REQUIRE(d.scale_dtype == MEMOPT_SCALE_F32 || d.scale_dtype == MEMOPT_SCALE_F16, MEMOPT_ERR_INVALID,
+                   "paged_attention: unknown scale dtype");
+  }
+  return MEMOPT_OK;
+}
+
+static int decode_workspace(const memopt_attn_desc &d, int32_t *splits, int64_t *bytes) {
+  *splits = decode_splits(d.batch, d.num_heads, max_pages_visited(d));
+  *bytes = (*splits > 1) ? (int64_t)d.batch * d.num_heads * (*splits) * (d.head_dim + 2) * 4 : 0;
+  return MEMOPT_OK;
+}
+
+}  // namespace memopt
+
+using namespace memopt;
+
+extern "C" {
+
+int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes) {
+  MEMOPT_REQUIRE(desc && bytes, MEMOPT_ERR_INVALID, "attention_workspace_size: null argument");
+  int rc = validate(*desc);
+  if (rc != MEMOPT_OK) return rc;
+  *bytes = 0;
+  if (use_decode_int4(*desc)) {
+    int32_t splits;
+    return decode_workspace(*desc, &splits, bytes);
+  }
+  return MEMOPT_OK;
+}
+
+int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
+  MEMOPT_REQUIRE(desc, MEMOPT_ERR_INVALID, "paged_attention: null descriptor");
+  const memopt_attn_desc &d = *desc;
+  int rc = validate(d);
+  if (rc != MEMOPT_OK) return rc;
+  if (d.batch == 0 || d.q_len == 0 || d.num_heads == 0 || d.head_dim == 0) return MEMOPT_OK;
+  MEMOPT_REQUIRE(d.query && d.out && d.key_cache && d.value_cache && d.block_tables && d.context_lens,
+                 MEMOPT_ERR_INVALID, "paged_attention: null pointer");
+  const int32_t W = effective_window(d.window_size, d.max_seq_len);
+  const float scale = 1.0f / sqrtf((float)d.head_dim);
+  hipStream_t s = (hipStream_t)stream;
+
+  if (use_decode_int4(d)) {
+    int32_t splits;
+    int64_t need;
+    decode_workspace(d, &splits, &need);
+    MEMOPT_REQUIRE(need == 0 || (d.workspace && d.workspace_bytes >= need), MEMOPT_ERR_INVALID,
+                   "paged_attention: workspace too small (need " + std::to_string(need) + " bytes)");
+    DecodeParams p;
+    p.q = (const half_t *)d.query;
+    p.out = (half_t *)d.out;
+    p.kc = (const uint8_t *)d.key_cache;
+    p.vc = (const uint8_t *)d.value_cache;
+    p.ks = d.key_scales;
+    p.vs = d.value_scales;
+    p.kv_ps = d.kv_page_stride;
+    p.kv_hs = d.kv_head_stride;
+    p.kv_ts = d.kv_token_stride;
+    p.sc_ps = d.sc_page_stride;
+    p.sc_hs = d.sc_head_stride;
+    p.sc_ts = d.sc_token_stride;
+    p.bt = d.block_tables;
+    p.ctx = d.context_lens;
+    p.M = d.max_blocks_per_seq;
+    p.H = d.num_heads;
+    p.W = W;
+    p.sinks = d.num_sink_tokens < 0 ? 0 : d.num_sink_tokens;
+    p.splits = splits;
+    p.qk_scale_log2 = scale * 1.4426950408889634f;
+    p.ws_o = (float *)d.workspace;
+    p.ws_ml = splits > 1 ? (float *)d.workspace + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
+    return launch_decode_int4(p, d.batch, d.head_dim, d.scale_dtype, s);
+  }
+
+  GenericParams g;
+  g.q = (const half_t *)d.query;
+  g.out = (half_t *)d.out;
+  g.B = d.batch;
+  g.Lq = d.q_len;
+  g.H = d.num_heads;
+  g.D = d.head_dim;
+  g.int4 = d.kv_is_int4;
+  g.scale_f16 = d.scale_dtype == MEMOPT_SCALE_F16;
+  g.kc = d.key_cache;
+  g.vc = d.value_cache;
+  g.ks = d.key_scales;
+  g.vs = d.value_scales;
+  g.kv_ps = d.kv_page_stride;
+  g.kv_hs = d.kv_head_stride;
+  g.kv_ts = d.kv_token_stride;
+  g.sc_ps = d.sc_page_stride;
+  g.sc_hs = d.sc_head_stride;
+  g.sc_ts = d.sc_token_stride;
+  g.bs = d.block_size;
+  g.nb = d.num_kv_blocks;
+  g.bt = d.block_tables;
+  g.M = d.max_blocks_per_seq;
+  g.ctx = d.context_lens;
+  g.W = W;
+  g.sinks = d.num_sink_tokens < 0 ? 0 : d.num_sink_tokens;
+  g.causal = d.causal;
+  g.scale = scale;
+  MEMOPT_REQUIRE(d.q_len <= 65535 && d.batch <= 65535, MEMOPT_ERR_UNSUPPORTED,
+                 "paged_attention: q_len/batch > 65535 not supported by the generic kernel");
+  hipLaunchKernelGGL(generic_attention_kernel, dim3(d.num_heads, d.q_len, d.batch), dim3(64), 0, s, g);
+  return check_launch("paged_attention(generic)");
+}
+
+int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_len, int32_t num_heads,
+                                    int32_t head_dim, const void *key_cache, const void *value_cache,
+                                    int64_t num_kv_blocks, int32_t block_size, const int32_t *block_tables,
+                                    int32_t max_blocks_per_seq, const int32_t *context_lens,
+                                    int32_t max_seq_len, int32_t window_size, void *out, void *stream) {
+  memopt_attn_desc d = {};
+  d.query = query;
+  d.out = out;
+  d.batch = batch;
+  d.q_len = q_len;
+  d.num_heads = num_heads;
+  d.head_dim = head_dim;
+  d.kv_is_int4 = 0;
+  d.key_cache = key_cache;
+  d.value_cache = value_cache;
+  d.block_size = block_size;
+  d.num_kv_blocks = num_kv_blocks;
+  d.kv_head_stride = head_dim;
+  d.kv_token_stride = (int64_t)num_heads * head_dim;
+  d.kv_page_stride = (int64_t)block_size * num_heads * head_dim;
+  d.block_tables = block_tables;
+  d.max_blocks_per_seq = max_blocks_per_seq;
+  d.context_lens = context_lens;
+  d.max_seq_len = max_seq_len;
+  d.window_size = window_size;
+  return memopt_paged_attention(&d, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,108 @@
+// common.hpp — shared host/device helpers for the gfx950 INT4 KV-cache
+// data plane: status/error plumbing for the C ABI, the registered pool,
+// fp16 bit helpers and wave64 cross-lane primitives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+#include <mutex>
+
+#include "../../include/memopt_hip.h"
+
+namespace memopt {
+
+// ---------------------------------------------------------------------------
+// Error plumbing (host)
+// ---------------------------------------------------------------------------
+void set_error(const std::string &msg);
+void clear_error();
+
+#define MEMOPT_REQUIRE(cond, code, msg)                                        \
+  do {                                                                         \
+    if (!(cond)) {                                                             \
+      ::memopt::set_error(msg);                                                \
+      return (code);                                                           \
+    }                                                                          \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+int check_launch(const char *what);
+
+// ---------------------------------------------------------------------------
+// Registered pool (host state; storage is owned by the caller)
+// ---------------------------------------------------------------------------
+struct PoolView {
+  bool initialized = false;
+  int64_t num_blocks = 0;
+  int32_t block_size = 0, num_heads = 0, head_dim = 0, kv_format = MEMOPT_KV_FP16;
+  void *key = nullptr, *value = nullptr;              // fp16 rows or INT4 codes
+  void *key_scales = nullptr, *value_scales = nullptr;  // INT4 fp16 scales
+};
+// Snapshot of the live pool (taken under the pool lock).
+PoolView pool_snapshot();
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// DPP lane exchange inside quads / rows of 16 (no LDS traffic).
+// quad_perm xor-1 = [1,0,3,2] (0xB1), xor-2 = [2,3,0,1] (0x4E).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xor1(float v) { return dpp_f32<0xB1>(v); }
+__device__ __forceinline__ float xor2(float v) { return dpp_f32<0x4E>(v); }
+// row_half_mirror (0x141): lane i <-> 7-i inside each group of 8.
+__device__ __forceinline__ float half_mirror(float v) { return dpp_f32<0x141>(v); }
+// Generic wave64 butterfly through the LDS crossbar (ds_bpermute / swizzle).
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Group-64 symmetric INT4 code of v with scale s (IEEE divide, roundf half
+// away from zero, +8 offset, clamp [0,15]) — TheRadDani/memopt-transformer-runtime
+// src/csrc/quantization.cu:183-186. NaN quotients give code 8, like the
+// float->int conversion of the reference (v_cvt_i32_f32(NaN) = 0).
+__device__ __forceinline__ uint32_t int4_code(float v, float s) {
+  const float r = roundf(v / s);
+  int iq = (int)r + 8;
+  iq = iq < 0 ? 0 : (iq > 15 ? 15 : iq);
+  return (uint32_t)iq;
+}
+
+// Quantizes 8 consecutive elements (one 16-byte lane chunk of a 64-element
+// group spread over 8 lanes) into one packed word (element i in bits 4i..4i+3,
+// i.e. byte j = code[2j] | code[2j+1] << 4). Returns the packed word and sets
+// `scale` to the group's fp32 scale. Lanes 8k..8k+7 must hold one group.
+__device__ __forceinline__ uint32_t quantize8(const float v[8], float &scale) {
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
+  a = fmaxf(a, xor1(a));
+  a = fmaxf(a, xor2(a));
+  a = fmaxf(a, half_mirror(a));
+  scale = (a > 0.0f) ? (a / 7.0f) : 1.0f;
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w |= int4_code(v[i], scale) << (4 * i);
+  return w;
+}
+
+__device__ __forceinline__ void unpack_half8(uint4 u, float f[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    half2_t h = as_half2(w[i]);
+    f[2 * i] = (float)h.x;
+    f[2 * i + 1] = (float)h.y;
+  }
+}
+
+}  // namespace memopt

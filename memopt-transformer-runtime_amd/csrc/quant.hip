@@ -1,0 +1,262 @@
+// quant.hip — group-64 INT4 quantize / dequantize and the paged write path.
+//
+// Reference semantics: TheRadDani/memopt-transformer-runtime
+//   src/csrc/quantization.cu:104-203 (quantize), :232-270 (dequantize),
+//   src/csrc/kv_cache.cu:228-260   (write_cache scatter).
+//
+// gfx950 mapping: a 64-element group is 128 contiguous bytes of fp16, read as
+// one 16-byte load by each of 8 consecutive lanes; the group absmax is a
+// 3-step DPP max inside those 8 lanes (no LDS, no barrier); each lane packs its
+// 8 codes into one 32-bit word, so a wave reads 1 KiB and writes 256 B of codes
+// per step, fully coalesced. The same device routine quantizes token rows
+// straight into INT4 pages in write_cache (fused write + quantize).
+#include "common.hpp"
+
+namespace memopt {
+
+static constexpr int kThreads = 256;
+
+static inline unsigned grid_for(int64_t work_items, int64_t cap = 16384) {
+  int64_t g = (work_items + kThreads - 1) / kThreads;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load8(const half_t *p, float f[8]) {
+  if (VEC) {
+    unpack_half8(*reinterpret_cast<const uint4 *>(p), f);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)p[i];
+  }
+}
+
+// One lane = 8 consecutive elements; chunk i covers elements [8i, 8i+8).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void quantize_kernel(const half_t *__restrict__ in,
+                                                            uint8_t *__restrict__ packed,
+                                                            float *__restrict__ scales,
+                                                            int64_t n_chunks) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
+    float v[8];
+    load8<VEC>(in + i * 8, v);
+    float s;
+    const uint32_t w = quantize8(v, s);
+    if (VEC) {
+      reinterpret_cast<uint32_t *>(packed)[i] = w;
+    } else {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) packed[i * 4 + b] = (uint8_t)(w >> (8 * b));
+    }
+    if ((i & 7) == 0) scales[i >> 3] = s;
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t *__restrict__ packed,
+                                                              const float *__restrict__ scales,
+                                                              half_t *__restrict__ out,
+                                                              int64_t n_chunks) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
+    uint32_t w;
+    if (VEC) {
+      w = reinterpret_cast<const uint32_t *>(packed)[i];
+    } else {
+      w = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w |= (uint32_t)packed[i * 4 + b] << (8 * b);
+    }
+    const float s = scales[i >> 3];
+    half_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (half_t)((float)((int)((w >> (4 * e)) & 0xF) - 8) * s);
+    if (VEC) {
+      uint4 o;
+      o.x = as_u32(half2_t{h[0], h[1]});
+      o.y = as_u32(half2_t{h[2], h[3]});
+      o.z = as_u32(half2_t{h[4], h[5]});
+      o.w = as_u32(half2_t{h[6], h[7]});
+      *reinterpret_cast<uint4 *>(out + i * 8) = o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[i * 8 + e] = h[e];
+    }
+  }
+}
+
+// fp16 pool scatter: chunk i = 8 halves of token (i / cpr); cpr = H*D/8.
+__global__ __launch_bounds__(kThreads) void write_fp16_kernel(
+    const uint4 *__restrict__ keys, const uint4 *__restrict__ values, uint4 *__restrict__ kpool,
+    uint4 *__restrict__ vpool, const int32_t *__restrict__ slots, int64_t n_chunks, int64_t cpr,
+    int64_t n_slots) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
+    const int64_t t = i / cpr, c = i - t * cpr;
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= n_slots) continue;
+    kpool[slot * cpr + c] = keys[i];
+    vpool[slot * cpr + c] = values[i];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void write_fp16_scalar_kernel(
+    const half_t *__restrict__ keys, const half_t *__restrict__ values, half_t *__restrict__ kpool,
+    half_t *__restrict__ vpool, const int32_t *__restrict__ slots, int64_t n, int64_t row,
+    int64_t n_slots) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    const int64_t t = i / row, c = i - t * row;
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= n_slots) continue;
+    kpool[slot * row + c] = keys[i];
+    vpool[slot * row + c] = values[i];
+  }
+}
+
+// Fused write + quantize into INT4 pages. Chunk i = 8 elements of the
+// (token, head) row; page layout codes [nb, H, bs, D/2], scales [nb, H, bs, D/64].
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void write_int4_kernel(
+    const half_t *__restrict__ keys, const half_t *__restrict__ values, uint8_t *__restrict__ kc,
+    uint8_t *__restrict__ vc, half_t *__restrict__ ks, half_t *__restrict__ vs,
+    const int32_t *__restrict__ slots, int64_t n_chunks, int32_t H, int32_t D, int32_t bs,
+    int64_t n_slots) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const int32_t cpr = D / 8;  // chunks per (token, head) row
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
+    const int64_t th = i / cpr;
+    const int32_t c = (int32_t)(i - th * cpr);
+    const int64_t t = th / H;
+    const int32_t h = (int32_t)(th - t * H);
+    const int64_t slot = slots[t];
+    float kv[8], vv[8];
+    load8<VEC>(keys + i * 8, kv);
+    load8<VEC>(values + i * 8, vv);
+    float s_k, s_v;
+    // All 8 lanes of a group run quantize8 together (same token => same branch).
+    const uint32_t wk = quantize8(kv, s_k);
+    const uint32_t wv = quantize8(vv, s_v);
+    if (slot < 0 || slot >= n_slots) continue;
+    const int64_t page = slot / bs, pos = slot - page * bs;
+    const int64_t rowid = (page * H + h) * bs + pos;  // (page, head, token) row
+    const int64_t cb = rowid * (D / 2) + (int64_t)c * 4;
+    if (VEC) {
+      *reinterpret_cast<uint32_t *>(kc + cb) = wk;
+      *reinterpret_cast<uint32_t *>(vc + cb) = wv;
+    } else {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        kc[cb + b] = (uint8_t)(wk >> (8 * b));
+        vc[cb + b] = (uint8_t)(wv >> (8 * b));
+      }
+    }
+    if ((c & 7) == 0) {
+      const int64_t si = rowid * (D / 64) + (c >> 3);
+      ks[si] = (half_t)s_k;
+      vs[si] = (half_t)s_v;
+    }
+  }
+}
+
+}  // namespace memopt
+
+using namespace memopt;
+
+static inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+extern "C" {
+
+int memopt_quantize_kv_cache_int4(const void *cache, int64_t numel, int64_t last_dim,
+                                  int32_t group_size, uint8_t *packed_out, float *scales_out,
+                                  void *stream) {
+  MEMOPT_REQUIRE(group_size == 64, MEMOPT_ERR_INVALID,
+                 "quantize_kv_cache_int4: group_size must equal 64 (got " + std::to_string(group_size) + ")");
+  MEMOPT_REQUIRE(numel % 64 == 0, MEMOPT_ERR_INVALID,
+                 "quantize_kv_cache_int4: total_elements (" + std::to_string(numel) +
+                     ") must be divisible by group_size (64)");
+  MEMOPT_REQUIRE(last_dim % 2 == 0, MEMOPT_ERR_INVALID,
+                 "quantize_kv_cache_int4: last dimension (" + std::to_string(last_dim) +
+                     ") must be even for INT4 packing");
+  if (numel == 0) return MEMOPT_OK;
+  MEMOPT_REQUIRE(cache && packed_out && scales_out, MEMOPT_ERR_INVALID, "quantize_kv_cache_int4: null pointer");
+  const int64_t n_chunks = numel / 8;
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = aligned(cache, 16) && aligned(packed_out, 4);
+  if (vec)
+    hipLaunchKernelGGL(quantize_kernel<true>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s,
+                       (const half_t *)cache, packed_out, scales_out, n_chunks);
+  else
+    hipLaunchKernelGGL(quantize_kernel<false>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s,
+                       (const half_t *)cache, packed_out, scales_out, n_chunks);
+  return check_launch("quantize_kv_cache_int4");
+}
+
+int memopt_dequantize_kv_cache_int4(const uint8_t *packed, int64_t packed_numel, const float *scales,
+                                    int64_t num_scales, int32_t group_size, void *out, void *stream) {
+  MEMOPT_REQUIRE(group_size == 64, MEMOPT_ERR_INVALID,
+                 "dequantize_kv_cache_int4: group_size must equal 64");
+  const int64_t total = packed_numel * 2;
+  MEMOPT_REQUIRE(total % 64 == 0 && num_scales == total / 64, MEMOPT_ERR_INVALID,
+                 "dequantize_kv_cache_int4: scales length (" + std::to_string(num_scales) +
+                     ") != expected num_groups (" + std::to_string(total / 64) + ")");
+  if (total == 0) return MEMOPT_OK;
+  MEMOPT_REQUIRE(packed && scales && out, MEMOPT_ERR_INVALID, "dequantize_kv_cache_int4: null pointer");
+  const int64_t n_chunks = total / 8;
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = aligned(packed, 4) && aligned(out, 16);
+  if (vec)
+    hipLaunchKernelGGL(dequantize_kernel<true>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s, packed,
+                       scales, (half_t *)out, n_chunks);
+  else
+    hipLaunchKernelGGL(dequantize_kernel<false>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s, packed,
+                       scales, (half_t *)out, n_chunks);
+  return check_launch("dequantize_kv_cache_int4");
+}
+
+int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens, int32_t num_heads,
+                       int32_t head_dim, const int32_t *slot_mapping, void *stream) {
+  const PoolView p = pool_snapshot();
+  MEMOPT_REQUIRE(p.initialized, MEMOPT_ERR_STATE, "write_cache: pool not initialized; call init_pool first");
+  MEMOPT_REQUIRE(num_heads == p.num_heads, MEMOPT_ERR_INVALID, "write_cache: num_heads != pool.num_heads");
+  MEMOPT_REQUIRE(head_dim == p.head_dim, MEMOPT_ERR_INVALID, "write_cache: head_dim != pool.head_dim");
+  if (num_tokens == 0) return MEMOPT_OK;
+  MEMOPT_REQUIRE(keys && values && slot_mapping, MEMOPT_ERR_INVALID, "write_cache: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t n_slots = p.num_blocks * p.block_size;
+  const int64_t row = (int64_t)num_heads * head_dim;
+  if (p.kv_format == MEMOPT_KV_FP16) {
+    const bool vec = row % 8 == 0 && aligned(keys, 16) && aligned(values, 16) && aligned(p.key, 16) &&
+                     aligned(p.value, 16);
+    if (vec) {
+      const int64_t cpr = row / 8, n = num_tokens * cpr;
+      hipLaunchKernelGGL(write_fp16_kernel, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint4 *)keys,
+                         (const uint4 *)values, (uint4 *)p.key, (uint4 *)p.value, slot_mapping, n, cpr,
+                         n_slots);
+    } else {
+      const int64_t n = num_tokens * row;
+      hipLaunchKernelGGL(write_fp16_scalar_kernel, dim3(grid_for(n)), dim3(kThreads), 0, s,
+                         (const half_t *)keys, (const half_t *)values, (half_t *)p.key, (half_t *)p.value,
+                         slot_mapping, n, row, n_slots);
+    }
+  } else {
+    const int64_t n = num_tokens * row / 8;
+    const bool vec = aligned(keys, 16) && aligned(values, 16);
+    if (vec)
+      hipLaunchKernelGGL(write_int4_kernel<true>, dim3(grid_for(n)), dim3(kThreads), 0, s,
+                         (const half_t *)keys, (const half_t *)values, (uint8_t *)p.key, (uint8_t *)p.value,
+                         (half_t *)p.key_scales, (half_t *)p.value_scales, slot_mapping, n, num_heads, head_dim,
+                         p.block_size, n_slots);
+    else
+      hipLaunchKernelGGL(write_int4_kernel<false>, dim3(grid_for(n)), dim3(kThreads), 0, s,
+                         (const half_t *)keys, (const half_t *)values, (uint8_t *)p.key, (uint8_t *)p.value,
+                         (half_t *)p.key_scales, (half_t *)p.value_scales, slot_mapping, n, num_heads, head_dim,
+                         p.block_size, n_slots);
+  }
+  return check_launch("write_cache");
+}
+
+}  // extern "C"

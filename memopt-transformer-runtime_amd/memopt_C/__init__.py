@@ -1,0 +1,532 @@
+"""memopt_C — drop-in for the reference's pybind11 extension, backed by gfx950 HIP.
+
+Same module name, function names, argument order/keywords, return types and
+error type (``RuntimeError``) as TheRadDani/memopt-transformer-runtime
+``src/csrc/extension.cpp:10-124``, so ``memopt.DynamicAttention`` and the
+reference tests run unchanged against it. Calls go through the C ABI of
+``libmemopt_hip.so`` (declared in ``include/memopt_hip.h``); torch is used only
+to allocate device tensors and to pass the current HIP stream.
+
+Additions (new names or keyword-only arguments whose defaults keep the
+reference behaviour):
+  * ``get_key_pool()`` / ``get_value_pool()`` — called by the reference's
+    ``DynamicAttention`` (src/memopt/attention.py:330-331) but missing from
+    its extension;
+  * ``init_pool(..., kv_format="int4")`` — INT4 page pool (codes
+    [nb, H, bs, D/2] u8 + fp16 scales [nb, H, bs, D/64]); ``write_cache`` then
+    quantizes on the fly and ``get_pool_scales()`` returns the scales;
+  * ``dynamic_sparse_attention(..., *, num_sink_tokens=0, causal=False,
+    key_scales=None, value_scales=None, kv_layout=None)`` — INT4 caches are
+    dequantized just in time inside the kernel;
+  * ``free_evicted_blocks(is_block_free)`` — the post-eviction sweep the
+    reference documents but never implements (src/csrc/kv_cache.cu:1033-1036).
+
+The library is loaded at import; a missing or unloadable library raises
+``ImportError`` naming the path (there is no CPU fallback).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import List, Optional, Tuple
+
+import torch  # must precede the HIP library so both share one HIP runtime
+
+__all__ = [
+    "get_hello", "init_pool", "allocate_block", "free_block", "get_pool_tensors",
+    "get_key_pool", "get_value_pool", "get_pool_scales", "free_blocks_count",
+    "write_cache", "evict_cache", "evict_tokens", "free_evicted_blocks",
+    "dynamic_sparse_attention", "PreparedAttention", "quantize_kv_cache_int4", "dequantize_kv_cache_int4",
+    "library_path",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+library_path = os.environ.get("MEMOPT_HIP_LIB", os.path.join(_HERE, "libmemopt_hip.so"))
+
+if not os.path.exists(library_path):
+    raise ImportError(
+        f"memopt_C: {library_path} is missing; build it with "
+        "`python memopt-transformer-runtime_amd/build.py` (there is no CPU fallback)")
+try:
+    _lib = ctypes.CDLL(library_path)
+except OSError as exc:  # pragma: no cover - environment specific
+    raise ImportError(f"memopt_C: cannot load {library_path}: {exc}") from exc
+
+_i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+
+class AttnDesc(ctypes.Structure):
+    """Mirror of ``memopt_attn_desc`` (include/memopt_hip.h)."""
+
+    _fields_ = [
+        ("query", _vp), ("out", _vp),
+        ("batch", _i32), ("q_len", _i32), ("num_heads", _i32), ("head_dim", _i32),
+        ("kv_is_int4", _i32),
+        ("key_cache", _vp), ("value_cache", _vp), ("key_scales", _vp), ("value_scales", _vp),
+        ("scale_dtype", _i32), ("block_size", _i32), ("num_kv_blocks", _i64),
+        ("kv_page_stride", _i64), ("kv_head_stride", _i64), ("kv_token_stride", _i64),
+        ("sc_page_stride", _i64), ("sc_head_stride", _i64), ("sc_token_stride", _i64),
+        ("block_tables", _vp), ("max_blocks_per_seq", _i32), ("context_lens", _vp),
+        ("max_seq_len", _i32), ("window_size", _i32), ("num_sink_tokens", _i32), ("causal", _i32),
+        ("workspace", _vp), ("workspace_bytes", _i64),
+    ]
+
+
+def _sig(name, args, res=_i32):
+    f = getattr(_lib, name)
+    f.argtypes = args
+    f.restype = res
+    return f
+
+
+_lib.memopt_last_error.restype = ctypes.c_char_p
+_lib.memopt_get_hello.restype = ctypes.c_char_p
+_c_init_pool = _sig("memopt_init_pool", [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp])
+_c_pool_info = _sig("memopt_pool_info", [ctypes.POINTER(_i64)] + [ctypes.POINTER(_i32)] * 4)
+_c_reset_pool = _sig("memopt_reset_pool", [])
+_c_alloc = _sig("memopt_allocate_block", [ctypes.POINTER(_i64)])
+_c_free = _sig("memopt_free_block", [_i64])
+_c_free_count = _sig("memopt_free_blocks_count", [ctypes.POINTER(_i64)])
+_c_write = _sig("memopt_write_cache", [_vp, _vp, _i64, _i32, _i32, _vp, _vp])
+_c_evict_cache = _sig("memopt_evict_cache", [_vp, _i64, _f32, _i32, _vp])
+_c_evict_tokens = _sig("memopt_evict_tokens", [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _i64, _f32, _i32, _vp])
+_c_quant = _sig("memopt_quantize_kv_cache_int4", [_vp, _i64, _i64, _i32, _vp, _vp, _vp])
+_c_dequant = _sig("memopt_dequantize_kv_cache_int4", [_vp, _i64, _vp, _i64, _i32, _vp, _vp])
+_c_dsa = _sig("memopt_dynamic_sparse_attention",
+              [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _i32, _vp, _i32, _vp, _i32, _i32, _vp, _vp])
+_c_ws = _sig("memopt_attention_workspace_size", [ctypes.POINTER(AttnDesc), ctypes.POINTER(_i64)])
+_c_attn = _sig("memopt_paged_attention", [ctypes.POINTER(AttnDesc), _vp])
+
+KV_FP16, KV_INT4 = 0, 1
+_FORMATS = {"fp16": KV_FP16, "int4": KV_INT4}
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(_lib.memopt_last_error().decode())
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _cuda(t: torch.Tensor, name: str, fn: str) -> None:
+    _require(isinstance(t, torch.Tensor) and t.is_cuda, f"{fn}: {name} must be a CUDA tensor")
+
+
+# ---------------------------------------------------------------------------
+# Handshake
+# ---------------------------------------------------------------------------
+
+def get_hello() -> str:
+    """src/csrc/extension.cpp:6-8 (string carries "MemOpt C++ Backend Initialized")."""
+    return _lib.memopt_get_hello().decode()
+
+
+# ---------------------------------------------------------------------------
+# Pool — src/csrc/kv_cache.cu:83-201
+# ---------------------------------------------------------------------------
+
+_pool_lock = threading.Lock()
+_pool: dict = {}
+
+
+def init_pool(num_blocks: int, block_size: int, num_heads: int, head_dim: int,
+              kv_format: str = "fp16") -> None:
+    """Allocate zeroed pool storage on the current device and seed the FIFO free list.
+
+    Idempotent for identical parameters (src/csrc/kv_cache.cu:115-122);
+    different parameters reset the pool. Invalid parameters raise
+    ``RuntimeError`` and leave no pool behind.
+    """
+    fmt = _FORMATS.get(kv_format)
+    _require(fmt is not None, f"init_pool: kv_format must be one of {sorted(_FORMATS)}")
+    with _pool_lock:
+        nb, bs, h, d, f = _i64(), _i32(), _i32(), _i32(), _i32()
+        if _c_pool_info(ctypes.byref(nb), ctypes.byref(bs), ctypes.byref(h), ctypes.byref(d), ctypes.byref(f)):
+            if (nb.value, bs.value, h.value, d.value, f.value) == (num_blocks, block_size, num_heads, head_dim, fmt):
+                return
+        _pool.clear()
+        _c_reset_pool()
+        ok = num_blocks > 0 and block_size > 0 and num_heads > 0 and head_dim > 0 and head_dim % 2 == 0
+        if not ok or (fmt == KV_INT4 and head_dim % 64):
+            # Let the library produce the reference's message (and stay torn down).
+            _check(_c_init_pool(num_blocks, block_size, num_heads, head_dim, fmt, 1, 1, 1, 1))
+        dev = torch.device("cuda", torch.cuda.current_device())
+        if fmt == KV_FP16:
+            shape = (num_blocks, block_size, num_heads, head_dim)
+            k = torch.zeros(shape, dtype=torch.float16, device=dev)
+            v = torch.zeros(shape, dtype=torch.float16, device=dev)
+            ks = vs = None
+        else:
+            k = torch.full((num_blocks, num_heads, block_size, head_dim // 2), 0x88, dtype=torch.uint8, device=dev)
+            v = torch.full_like(k, 0x88)
+            ks = torch.ones((num_blocks, num_heads, block_size, head_dim // 64), dtype=torch.float16, device=dev)
+            vs = torch.ones_like(ks)
+        _check(_c_init_pool(num_blocks, block_size, num_heads, head_dim, fmt, k.data_ptr(), v.data_ptr(),
+                            ks.data_ptr() if ks is not None else None, vs.data_ptr() if vs is not None else None))
+        _pool.update(k=k, v=v, ks=ks, vs=vs, fmt=fmt, nb=num_blocks, bs=block_size, h=num_heads, d=head_dim)
+
+
+def _pool_or_raise(fn: str) -> dict:
+    _require(bool(_pool), f"{fn}: pool not initialized")
+    return _pool
+
+
+def allocate_block() -> int:
+    """Pop one free block (FIFO); -1 when exhausted (src/csrc/kv_cache.cu:163-172)."""
+    out = _i64()
+    _check(_c_alloc(ctypes.byref(out)))
+    return int(out.value)
+
+
+def free_block(block_idx: int) -> None:
+    """Return a block to the free list (src/csrc/kv_cache.cu:179-185)."""
+    _check(_c_free(int(block_idx)))
+
+
+def free_blocks_count() -> int:
+    out = _i64()
+    _check(_c_free_count(ctypes.byref(out)))
+    return int(out.value)
+
+
+def get_pool_tensors() -> Tuple[torch.Tensor, torch.Tensor]:
+    """(key_pool, value_pool) aliases of the live storage (src/csrc/kv_cache.cu:190-193).
+
+    fp16 pools: [nb, bs, H, D] fp16. INT4 pools: codes [nb, H, bs, D/2] uint8.
+    """
+    p = _pool_or_raise("get_pool_tensors")
+    return p["k"], p["v"]
+
+
+def get_key_pool() -> torch.Tensor:
+    return _pool_or_raise("get_key_pool")["k"]
+
+
+def get_value_pool() -> torch.Tensor:
+    return _pool_or_raise("get_value_pool")["v"]
+
+
+def get_pool_scales() -> Tuple[torch.Tensor, torch.Tensor]:
+    """fp16 group scales [nb, H, bs, D/64] of an INT4 pool."""
+    p = _pool_or_raise("get_pool_scales")
+    _require(p["fmt"] == KV_INT4, "get_pool_scales: pool is not an INT4 pool")
+    return p["ks"], p["vs"]
+
+
+# ---------------------------------------------------------------------------
+# write_cache — src/csrc/kv_cache.cu:282-348
+# ---------------------------------------------------------------------------
+
+def write_cache(keys: torch.Tensor, values: torch.Tensor, block_tables: torch.Tensor,
+                slot_mapping: torch.Tensor, *, validate_slots: bool = True) -> None:
+    """Scatter [T, H, D] fp16 rows into pool slots (INT4 pools: quantize on the fly).
+
+    ``block_tables`` is accepted and unused, as in the reference (:279-280).
+    Slots outside the pool raise ``RuntimeError("... out of bounds")``; that
+    check costs one device-to-host sync, so hot loops whose slots are known
+    good may pass ``validate_slots=False`` (the kernel still skips, never
+    writes, out-of-range slots).
+    """
+    p = _pool_or_raise("write_cache")
+    _require(keys.dim() == 3, "write_cache: keys must be 3-D [num_tokens, num_heads, head_dim]")
+    _require(values.dim() == 3, "write_cache: values must be 3-D [num_tokens, num_heads, head_dim]")
+    _require(slot_mapping.dim() == 1, "write_cache: slot_mapping must be 1-D [num_tokens]")
+    T, H, D = keys.shape
+    _require(tuple(values.shape) == (T, H, D), "write_cache: keys/values shape mismatch")
+    _require(slot_mapping.shape[0] == T, "write_cache: slot_mapping length != num_tokens")
+    _require(H == p["h"], "write_cache: num_heads != pool.num_heads")
+    _require(D == p["d"], "write_cache: head_dim != pool.head_dim")
+    _require(keys.dtype == torch.float16 and values.dtype == torch.float16, "write_cache: keys/values must be fp16")
+    _cuda(keys, "keys", "write_cache")
+    _cuda(values, "values", "write_cache")
+    _cuda(slot_mapping, "slot_mapping", "write_cache")
+    _require(slot_mapping.dtype == torch.int32, "write_cache: slot_mapping must be int32")
+    if T == 0:
+        return
+    keys, values, slot_mapping = keys.contiguous(), values.contiguous(), slot_mapping.contiguous()
+    if validate_slots:
+        lo, hi = (int(x) for x in torch.aminmax(slot_mapping))
+        _require(lo >= 0 and hi < p["nb"] * p["bs"], "write_cache: slot_mapping out of bounds")
+    with torch.cuda.device(keys.device):
+        _check(_c_write(keys.data_ptr(), values.data_ptr(), T, H, D, slot_mapping.data_ptr(), _stream(keys)))
+
+
+# ---------------------------------------------------------------------------
+# Eviction — src/csrc/kv_cache.cu:503-559, :1053-1156
+# ---------------------------------------------------------------------------
+
+def evict_cache(block_tables: torch.Tensor, attention_scores: torch.Tensor, retain_ratio: float,
+                num_sink_tokens: int = 4) -> None:
+    """Pool-centric eviction over scores [num_blocks, block_size, H] (f32)."""
+    p = _pool_or_raise("evict_cache")
+    _require(0.0 < retain_ratio <= 1.0, "evict_cache: retain_ratio must be in (0, 1]")
+    _require(attention_scores.dim() == 3,
+             "evict_cache: attention_scores must be 3-D [num_blocks, block_size, num_heads]")
+    _require(attention_scores.dtype == torch.float32, "evict_cache: attention_scores must be float32")
+    nb, bs, h = attention_scores.shape
+    _require(nb <= p["nb"], "evict_cache: attention_scores num_blocks > pool.num_blocks")
+    _require(bs == p["bs"], "evict_cache: attention_scores block_size != pool.block_size")
+    _require(h == p["h"], "evict_cache: attention_scores num_heads != pool.num_heads")
+    _cuda(attention_scores, "attention_scores", "evict_cache")
+    scores = attention_scores.contiguous()
+    with torch.cuda.device(scores.device):
+        _check(_c_evict_cache(scores.data_ptr(), nb, float(retain_ratio), int(num_sink_tokens), _stream(scores)))
+
+
+def evict_tokens(attention_scores: torch.Tensor, block_tables: torch.Tensor, is_block_free: torch.Tensor,
+                 retain_ratio: float, num_sink_tokens: int = 4) -> None:
+    """Sequence-centric Ada-KV eviction; mutates the pool, ``block_tables`` and ``is_block_free``.
+
+    ``block_tables`` and ``is_block_free`` must be contiguous int32 CUDA
+    tensors (the reference silently drops mutations of non-contiguous ones).
+    """
+    p = _pool_or_raise("evict_tokens")
+    _require(0.0 < retain_ratio <= 1.0, "evict_tokens: retain_ratio must be in (0, 1]")
+    _require(attention_scores.dim() == 3,
+             "evict_tokens: attention_scores must be 3-D [num_seqs, num_heads, seq_len]")
+    _require(attention_scores.dtype == torch.float32, "evict_tokens: attention_scores must be float32")
+    _require(block_tables.dim() == 2, "evict_tokens: block_tables must be 2-D [num_seqs, max_blocks_per_seq]")
+    _require(block_tables.dtype == torch.int32, "evict_tokens: block_tables must be int32")
+    _require(is_block_free.dim() == 1, "evict_tokens: is_block_free must be 1-D [total_pool_blocks]")
+    _require(is_block_free.dtype == torch.int32, "evict_tokens: is_block_free must be int32")
+    N, H, L = attention_scores.shape
+    _require(H == p["h"], "evict_tokens: attention_scores num_heads != pool.num_heads")
+    _require(block_tables.shape[0] == N, "evict_tokens: block_tables batch size != num_seqs")
+    _require(is_block_free.shape[0] <= p["nb"], "evict_tokens: is_block_free size > pool.num_blocks")
+    for t, n in ((attention_scores, "attention_scores"), (block_tables, "block_tables"),
+                 (is_block_free, "is_block_free")):
+        _cuda(t, n, "evict_tokens")
+        _require(t.device == attention_scores.device, f"evict_tokens: {n} on a different device")
+    _require(block_tables.is_contiguous() and is_block_free.is_contiguous(),
+             "evict_tokens: block_tables and is_block_free must be contiguous (they are mutated in place)")
+    if N == 0 or L == 0:
+        return
+    scores = attention_scores.contiguous()
+    with torch.cuda.device(scores.device):
+        _check(_c_evict_tokens(scores.data_ptr(), N, H, L, block_tables.data_ptr(), block_tables.shape[1],
+                               is_block_free.data_ptr(), is_block_free.shape[0], float(retain_ratio),
+                               int(num_sink_tokens), _stream(scores)))
+
+
+def free_evicted_blocks(is_block_free: torch.Tensor) -> List[int]:
+    """Return every block with ``is_block_free == num_heads`` to the free list and reset its counter.
+
+    The caller-side step documented at src/csrc/kv_cache.cu:1033-1036.
+    Returns the freed block indices.
+    """
+    p = _pool_or_raise("free_evicted_blocks")
+    idx = torch.nonzero(is_block_free == p["h"]).flatten()
+    freed = [int(i) for i in idx.tolist()]
+    for b in freed:
+        free_block(b)
+    if freed:
+        is_block_free[idx] = 0
+    return freed
+
+
+# ---------------------------------------------------------------------------
+# Quantization — src/csrc/quantization.cu:294-428
+# ---------------------------------------------------------------------------
+
+def quantize_kv_cache_int4(cache: torch.Tensor, group_size: int) -> List[torch.Tensor]:
+    """[packed uint8 (last dim / 2), scales float32 [numel / 64]]."""
+    _cuda(cache, "cache", "quantize_kv_cache_int4")
+    _require(cache.is_contiguous(), "quantize_kv_cache_int4: cache must be contiguous")
+    _require(cache.dtype == torch.float16, "quantize_kv_cache_int4: cache must be float16")
+    _require(group_size == 64, f"quantize_kv_cache_int4: group_size must equal 64 (got {group_size})")
+    _require(cache.dim() >= 1, "quantize_kv_cache_int4: cache must have at least one dimension")
+    n = cache.numel()
+    _require(n % group_size == 0,
+             f"quantize_kv_cache_int4: total_elements ({n}) must be divisible by group_size ({group_size})")
+    last = cache.shape[-1]
+    _require(last % 2 == 0, f"quantize_kv_cache_int4: last dimension ({last}) must be even for INT4 packing")
+    packed = torch.empty(cache.shape[:-1] + (last // 2,), dtype=torch.uint8, device=cache.device)
+    scales = torch.empty((n // group_size,), dtype=torch.float32, device=cache.device)
+    if n:
+        with torch.cuda.device(cache.device):
+            _check(_c_quant(cache.data_ptr(), n, last, group_size, packed.data_ptr(), scales.data_ptr(),
+                            _stream(cache)))
+    return [packed, scales]
+
+
+def dequantize_kv_cache_int4(q_cache: torch.Tensor, scales: torch.Tensor, group_size: int) -> torch.Tensor:
+    """fp16 tensor with the last dim doubled."""
+    _cuda(q_cache, "q_cache", "dequantize_kv_cache_int4")
+    _cuda(scales, "scales", "dequantize_kv_cache_int4")
+    _require(q_cache.is_contiguous(), "dequantize_kv_cache_int4: q_cache must be contiguous")
+    _require(scales.is_contiguous(), "dequantize_kv_cache_int4: scales must be contiguous")
+    _require(q_cache.dtype == torch.uint8, "dequantize_kv_cache_int4: q_cache must be uint8")
+    _require(scales.dtype == torch.float32, "dequantize_kv_cache_int4: scales must be float32")
+    _require(group_size == 64, "dequantize_kv_cache_int4: group_size must equal 64")
+    total = q_cache.numel() * 2
+    _require(total % 64 == 0 and scales.numel() == total // 64,
+             f"dequantize_kv_cache_int4: scales length ({scales.numel()}) != expected num_groups ({total // 64})")
+    out = torch.empty(q_cache.shape[:-1] + (q_cache.shape[-1] * 2,), dtype=torch.float16, device=q_cache.device)
+    if total:
+        with torch.cuda.device(q_cache.device):
+            _check(_c_dequant(q_cache.data_ptr(), q_cache.numel(), scales.data_ptr(), scales.numel(), group_size,
+                              out.data_ptr(), _stream(q_cache)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Attention — src/csrc/attention.cu:371-521
+# ---------------------------------------------------------------------------
+
+def _int4_layout(key_cache, key_scales, kv_layout, num_heads, head_dim):
+    """Resolve (block_size, num_blocks, code strides, scale strides, scale dtype)."""
+    if kv_layout is None:
+        kv_layout = "pages" if key_scales.dtype == torch.float16 else "token_major"
+    G = head_dim // 64
+    if kv_layout == "pages":  # codes [nb, H, bs, D/2], scales [nb, H, bs, D/64]
+        nb, h, bs, dh = key_cache.shape
+        _require(h == num_heads and dh * 2 == head_dim, "dynamic_sparse_attention: INT4 page shape mismatch")
+        kv = (h * bs * dh, bs * dh, dh)
+        sc = (h * bs * G, bs * G, G)
+    elif kv_layout == "token_major":  # codes [nb, bs, H, D/2], scales [nb*bs*H*D/64]
+        nb, bs, h, dh = key_cache.shape
+        _require(h == num_heads and dh * 2 == head_dim, "dynamic_sparse_attention: INT4 cache shape mismatch")
+        kv = (bs * h * dh, dh, h * dh)
+        sc = (bs * h * G, G, h * G)
+    else:
+        raise RuntimeError(f"dynamic_sparse_attention: unknown kv_layout {kv_layout!r}")
+    _require(key_scales.numel() == nb * bs * num_heads * G, "dynamic_sparse_attention: scales size mismatch")
+    sdt = 1 if key_scales.dtype == torch.float16 else 0
+    _require(key_scales.dtype in (torch.float16, torch.float32), "dynamic_sparse_attention: scales must be f16/f32")
+    return bs, nb, kv, sc, sdt
+
+
+def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size,
+                    num_sink_tokens, causal, key_scales, value_scales, kv_layout, out):
+    """Validate like src/csrc/attention.cu:383-439 and fill an AttnDesc.
+
+    Returns (desc, out, workspace, keepalive) or (None, out, None, ()) for empty shapes.
+    """
+    fn = "dynamic_sparse_attention"
+    for t, n in ((query, "query"), (key_cache, "key_cache"), (value_cache, "value_cache"),
+                 (block_tables, "block_tables"), (context_lens, "context_lens")):
+        _require(isinstance(t, torch.Tensor) and t.is_cuda, f"{n} must be a CUDA tensor")
+        _require(t.is_contiguous(), f"{n} must be contiguous")
+    _require(query.dim() == 4, "query must be 4-D [batch, q_len, num_heads, head_dim]")
+    _require(key_cache.dim() == 4, "key_cache must be 4-D [num_kv_blocks, block_size, num_heads, head_dim]")
+    _require(value_cache.dim() == 4, "value_cache must be 4-D [num_kv_blocks, block_size, num_heads, head_dim]")
+    _require(block_tables.dim() == 2, "block_tables must be 2-D [batch, max_blocks_per_seq]")
+    _require(context_lens.dim() == 1, "context_lens must be 1-D [batch]")
+    _require(query.dtype == torch.float16, "query must be fp16")
+    _require(block_tables.dtype == torch.int32, "block_tables must be int32")
+    _require(context_lens.dtype == torch.int32, "context_lens must be int32")
+    B, Lq, H, D = query.shape
+    _require(block_tables.shape[0] == B, "block_tables batch dimension mismatch")
+    _require(context_lens.shape[0] == B, "context_lens batch dimension mismatch")
+    if out is None:
+        out = torch.empty_like(query)
+    _require(out.shape == query.shape and out.dtype == torch.float16 and out.is_contiguous() and out.is_cuda,
+             f"{fn}: out must be a contiguous fp16 CUDA tensor shaped like query")
+    int4 = key_cache.dtype == torch.uint8
+    if int4:
+        _require(value_cache.dtype == torch.uint8 and value_cache.shape == key_cache.shape,
+                 "value_cache must match key_cache (INT4 codes)")
+        if key_scales is None and _pool and _pool["fmt"] == KV_INT4 and \
+                key_cache.data_ptr() == _pool["k"].data_ptr() and value_cache.data_ptr() == _pool["v"].data_ptr():
+            key_scales, value_scales = _pool["ks"], _pool["vs"]
+        _require(key_scales is not None and value_scales is not None, f"{fn}: INT4 caches need key/value scales")
+        for t, n in ((key_scales, "key_scales"), (value_scales, "value_scales")):
+            _require(t.is_cuda and t.is_contiguous(), f"{n} must be a contiguous CUDA tensor")
+        _require(key_scales.dtype == value_scales.dtype and key_scales.shape == value_scales.shape,
+                 f"{fn}: key/value scales mismatch")
+        _require(D % 64 == 0, f"{fn}: INT4 caches need head_dim % 64 == 0")
+        bs, nb, kv, sc, sdt = _int4_layout(key_cache, key_scales, kv_layout, H, D)
+    else:
+        _require(key_cache.dtype == torch.float16, "key_cache must be fp16")
+        _require(value_cache.dtype == torch.float16, "value_cache must be fp16")
+        nb, bs = key_cache.shape[0], key_cache.shape[1]
+        _require(key_cache.shape[2] == H, f"key_cache num_heads {key_cache.shape[2]} != query num_heads {H}")
+        _require(key_cache.shape[3] == D, f"key_cache head_dim {key_cache.shape[3]} != query head_dim {D}")
+        _require(value_cache.shape[1] == bs, "value_cache block_size mismatch")
+        _require(value_cache.shape[2] == H, "value_cache num_heads mismatch")
+        _require(value_cache.shape[3] == D, "value_cache head_dim mismatch")
+        kv = (bs * H * D, D, H * D)
+        sc = (0, 0, 0)
+        sdt = 0
+    if B == 0 or Lq == 0 or H == 0 or D == 0:
+        return None, out, None, ()
+    d = AttnDesc()
+    d.query, d.out = query.data_ptr(), out.data_ptr()
+    d.batch, d.q_len, d.num_heads, d.head_dim = B, Lq, H, D
+    d.kv_is_int4 = int(int4)
+    d.key_cache, d.value_cache = key_cache.data_ptr(), value_cache.data_ptr()
+    if int4:
+        d.key_scales, d.value_scales = key_scales.data_ptr(), value_scales.data_ptr()
+    d.scale_dtype, d.block_size, d.num_kv_blocks = sdt, bs, nb
+    d.kv_page_stride, d.kv_head_stride, d.kv_token_stride = kv
+    d.sc_page_stride, d.sc_head_stride, d.sc_token_stride = sc
+    d.block_tables, d.max_blocks_per_seq = block_tables.data_ptr(), block_tables.shape[1]
+    d.context_lens = context_lens.data_ptr()
+    d.max_seq_len, d.window_size = int(max_seq_len), int(window_size)
+    d.num_sink_tokens, d.causal = int(num_sink_tokens), int(bool(causal))
+    need = _i64()
+    _check(_c_ws(ctypes.byref(d), ctypes.byref(need)))
+    ws = None
+    if need.value > 0:
+        ws = torch.empty(need.value, dtype=torch.uint8, device=query.device)
+        d.workspace, d.workspace_bytes = ws.data_ptr(), need.value
+    keep = (query, key_cache, value_cache, block_tables, context_lens, key_scales, value_scales)
+    return d, out, ws, keep
+
+
+def dynamic_sparse_attention(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                             block_tables: torch.Tensor, context_lens: torch.Tensor, max_seq_len: int,
+                             window_size: int, *, num_sink_tokens: int = 0, causal: bool = False,
+                             key_scales: Optional[torch.Tensor] = None, value_scales: Optional[torch.Tensor] = None,
+                             kv_layout: Optional[str] = None) -> torch.Tensor:
+    """Paged sparse attention; returns fp16 [batch, q_len, H, D].
+
+    Reference semantics for fp16 caches with the default keywords:
+    non-causal, keys [max(0, ctx-W), ctx), pages with block_tables < 0
+    skipped, W <= 0 or W > max_seq_len -> max_seq_len, scale 1/sqrt(D),
+    no visible key -> 0. uint8 caches are INT4 codes: "pages" layout
+    ([nb, H, bs, D/2] + fp16 scales, the INT4 pool) or "token_major"
+    ([nb, bs, H, D/2] + fp32 scales, quantize_kv_cache_int4 of an fp16 pool);
+    when the codes are the live INT4 pool and no scales are given, the
+    pool's scales are used.
+    """
+    with torch.cuda.device(query.device):
+        d, out, ws, _keep = _attention_desc(query, key_cache, value_cache, block_tables, context_lens,
+                                            max_seq_len, window_size, num_sink_tokens, causal, key_scales,
+                                            value_scales, kv_layout, None)
+        if d is not None:
+            _check(_c_attn(ctypes.byref(d), _stream(query)))
+    return out
+
+
+class PreparedAttention:
+    """A validated ``dynamic_sparse_attention`` call bound to fixed tensors.
+
+    Construction does the argument checks and workspace allocation once;
+    each call launches on the current stream with a single C-ABI call and
+    returns ``out`` (overwritten in place). Intended for decode loops where
+    only the tensor *contents* change between steps.
+    """
+
+    def __init__(self, query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size, *,
+                 num_sink_tokens=0, causal=False, key_scales=None, value_scales=None, kv_layout=None, out=None):
+        self.device = query.device
+        with torch.cuda.device(self.device):
+            self._d, self.out, self._ws, self._keep = _attention_desc(
+                query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size,
+                num_sink_tokens, causal, key_scales, value_scales, kv_layout, out)
+        self._dp = ctypes.byref(self._d) if self._d is not None else None
+
+    def __call__(self, stream: Optional[int] = None) -> torch.Tensor:
+        if self._dp is not None:
+            s = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
+            _check(_c_attn(self._dp, s))
+        return self.out

@@ -1,0 +1,47 @@
+/*
+ * quant_ref.c — C restatement of the reference INT4 quantizer, used as an
+ * independent CPU check of oracle.py (TEST INFRASTRUCTURE ONLY: only tests,
+ * the smoke check and the benchmark's CPU-baseline leg load it).
+ *
+ * Follows TheRadDani/memopt-transformer-runtime src/csrc/quantization.cu:
+ *   :129-171  absmax over a 64-element group; scale = absmax > 0 ? absmax/7 : 1
+ *   :183-186  code = clamp((int)roundf(v / scale) + 8, 0, 15)
+ *   :198-200  byte = code[2i] | code[2i+1] << 4
+ *   :254-262  dequant = float(code - 8) * scale (fp32; fp16 cast done by caller)
+ * Compiled without -ffast-math so division and roundf are IEEE / C99 exact.
+ */
+#include <math.h>
+#include <stdint.h>
+
+#define GROUP 64
+
+void oracle_quantize_int4(const float *in, int64_t num_groups, uint8_t *packed,
+                          float *scales) {
+  for (int64_t g = 0; g < num_groups; ++g) {
+    const float *v = in + g * GROUP;
+    float absmax = 0.0f;
+    for (int i = 0; i < GROUP; ++i) absmax = fmaxf(absmax, fabsf(v[i]));
+    const float scale = (absmax > 0.0f) ? (absmax / 7.0f) : 1.0f;
+    scales[g] = scale;
+    int codes[GROUP];
+    for (int i = 0; i < GROUP; ++i) {
+      const float r = roundf(v[i] / scale);
+      int iq = isnan(r) ? 8 : (int)r + 8;
+      codes[i] = iq < 0 ? 0 : (iq > 15 ? 15 : iq);
+    }
+    for (int i = 0; i < GROUP / 2; ++i)
+      packed[g * (GROUP / 2) + i] = (uint8_t)((codes[2 * i] & 0xF) | ((codes[2 * i + 1] & 0xF) << 4));
+  }
+}
+
+void oracle_dequantize_int4(const uint8_t *packed, const float *scales,
+                            int64_t num_groups, float *out) {
+  for (int64_t g = 0; g < num_groups; ++g) {
+    const float s = scales[g];
+    for (int i = 0; i < GROUP / 2; ++i) {
+      const uint8_t b = packed[g * (GROUP / 2) + i];
+      out[g * GROUP + 2 * i] = (float)((int)(b & 0xF) - 8) * s;
+      out[g * GROUP + 2 * i + 1] = (float)((int)(b >> 4) - 8) * s;
+    }
+  }
+}

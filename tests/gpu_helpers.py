@@ -1,0 +1,49 @@
+"""Helpers shared by the GPU tests (inputs, oracle round trips, tolerances)."""
+import numpy as np
+import torch
+
+# Floating-point tolerance of fused INT4 attention vs the composition oracle
+# (max-abs 2e-3 / rtol 1e-2 in fp16).
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def dev():
+    return torch.device("cuda", 0)
+
+
+def to_dev(a, dtype=None):
+    t = torch.as_tensor(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(dev())
+
+
+def assert_close(got, want, atol=ATOL, rtol=RTOL, what=""):
+    g = got.detach().float().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got, np.float32)
+    w = want.detach().float().cpu().numpy() if isinstance(want, torch.Tensor) else np.asarray(want, np.float32)
+    assert g.shape == w.shape, (g.shape, w.shape)
+    err = np.abs(g - w)
+    bad = err > atol + rtol * np.abs(w)
+    assert not bad.any(), f"{what}: {bad.sum()} elements off, max abs err {err.max():.3e}"
+
+
+def same_bits(got, want):
+    g = got.detach().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got)
+    w = np.asarray(want)
+    assert g.shape == w.shape, (g.shape, w.shape)
+    assert g.dtype.itemsize == w.dtype.itemsize
+    v = {1: np.uint8, 2: np.uint16, 4: np.uint32}[g.dtype.itemsize]
+    diff = np.nonzero(g.view(v) != w.view(v))
+    assert diff[0].size == 0, f"{diff[0].size} mismatches, first at {tuple(d[0] for d in diff)}"
+
+
+class _LazyExtension:
+    """Imports memopt_C on first use, so CPU-only collection never needs the
+    built library while a GPU test without it fails loudly (ImportError)."""
+
+    def __getattr__(self, name):
+        import memopt_C
+        return getattr(memopt_C, name)
+
+
+memopt_C = _LazyExtension()

@@ -1,0 +1,162 @@
+"""GPU parity of the fused INT4 paged decode kernel (q_len == 1, 16-token pages)
+against the composition oracle dequantize -> attention
+up to the full config 2 / 3 shapes."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import ATOL, RTOL, assert_close, dev, memopt_C, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _int4(kp, vp):
+    kc, ks = O.to_int4_pages(kp)
+    vc, vs = O.to_int4_pages(vp)
+    return kc, ks, vc, vs
+
+
+def _decode(q, kc, ks, vc, vs, bt, cl, msl, W, sinks=0, layout="pages"):
+    return memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kc), to_dev(vc), to_dev(bt), to_dev(cl), msl, W,
+                                             num_sink_tokens=sinks, key_scales=to_dev(ks), value_scales=to_dev(vs),
+                                             kv_layout=layout)
+
+
+def test_config1_decode():
+    """[64, 16, 8, 64] K/V N(0,1) 1% x8 seed 0, batch 1,
+    random page permutation, 1024 tokens, retain 1.0, 4 sinks."""
+    g = torch.Generator().manual_seed(0)
+    k = O.outlier_normal(g, (64, 16, 8, 64), 0.01, 8.0)
+    v = O.outlier_normal(g, (64, 16, 8, 64), 0.01, 8.0)
+    q = torch.randn((1, 1, 8, 64), generator=g).half().numpy()
+    bt = torch.randperm(64, generator=g).to(torch.int32).numpy()[None]
+    cl = np.array([1024], np.int32)
+    # token-major surface INT4 (fp32 scales): exactly the reference's INT4 path
+    kp, ks = O.quantize_int4(k)
+    vp, vs = O.quantize_int4(v)
+    want = O.paged_attention(q, O.dequantize_int4(kp, ks), O.dequantize_int4(vp, vs), bt, cl, 1024, 1024,
+                             num_sink_tokens=4)
+    got = _decode(q, kp, ks, vp, vs, bt, cl, 1024, 1024, 4, layout="token_major")
+    assert_close(got, want, what="config1 token_major")
+    # INT4 page pool (fp16 scales)
+    kc, kss, vc, vss = _int4(k, v)
+    want_p = O.paged_attention_int4(q, kc, kss, vc, vss, bt, cl, 1024, 1024, num_sink_tokens=4)
+    assert_close(_decode(q, kc, kss, vc, vss, bt, cl, 1024, 1024, 4), want_p, what="config1 pages")
+
+
+@pytest.mark.parametrize("B,H,D,ctx,W,sinks,unlink", [
+    (1, 1, 128, [4096], 4096, 0, 0),      # long single sequence: many splits
+    (2, 3, 64, [1000, 17], 200, 4, 2),    # ragged contexts, window, sinks, unlinked pages
+    (4, 2, 128, [1, 15, 16, 33], 64, 0, 0),
+    (2, 2, 128, [4100, 2050], 1024, 4, 5),
+    (1, 4, 128, [300], 8, 20, 0),          # sinks larger than the window
+])
+def test_decode_vs_oracle(B, H, D, ctx, W, sinks, unlink):
+    rng = np.random.default_rng(B * 7 + D)
+    bs = 16
+    M = (max(ctx) + bs - 1) // bs
+    nb = B * M + 5
+    kp = (rng.standard_normal((nb, bs, H, D)) * np.where(rng.random((nb, bs, H, D)) < 0.005, 10, 1)).astype(np.float16)
+    vp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    q = rng.standard_normal((B, 1, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    for i in range(unlink):
+        bt[0, rng.integers(0, M)] = -1
+    cl = np.array(ctx, np.int32)
+    kc, ks, vc, vs = _int4(kp, vp)
+    want = O.paged_attention_int4(q, kc, ks, vc, vs, bt, cl, 1 << 20, W, num_sink_tokens=sinks)
+    got = _decode(q, kc, ks, vc, vs, bt, cl, 1 << 20, W, sinks)
+    assert_close(got, want)
+    assert torch.equal(got, _decode(q, kc, ks, vc, vs, bt, cl, 1 << 20, W, sinks))  # deterministic
+
+
+# ---------------------------------------------------------------------------
+# Full-size configs: reference computed on the GPU in fp32 from the INT4 pages
+# dequantized by the (separately bit-exact) surface dequantize kernel.
+# ---------------------------------------------------------------------------
+
+def dequant_pages_dev(codes, scales):
+    """INT4 pages [nb, H, bs, D/2] + fp16 scales -> fp16 pool [nb, bs, H, D]."""
+    c = codes.permute(0, 2, 1, 3).contiguous()
+    s = scales.permute(0, 2, 1, 3).contiguous().float().reshape(-1)
+    return memopt_C.dequantize_kv_cache_int4(c, s, 64)
+
+
+def reference_decode_dev(q, kpool, vpool, bt, ctx, W, sinks):
+    """fp32 attention of one query per (b, h) over sinks U window on the GPU."""
+    B, _, H, D = q.shape
+    bs = kpool.shape[1]
+    out = torch.zeros(B, H, D, device=q.device)
+    for b in range(B):
+        c = int(ctx[b])
+        pages = bt[b, : (c + bs - 1) // bs].long()
+        ok = (pages >= 0).repeat_interleave(bs)[:c]
+        k = kpool[pages.clamp(min=0)].reshape(-1, H, D)[:c].float()
+        v = vpool[pages.clamp(min=0)].reshape(-1, H, D)[:c].float()
+        j = torch.arange(c, device=q.device)
+        vis = ((j >= c - W) | (j < sinks)) & ok
+        k, v = k[vis].permute(1, 0, 2), v[vis].permute(1, 0, 2)     # [H, n, D]
+        s = (k @ q[b, 0].float()[:, :, None]).squeeze(-1) / D ** 0.5  # [H, n]
+        p = torch.softmax(s, dim=-1)
+        out[b] = (p[:, None, :] @ v).squeeze(1)
+    return out.half()[:, None]
+
+
+def _fill_int4_pool(B, H, D, ctx, frac, mult, seed):
+    nbps = ctx // 16
+    nb = B * nbps
+    memopt_C.init_pool(nb, 16, H, D, kv_format="int4")
+    g = torch.Generator(device=dev()).manual_seed(seed)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed)).to(torch.int32)
+    bt = perm.reshape(B, nbps).to(dev())
+    slots = (bt.long()[:, :, None] * 16 + torch.arange(16, device=dev())).reshape(-1).to(torch.int32)
+    chunk = max(1, B // 4)  # write K/V a few sequences at a time to bound memory
+    for b0 in range(0, B, chunk):
+        n = chunk * ctx
+        k = torch.randn(n, H, D, device=dev(), generator=g)
+        k = torch.where(torch.rand(n, H, D, device=dev(), generator=g) < frac, k * mult, k).half()
+        v = torch.randn(n, H, D, device=dev(), generator=g)
+        v = torch.where(torch.rand(n, H, D, device=dev(), generator=g) < frac, v * mult, v).half()
+        memopt_C.write_cache(k, v, bt, slots[b0 * ctx:(b0 + chunk) * ctx].contiguous())
+        del k, v
+    q = torch.randn(B, 1, H, D, device=dev(), generator=g).half()
+    return q, bt
+
+
+def test_config2_full_size():
+    """Config 2: B16 H32 D128 ctx 4096, INT4 pages, random permutation, retain 1.0."""
+    B, H, D, ctx = 16, 32, 128, 4096
+    q, bt = _fill_int4_pool(B, H, D, ctx, 0.005, 10.0, 0)
+    cl = torch.full((B,), ctx, dtype=torch.int32, device=dev())
+    kc, vc = memopt_C.get_pool_tensors()
+    got = memopt_C.dynamic_sparse_attention(q, kc, vc, bt, cl, ctx, ctx)
+    ks, vs = memopt_C.get_pool_scales()
+    want = reference_decode_dev(q, dequant_pages_dev(kc, ks), dequant_pages_dev(vc, vs), bt, cl, ctx, 0)
+    assert_close(got, want, what="config2")
+    # CPU oracle on two sequences (composition through numpy)
+    for b in (0, 11):
+        pages = bt[b].cpu().numpy()
+        sub = lambda t: t[torch.as_tensor(pages).long().to(dev())].cpu().numpy()
+        w = O.paged_attention_int4(q[b:b + 1].cpu().numpy(), sub(kc), sub(ks), sub(vc), sub(vs),
+                                   np.arange(len(pages), dtype=np.int32)[None], np.array([ctx], np.int32), ctx, ctx)
+        assert_close(got[b:b + 1], w, what=f"config2 oracle b={b}")
+
+
+def test_config3_evict_then_sparse_decode():
+    """Config 3: ctx 8192, evict_tokens(r=0.75, 4 sinks) on LogNormal scores,
+    then decode over 4 sinks + a 2048-token window; evicted rows read as zeros."""
+    B, H, D, ctx, W, sinks = 16, 32, 128, 8192, 2048, 4
+    q, bt = _fill_int4_pool(B, H, D, ctx, 0.005, 10.0, 1)
+    scores = torch.exp(torch.randn(B, H, ctx, generator=torch.Generator().manual_seed(3))).to(dev())
+    ibf = torch.zeros(bt.numel(), dtype=torch.int32, device=dev())
+    bt0 = bt.clone()
+    memopt_C.evict_tokens(scores, bt, ibf, 0.75, sinks)
+    # unlinked pages are exactly those with H votes
+    assert torch.equal(bt == -1, (ibf[bt0.long()] == H))
+    cl = torch.full((B,), ctx, dtype=torch.int32, device=dev())
+    kc, vc = memopt_C.get_pool_tensors()
+    ks, vs = memopt_C.get_pool_scales()
+    got = memopt_C.dynamic_sparse_attention(q, kc, vc, bt, cl, ctx, W, num_sink_tokens=sinks)
+    want = reference_decode_dev(q, dequant_pages_dev(kc, ks), dequant_pages_dev(vc, vs), bt, cl, W, sinks)
+    assert_close(got, want, what="config3")

@@ -1,0 +1,102 @@
+"""GPU parity of evict_tokens / evict_cache against the oracle (intended
+semantics; the reference's literal defects are documented in the oracle)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_helpers import dev, memopt_C, same_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _pool_state(fmt):
+    k, v = memopt_C.get_pool_tensors()
+    st = {"format": fmt, "k": k.cpu().numpy(), "v": v.cpu().numpy()}
+    if fmt == "int4":
+        ks, vs = memopt_C.get_pool_scales()
+        st.update(ks=ks.cpu().numpy(), vs=vs.cpu().numpy())
+    return st
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int4"])
+@pytest.mark.parametrize("N,H,L,bs,r,sinks", [
+    (2, 4, 100, 16, 0.5, 4), (3, 2, 64, 16, 0.75, 0), (1, 8, 4096, 16, 0.75, 4),
+    (2, 2, 8192, 16, 0.3, 4), (2, 3, 50, 8, 0.1, 2), (1, 2, 40, 16, 1.0, 4)])
+def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
+    rng = np.random.default_rng(L + N)
+    D = 64
+    M = (L + bs - 1) // bs
+    nb = N * M + 3
+    memopt_C.init_pool(nb, bs, H, D, kv_format=fmt)
+    T = nb * bs
+    k = rng.standard_normal((T, H, D)).astype(np.float16)
+    v = rng.standard_normal((T, H, D)).astype(np.float16)
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)),
+                         to_dev(np.arange(T, dtype=np.int32)))
+    scores = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    scores[0, :, 16:32] = 1e-6  # one logical block evicted in every head -> unlinked
+    scores[:, 0, 1] = scores[:, 0, 2]  # ties
+    bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
+    ibf = np.zeros(nb, np.int32)
+    before = _pool_state(fmt)
+    bt_d, ibf_d = to_dev(bt), to_dev(ibf)
+    memopt_C.evict_tokens(to_dev(scores), bt_d, ibf_d, r, sinks)
+    O.evict_tokens_intended(scores, bt, ibf, r, sinks, before, bs)
+    after = _pool_state(fmt)
+    for key in before:
+        if key != "format":
+            same_bits(after[key], before[key])
+    same_bits(bt_d, bt)
+    same_bits(ibf_d, ibf)
+
+
+def test_evict_then_free_sweep():
+    memopt_C.init_pool(8, 16, 2, 64)
+    bt = torch.tensor([[memopt_C.allocate_block() for _ in range(4)]], dtype=torch.int32, device=dev())
+    scores = torch.ones(1, 2, 64, device=dev())
+    scores[:, :, 16:32] = 0.0
+    ibf = torch.zeros(8, dtype=torch.int32, device=dev())
+    memopt_C.evict_tokens(scores, bt, ibf, 0.75, 4)
+    assert bt.tolist() == [[0, -1, 2, 3]]
+    assert memopt_C.free_evicted_blocks(ibf) == [1] and memopt_C.free_blocks_count() == 5
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int4"])
+def test_evict_cache_vs_oracle(fmt):
+    rng = np.random.default_rng(5)
+    nb, bs, H, D = 6, 16, 4, 64
+    memopt_C.init_pool(nb, bs, H, D, kv_format=fmt)
+    T = nb * bs
+    k = rng.standard_normal((T, H, D)).astype(np.float16)
+    memopt_C.write_cache(to_dev(k), to_dev(k), to_dev(np.zeros((1, 1), np.int32)),
+                         to_dev(np.arange(T, dtype=np.int32)))
+    scores = rng.standard_normal((nb, bs, H)).astype(np.float32)
+    memopt_C.evict_cache(to_dev(np.zeros((1, 1), np.int32)), to_dev(scores), 0.4)
+    if fmt == "fp16":
+        kp = k.reshape(nb, bs, H, D).copy()
+        vp = kp.copy()
+        O.evict_cache(kp, vp, scores, 0.4)
+        same_bits(memopt_C.get_key_pool(), kp)
+    else:
+        fp = k.reshape(nb, bs, H, D).copy()
+        O.evict_cache(fp, fp.copy(), scores, 0.4)
+        zero = np.all(fp == 0, axis=-1)  # [nb, bs, H] evicted rows
+        codes = memopt_C.get_key_pool().cpu().numpy()  # [nb, H, bs, D/2]
+        for b in range(nb):
+            for p in range(bs):
+                for h in range(H):
+                    assert (codes[b, h, p] == 0x88).all() == zero[b, p, h]
+
+
+def test_evict_errors():
+    memopt_C.init_pool(4, 16, 2, 64)
+    s = torch.ones(1, 2, 64, device=dev())
+    bt = torch.zeros(1, 4, dtype=torch.int32, device=dev())
+    ibf = torch.zeros(4, dtype=torch.int32, device=dev())
+    with pytest.raises(RuntimeError, match="retain_ratio"):
+        memopt_C.evict_tokens(s, bt, ibf, 0.0)
+    with pytest.raises(RuntimeError, match="num_heads"):
+        memopt_C.evict_tokens(torch.ones(1, 3, 64, device=dev()), bt, ibf, 0.5)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        memopt_C.evict_tokens(s, torch.zeros(4, 1, dtype=torch.int32, device=dev()).t(), ibf, 0.5)

@@ -1,0 +1,385 @@
+"""CPU checks that pin the oracle (oracle/oracle.py) independently of itself.
+
+Each check is chosen so that a plausible slip in the restatement (round
+half-to-even instead of half-away, swapped nibbles, a dropped sink, an
+off-by-one window edge, a transposed page layout) fails it:
+  * known answers from the reference's own tests (tests/test_quant.py:439-566);
+  * exact rational (fractions.Fraction) evaluation of IEEE fp32 division and
+    rounding, and C ``roundf``, on random and adversarial groups;
+  * agreement with the independent C restatement (oracle/quant_ref.c, libm);
+  * attention against torch's scaled_dot_product_attention on unpaged K/V
+    and against a float64 brute-force loop on tiny inputs;
+  * eviction against brute-force ``sorted()`` selection.
+"""
+from fractions import Fraction
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+
+
+# ---------------------------------------------------------------------------
+# Exact rational model of IEEE rounding
+# ---------------------------------------------------------------------------
+
+def round_ieee(x: Fraction, prec: int, emin: int) -> Fraction:
+    """Round-to-nearest-even of an exact rational to a binary float with
+    `prec` significand bits and minimum normal exponent `emin` (subnormals
+    included, no overflow)."""
+    if x == 0:
+        return Fraction(0)
+    s = -1 if x < 0 else 1
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, emin)
+    quantum = Fraction(2) ** (e - prec + 1)
+    m = a / quantum
+    n = m.numerator // m.denominator
+    rem = m - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return s * n * quantum
+
+
+def rn32(x):
+    return round_ieee(x, 24, -126)
+
+
+def rn16(x):
+    return round_ieee(x, 11, -14)
+
+
+def exact_quant_group(vals16: np.ndarray):
+    """Reference quantizer evaluated in exact arithmetic (src/csrc/quantization.cu:129-202)."""
+    v = [Fraction(float(x)) for x in vals16.astype(np.float64)]
+    absmax = max(abs(x) for x in v)
+    scale = rn32(absmax / 7) if absmax > 0 else Fraction(1)
+    codes = []
+    for x in v:
+        q = rn32(x / scale)
+        r = math.floor(abs(q) + Fraction(1, 2)) * (1 if q >= 0 else -1)  # roundf: half away from zero
+        codes.append(min(max(r + 8, 0), 15))
+    return codes, scale
+
+
+# ---------------------------------------------------------------------------
+# Quantize: known answers
+# ---------------------------------------------------------------------------
+
+def test_kat_zeros():
+    packed, scales = O.quantize_int4(np.zeros((4, 128), np.float16))
+    assert (packed == 0x88).all() and (scales == 1.0).all()
+    assert (O.dequantize_int4(packed, scales) == 0).all()
+
+
+def test_kat_alternating_pm7():
+    x = np.empty(64, np.float16)
+    x[0::2], x[1::2] = 7.0, -7.0
+    packed, scales = O.quantize_int4(x)
+    assert scales.tolist() == [1.0] and (packed == 0x1F).all()  # lo = 15 (+7), hi = 1 (-7)
+    assert (O.dequantize_int4(packed, scales) == x).all()
+
+
+def test_kat_constant_half():
+    packed, scales = O.quantize_int4(np.full((4, 128), 0.5, np.float16))
+    assert (packed == 0xFF).all()
+    assert np.allclose(scales, np.float32(0.5) / np.float32(7))
+    d = O.dequantize_int4(packed, scales).astype(np.float32)
+    assert ((d - 0.5) ** 2).mean() < 1e-6
+
+
+def test_kat_single_group_shapes():
+    packed, scales = O.quantize_int4(np.random.default_rng(0).uniform(-1, 1, 64).astype(np.float16))
+    assert packed.shape == (32,) and scales.shape == (1,)
+
+
+def test_kat_round_half_away_and_nibble_order():
+    # absmax 7 -> scale exactly 1.0: v/scale == v, so the rounding mode is visible.
+    x = np.zeros(64, np.float16)
+    x[:10] = [0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 3.5, -3.5, 6.5, 7.0]
+    packed, scales = O.quantize_int4(x)
+    assert scales[0] == 1.0
+    codes = O.unpack_codes(packed)[:10].tolist()
+    # roundf: 0.5->1, -0.5->-1, 1.5->2, -1.5->-2, 2.5->3, -2.5->-3, 3.5->4, -3.5->-4, 6.5->7
+    assert codes == [9, 7, 10, 6, 11, 5, 12, 4, 15, 15]
+    # byte 0 = code[0] | code[1] << 4 (low nibble = even element)
+    assert packed[0] == (9 | (7 << 4))
+
+
+def test_quantize_exact_rational_random():
+    rng = np.random.default_rng(1)
+    groups = [
+        rng.standard_normal(64),
+        rng.standard_normal(64) * 1e-3,
+        rng.uniform(-100, 100, 64),
+        np.where(rng.random(64) < 0.05, 8.0, 1.0) * rng.standard_normal(64),
+        rng.standard_normal(64) * 6e-6,             # fp16 subnormals
+        np.linspace(-1, 1, 64),                     # many exact ties after scaling
+        np.array([7.0 * k / 8 for k in range(-32, 32)]),
+    ]
+    for g in groups:
+        x = g.astype(np.float16)
+        packed, scales = O.quantize_int4(x)
+        codes, scale = exact_quant_group(x)
+        assert Fraction(float(scales[0])) == scale
+        assert O.unpack_codes(packed).tolist() == codes
+
+
+def test_quantize_c_restatement_agrees():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((4096, 64)) * rng.choice([1.0, 8.0], size=(4096, 64), p=[0.99, 0.01])
+    x[0] = 0.0
+    x[1] = 1e-7
+    x[2, :] = np.linspace(-7, 7, 64)
+    x = x.astype(np.float16)
+    p1, s1 = O.quantize_int4(x)
+    p2, s2 = O.quantize_int4_c(x)
+    assert np.array_equal(p1, p2)
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+    d1, d2 = O.dequantize_int4(p1, s1), O.dequantize_int4_c(p2, s2)
+    assert np.array_equal(d1.view(np.uint16), d2.view(np.uint16))
+
+
+def test_dequantize_exact_rational():
+    rng = np.random.default_rng(3)
+    scales = np.concatenate([rng.uniform(1e-6, 20, 30), [1.0, 0.5 / 7, 1e-7]]).astype(np.float32)
+    codes = rng.integers(0, 16, size=(scales.size, 64)).astype(np.uint8)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    out = O.dequantize_int4(packed, scales)
+    for g in range(scales.size):
+        s = Fraction(float(scales[g]))
+        for e in (0, 1, 31, 63):
+            want = rn16(rn32((int(codes[g, e]) - 8) * s))
+            assert Fraction(float(out[g, e])) == want
+
+
+@pytest.mark.parametrize("dist,bound", [("uniform", 5e-3), ("normal", 5e-2), ("small", 5e-5)])
+def test_mse_bounds(dist, bound):
+    """Reference accuracy bounds (tests/test_quant.py:309-375) hold for the oracle."""
+    rng = np.random.default_rng(4)
+    x = {"uniform": rng.uniform(-1, 1, 8192), "normal": rng.standard_normal(8192),
+         "small": rng.uniform(-0.1, 0.1, 8192)}[dist].astype(np.float16)
+    p, s = O.quantize_int4(x)
+    d = O.dequantize_int4(p, s).astype(np.float32)
+    assert ((d - x.astype(np.float32)) ** 2).mean() < bound
+
+
+def test_error_bound_half_step():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((256, 64)) * 3).astype(np.float16)
+    p, s = O.quantize_int4(x)
+    d = O.dequantize_int4(p, s).astype(np.float32)
+    err = np.abs(d - x.astype(np.float32)).reshape(-1, 64)
+    # |deq - v| <= scale/2 plus the final fp16 rounding of the dequantized value
+    assert (err <= s[:, None] / 2 * (1 + 1e-6) + np.abs(d).reshape(-1, 64) * 2.0 ** -11).all()
+    codes = O.unpack_codes(p)
+    assert codes.min() >= 1 and codes.max() <= 15  # finite inputs never reach code 0
+
+
+def test_int4_pages_layout():
+    rng = np.random.default_rng(6)
+    pool = rng.standard_normal((3, 16, 4, 128)).astype(np.float16)
+    codes, sc = O.to_int4_pages(pool)
+    assert codes.shape == (3, 4, 16, 64) and sc.shape == (3, 4, 16, 2) and sc.dtype == np.float16
+    packed, scales = O.quantize_int4(pool)
+    # (page 2, token 5, head 3) row == codes[2, 3, 5]
+    assert np.array_equal(codes[2, 3, 5], packed[2, 5, 3])
+    assert sc[1, 2, 7, 1] == np.float16(scales.reshape(3, 16, 4, 2)[1, 7, 2, 1])
+    back = O.from_int4_pages(codes, sc)
+    ref = O.dequantize_int4(packed, scales.astype(np.float16).astype(np.float32))
+    assert np.array_equal(back.view(np.uint16), ref.view(np.uint16))
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+
+def brute_attention(q, kpool, vpool, bt, ctx_lens, W, sinks, causal):
+    """float64 loops straight from the visibility definitions."""
+    B, Lq, H, D = q.shape
+    bs = kpool.shape[1]
+    out = np.zeros((B, Lq, H, D))
+    for b in range(B):
+        ctx = int(ctx_lens[b])
+        for i in range(Lq):
+            pos = ctx - Lq + i
+            keys = []
+            for j in range(ctx):
+                page = int(bt[b, j // bs])
+                if page < 0:
+                    continue
+                if causal:
+                    vis = j <= pos and (j < sinks or j >= pos - W + 1)
+                else:
+                    vis = j >= ctx - W or j < sinks
+                if vis:
+                    keys.append((page, j % bs))
+            if not keys:
+                continue
+            for h in range(H):
+                qv = q[b, i, h].astype(np.float64)
+                sc = np.array([qv @ kpool[p, s, h].astype(np.float64) for p, s in keys]) / math.sqrt(D)
+                w = np.exp(sc - sc.max())
+                w /= w.sum()
+                out[b, i, h] = sum(wk * vpool[p, s, h].astype(np.float64) for wk, (p, s) in zip(w, keys))
+    return out
+
+
+def _paged_case(seed, B, H, D, bs, nb, ctx, Lq):
+    rng = np.random.default_rng(seed)
+    kp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    vp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    q = rng.standard_normal((B, Lq, H, D)).astype(np.float16)
+    M = (max(ctx) + bs - 1) // bs
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    return q, kp, vp, bt, np.array(ctx, np.int32)
+
+
+def test_attention_paged_equals_dense_sdpa():
+    """Permuted pages + full window == torch SDPA on the unpaged K/V (tests/test_attention.py:112-192)."""
+    q, kp, vp, bt, cl = _paged_case(0, 2, 4, 64, 16, 20, [128, 128], 128)
+    out = O.paged_attention(q, kp, vp, bt, cl, 128, 128).astype(np.float32)
+    for b in range(2):
+        kd = torch.as_tensor(kp[bt[b]].reshape(-1, 4, 64)).float().permute(1, 0, 2)[None]
+        vd = torch.as_tensor(vp[bt[b]].reshape(-1, 4, 64)).float().permute(1, 0, 2)[None]
+        qb = torch.as_tensor(q[b:b + 1]).float().permute(0, 2, 1, 3)
+        ref = F.scaled_dot_product_attention(qb, kd, vd)[0].permute(1, 0, 2).half().float().numpy()
+        assert np.abs(out[b] - ref).max() <= 1e-3
+
+
+@pytest.mark.parametrize("W,sinks,causal,ctx,Lq", [
+    (24, 0, False, [50, 37], 1),
+    (24, 4, False, [50, 37], 1),
+    (10, 3, False, [64, 20], 3),
+    (1000, 0, True, [40, 33], 40),   # plain causal
+    (12, 4, True, [48, 30], 16),     # StreamingLLM sink + window
+    (1, 1, True, [20, 17], 5),
+])
+def test_attention_brute_force(W, sinks, causal, ctx, Lq):
+    Lq = min(Lq, min(ctx))
+    q, kp, vp, bt, cl = _paged_case(1, 2, 2, 64, 8, 20, ctx, Lq)
+    bt[1, 1] = -1  # an unlinked page
+    out = O.paged_attention(q, kp, vp, bt, cl, max_seq_len=1000, window_size=W, num_sink_tokens=sinks,
+                            causal=causal).astype(np.float64)
+    ref = brute_attention(q, kp, vp, bt, cl, O.effective_window(W, 1000), sinks, causal)
+    assert np.abs(out - ref).max() <= 2e-3
+
+
+def test_attention_causal_equals_sdpa_is_causal():
+    q, kp, vp, bt, cl = _paged_case(2, 1, 2, 64, 16, 4, [64], 64)
+    out = O.paged_attention(q, kp, vp, bt, cl, 64, 64, causal=True).astype(np.float32)
+    kd = torch.as_tensor(kp[bt[0]].reshape(-1, 2, 64)).float().permute(1, 0, 2)[None]
+    vd = torch.as_tensor(vp[bt[0]].reshape(-1, 2, 64)).float().permute(1, 0, 2)[None]
+    qb = torch.as_tensor(q).float().permute(0, 2, 1, 3)
+    ref = F.scaled_dot_product_attention(qb, kd, vd, is_causal=True)[0].permute(1, 0, 2).half().float().numpy()
+    assert np.abs(out[0] - ref).max() <= 1e-3
+
+
+def test_attention_special_cases():
+    q, kp, vp, bt, cl = _paged_case(3, 1, 2, 64, 16, 4, [1], 1)
+    out = O.paged_attention(q, kp, vp, bt, np.array([1], np.int32), 16, 16)
+    assert np.array_equal(out[0, 0], vp[bt[0, 0], 0])            # ctx = 1 -> the V row
+    bt2 = np.full_like(bt, -1)
+    out2 = O.paged_attention(q, kp, vp, bt2, np.array([16], np.int32), 16, 16)
+    assert (out2 == 0).all()                                       # nothing visible -> 0
+    assert O.effective_window(0, 77) == 77 and O.effective_window(100, 77) == 77 and O.effective_window(5, 77) == 5
+
+
+def test_sdpa_fallback_matches_sink_window_rule():
+    q, kp, vp, bt, cl = _paged_case(4, 1, 2, 64, 16, 8, [100], 1)
+    a = O.sdpa_fallback(q, kp, vp, bt, cl, 1 << 20, 30, 4)
+    b = O.paged_attention(q, kp, vp, bt, cl, 1 << 20, 30, num_sink_tokens=4)
+    assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# Eviction
+# ---------------------------------------------------------------------------
+
+def _pools(fmt, nb, bs, H, D, rng):
+    if fmt == "fp16":
+        return {"format": "fp16", "k": rng.standard_normal((nb, bs, H, D)).astype(np.float16),
+                "v": rng.standard_normal((nb, bs, H, D)).astype(np.float16)}
+    return {"format": "int4", "k": rng.integers(0, 256, (nb, H, bs, D // 2)).astype(np.uint8),
+            "v": rng.integers(0, 256, (nb, H, bs, D // 2)).astype(np.uint8),
+            "ks": rng.uniform(0.1, 1, (nb, H, bs, D // 64)).astype(np.float16),
+            "vs": rng.uniform(0.1, 1, (nb, H, bs, D // 64)).astype(np.float16)}
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int4"])
+@pytest.mark.parametrize("r,sinks", [(0.5, 4), (0.75, 0), (0.1, 2), (1.0, 4)])
+def test_evict_intended_brute_force(fmt, r, sinks):
+    rng = np.random.default_rng(7)
+    N, H, L, bs, D = 2, 3, 40, 4, 64
+    scores = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    scores[0, 1, 8:12] = 1e-9  # a block fully low in one head
+    pools = _pools(fmt, 24, bs, H, D, rng)
+    pools0 = {k: (v.copy() if isinstance(v, np.ndarray) else v) for k, v in pools.items()}
+    bt = rng.permutation(24)[:N * 10].reshape(N, 10).astype(np.int32)
+    bt0 = bt.copy()
+    free = np.zeros(24, np.int32)
+    ev = O.evict_tokens_intended(scores, bt, free, r, sinks, pools, bs)
+    keep = max(1, min(L, math.ceil(np.float32(r) * np.float32(L))))
+    for n in range(N):
+        for h in range(H):
+            boosted = [1e38 if t < sinks else float(scores[n, h, t]) for t in range(L)]
+            tau = sorted(boosted, reverse=True)[keep - 1]
+            want = [t >= sinks and boosted[t] < tau for t in range(L)]
+            assert ev[n, h].tolist() == want
+            for t in range(L):
+                p, s = bt0[n, t // bs], t % bs
+                if fmt == "fp16":
+                    row = pools["k"][p, s, h]
+                    assert (row == 0).all() if want[t] else np.array_equal(row, pools0["k"][p, s, h])
+                else:
+                    row = pools["k"][p, h, s]
+                    assert (row == 0x88).all() if want[t] else np.array_equal(row, pools0["k"][p, h, s])
+    # votes: block (seq 0, logical block 2) is fully evicted only in head 1 -> 1 vote, still linked
+    assert free[bt0[0, 2]] == (1 if ev[0, 1, 8:12].all() and not ev[0, 0, 8:12].all() else free[bt0[0, 2]])
+    assert ((bt == -1) == (free[np.clip(bt0, 0, None)] == H)).all()
+
+
+def test_evict_intended_unlinks_fully_evicted_blocks():
+    N, H, L, bs = 1, 2, 16, 4
+    scores = np.ones((N, H, L), np.float32)
+    scores[:, :, 4:8] = 0.0  # lowest in every head
+    pools = _pools("fp16", 8, bs, H, 64, np.random.default_rng(8))
+    bt = np.arange(4, dtype=np.int32)[None]
+    free = np.zeros(8, np.int32)
+    O.evict_tokens_intended(scores, bt, free, 0.75, 0, pools, bs)
+    assert bt.tolist() == [[0, -1, 2, 3]] and free.tolist() == [0, 2, 0, 0, 0, 0, 0, 0]
+
+
+def test_evict_literal_defects():
+    rng = np.random.default_rng(9)
+    scores = rng.lognormal(size=(2, 2, 256)).astype(np.float32)
+    thr, ev = O.evict_tokens_literal(scores, num_sink_tokens=4, retain_ratio=0.5)
+    assert ev.sum() == 0  # G10: 1e38 sinks pin the bisection -> nothing evicted
+    thr0, ev0 = O.evict_tokens_literal(scores, num_sink_tokens=0, retain_ratio=0.5)
+    kept = (~ev0).sum(axis=2)
+    assert (kept >= 128).all() and (kept <= 130).all()
+    assert O.literal_block_counts(np.ones(256, bool), 16).max() == 1  # G12: never reaches 16
+    assert O.literal_zeroed_dims([5], 128) == {5: [5, 37, 69, 101]}  # G11: 4 of 128 dims
+
+
+def test_evict_cache_brute_force():
+    rng = np.random.default_rng(10)
+    nb, bs, H, D = 3, 8, 2, 64
+    scores = rng.standard_normal((nb, bs, H)).astype(np.float32)
+    kp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    vp = kp.copy()
+    O.evict_cache(kp, vp, scores, 0.4)
+    keep = int(np.float32(0.4) * np.float32(bs))
+    for b in range(nb):
+        for h in range(H):
+            tau = sorted(scores[b, :, h].tolist(), reverse=True)[keep - 1]
+            for p in range(bs):
+                assert (kp[b, p, h] == 0).all() == (scores[b, p, h] < tau)
