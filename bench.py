@@ -104,23 +104,20 @@ def cpu_baseline_decode(torch, O, memopt_C, tables, q, cl, cfg, budget_s=15.0):
     """Reference CPU path (dequantize + gather + fp32 SDPA) on a bounded sample of config 2."""
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    kc, vc = memopt_C.get_pool_tensors()
-    ks, vs = memopt_C.get_pool_scales()
     bt = tables[0]
     nseq = 2
     pages = bt[:nseq].reshape(-1).long()
     # Copy only the sampled sequences' pages to host memory.
-    sub = lambda t: t[pages].cpu()
-    ck, sk, cv, sv = sub(kc), sub(ks), sub(vc), sub(vs)
+    sub = memopt_C.get_int4_pages()[pages].cpu()
     local_bt = torch.arange(pages.numel(), dtype=torch.int32).reshape(nseq, -1)
     qc, clc = q[:nseq].cpu(), cl[:nseq].cpu()
     ctx = cfg["ctx"]
     times = []
-    O.decode_int4_torch(qc, ck, sk, cv, sv, local_bt, clc, ctx, 0)  # warm-up
+    O.decode_int4_torch(qc, sub, local_bt, clc, ctx, 0)  # warm-up
     t_end = time.perf_counter() + budget_s
     while len(times) < 5 and time.perf_counter() < t_end:
         t0 = time.perf_counter()
-        O.decode_int4_torch(qc, ck, sk, cv, sv, local_bt, clc, ctx, 0)
+        O.decode_int4_torch(qc, sub, local_bt, clc, ctx, 0)
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
@@ -191,7 +188,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profile_traffic("decode_int4_config2_pmc.txt"),
-                     "kernel": "decode_int4_kernel<128, half>", "kernel_ms": round(launch_ms, 5)},
+                     "kernel": "decode_int4_pages_kernel<128, 8, 2>", "kernel_ms": round(launch_ms, 5)},
     }
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))

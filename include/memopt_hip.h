@@ -33,10 +33,18 @@ extern "C" {
 #define MEMOPT_ERR_HIP          3  /* HIP runtime / launch error              */
 #define MEMOPT_ERR_UNSUPPORTED  4  /* configuration not compiled in           */
 
-/* KV pool storage formats (memopt_init_pool `kv_format`). */
-#define MEMOPT_KV_FP16  0  /* fp16 [num_blocks, block_size, H, D] (reference layout)     */
-#define MEMOPT_KV_INT4  1  /* INT4 pages: codes u8 [num_blocks, H, block_size, D/2],     *
-                            * fp16 scales [num_blocks, H, block_size, D/64]              */
+/* KV storage formats (memopt_init_pool `kv_format`, memopt_attn_desc.kv_format). */
+#define MEMOPT_KV_FP16       0  /* fp16 [num_blocks, block_size, H, D] (reference layout)  */
+#define MEMOPT_KV_INT4       1  /* INT4 page pool, one u8 buffer [num_blocks, H, B] with    *
+                                 * B = 16*D + 64*(D/64) bytes per (page, head):             *
+                                 *   K codes (8*D) | V codes (8*D) | K scales | V scales    *
+                                 * (fp16 scales, 32*(D/64) bytes each); 16-token pages;     *
+                                 * codes laid out for the wave64 decode kernel: lane 8p+c   *
+                                 * owns tokens (p, p+8) x dims [c*D/8, (c+1)*D/8); see      *
+                                 * memopt-transformer-runtime_amd/csrc/page_format.hpp.     */
+#define MEMOPT_KV_INT4_ROWS  2  /* attention input only: INT4 codes in the reference's      *
+                                 * quantize_kv_cache_int4 byte order with arbitrary         *
+                                 * page/head/token strides + separate f32/f16 scales        */
 
 /* Scale element types for INT4 caches passed to attention. */
 #define MEMOPT_SCALE_F32 0
@@ -54,10 +62,12 @@ const char *memopt_get_hello(void);
 
 /* Replaces init_pool(num_blocks, block_size, num_heads, head_dim) —
  * src/csrc/kv_cache.cu:112-153, bound at src/csrc/extension.cpp:20-26.
- * The caller allocates zero-filled storage and passes it in:
- *   MEMOPT_KV_FP16: key/value = fp16 [nb, bs, H, D]; key_scales/value_scales unused.
- *   MEMOPT_KV_INT4: key/value = u8 codes [nb, H, bs, D/2];
- *                   key_scales/value_scales = fp16 [nb, H, bs, D/64].
+ * The caller allocates the storage, filled with the empty-row pattern, and
+ * passes it in:
+ *   MEMOPT_KV_FP16: key/value = fp16 [nb, bs, H, D] zeros; scale pointers unused.
+ *   MEMOPT_KV_INT4: key_pool = the page buffer (codes 0x88, scales 1.0);
+ *                   value_pool / key_scales / value_scales unused (NULL);
+ *                   block_size must be 16 and head_dim a multiple of 64.
  * The free list is reseeded FIFO 0..nb-1. Invalid parameters tear the pool
  * down and return MEMOPT_ERR_INVALID. */
 int memopt_init_pool(int64_t num_blocks, int32_t block_size, int32_t num_heads,
@@ -158,8 +168,9 @@ int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_
                                     int32_t window_size, void *out, void *stream);
 
 /* Extended paged attention: the reference semantics above plus
- *   - INT4 caches (codes + f32/f16 group-64 scales, arbitrary page/head/token
- *     strides, dequantized just in time) — replaces the reference's
+ *   - INT4 caches — the INT4 page pool, or reference-order codes with
+ *     f32/f16 group-64 scales and arbitrary page/head/token strides —
+ *     dequantized just in time; replaces the reference's
  *     dequantize_kv_cache_int4 -> dynamic_sparse_attention composition;
  *   - attention sinks (keys j < num_sink_tokens always visible, the token
  *     rule of src/memopt/triton_attention.py:523-532);
@@ -173,15 +184,16 @@ typedef struct memopt_attn_desc {
   const void *query;          /* fp16 [batch, q_len, H, D] contiguous        */
   void *out;                  /* fp16 [batch, q_len, H, D] contiguous        */
   int32_t batch, q_len, num_heads, head_dim;
-  int32_t kv_is_int4;         /* 0: fp16 cache, 1: INT4 codes + scales       */
-  const void *key_cache;      /* fp16 elements or u8 codes                   */
-  const void *value_cache;
-  const void *key_scales;     /* INT4 only                                   */
+  int32_t kv_format;          /* MEMOPT_KV_FP16 / _INT4 (page pool) / _INT4_ROWS */
+  const void *key_cache;      /* fp16 elements, INT4 page buffer, or u8 codes */
+  const void *value_cache;    /* unused for MEMOPT_KV_INT4                   */
+  const void *key_scales;     /* MEMOPT_KV_INT4_ROWS only                    */
   const void *value_scales;
-  int32_t scale_dtype;        /* MEMOPT_SCALE_F32 / MEMOPT_SCALE_F16         */
+  int32_t scale_dtype;        /* MEMOPT_SCALE_F32 / MEMOPT_SCALE_F16 (ROWS)  */
   int32_t block_size;         /* tokens per page                             */
   int64_t num_kv_blocks;
-  /* Strides: fp16 cache in elements; INT4 codes in bytes; scales in elements. */
+  /* Strides (FP16 / INT4_ROWS only; derived for INT4 pages): fp16 cache in
+   * elements, INT4 codes in bytes, scales in elements. */
   int64_t kv_page_stride, kv_head_stride, kv_token_stride;
   int64_t sc_page_stride, sc_head_stride, sc_token_stride;
   const int32_t *block_tables; /* [batch, max_blocks_per_seq]                */

@@ -15,6 +15,7 @@
 //     reference's dequantize kernel would (fp16(RNE((code-8)*scale))) before
 //     use, so it computes the reference composition.
 #include "attention.hpp"
+#include "page_format.hpp"
 
 namespace memopt {
 
@@ -22,7 +23,7 @@ struct GenericParams {
   const half_t *q;
   half_t *out;
   int32_t B, Lq, H, D;
-  int32_t int4, scale_f16;
+  int32_t fmt, scale_f16;  // fmt: MEMOPT_KV_FP16 / _INT4 (page pool) / _INT4_ROWS
   const void *kc, *vc, *ks, *vs;
   int64_t kv_ps, kv_hs, kv_ts, sc_ps, sc_hs, sc_ts;
   int32_t bs;
@@ -34,17 +35,28 @@ struct GenericParams {
   float scale;
 };
 
-__device__ __forceinline__ float kv_elem(const GenericParams &p, const void *cache, const void *scales,
-                                         int64_t page, int32_t pos, int32_t head, int32_t d) {
-  if (!p.int4) {
+__device__ __forceinline__ float kv_elem(const GenericParams &p, bool is_v, int64_t page, int32_t pos,
+                                         int32_t head, int32_t d) {
+  const void *cache = is_v ? p.vc : p.kc;
+  if (p.fmt == MEMOPT_KV_FP16) {
     const half_t *c = (const half_t *)cache;
     return (float)c[page * p.kv_ps + (int64_t)pos * p.kv_ts + (int64_t)head * p.kv_hs + d];
   }
-  const uint8_t *c = (const uint8_t *)cache;
-  const uint8_t byte = c[page * p.kv_ps + (int64_t)pos * p.kv_ts + (int64_t)head * p.kv_hs + (d >> 1)];
+  uint8_t byte;
+  float s;
+  if (p.fmt == MEMOPT_KV_INT4) {
+    const Int4Page f(p.D);
+    const uint8_t *blk = (const uint8_t *)p.kc + (page * p.H + head) * f.block;
+    byte = is_v ? blk[f.vcodes + f.v_byte(pos, d)] : blk[f.kcodes + f.k_byte(pos, d)];
+    s = (float)reinterpret_cast<const half_t *>(blk + (is_v ? f.vscales : f.kscales))[f.scale_idx(pos, d >> 6)];
+  } else {
+    const uint8_t *c = (const uint8_t *)cache;
+    byte = c[page * p.kv_ps + (int64_t)pos * p.kv_ts + (int64_t)head * p.kv_hs + (d >> 1)];
+    const void *scales = is_v ? p.vs : p.ks;
+    const int64_t si = page * p.sc_ps + (int64_t)pos * p.sc_ts + (int64_t)head * p.sc_hs + (d >> 6);
+    s = p.scale_f16 ? (float)((const half_t *)scales)[si] : ((const float *)scales)[si];
+  }
   const int code = (d & 1) ? (byte >> 4) : (byte & 0xF);
-  const int64_t si = page * p.sc_ps + (int64_t)pos * p.sc_ts + (int64_t)head * p.sc_hs + (d >> 6);
-  const float s = p.scale_f16 ? (float)((const half_t *)scales)[si] : ((const float *)scales)[si];
   return (float)(half_t)((float)(code - 8) * s);
 }
 
@@ -83,7 +95,7 @@ __global__ __launch_bounds__(64) void generic_attention_kernel(const GenericPara
 #pragma unroll
       for (int i = 0; i < kMaxDimPerLane; ++i) {
         const int d = lane + 64 * i;
-        if (d < p.D) part += qv[i] * kv_elem(p, p.kc, p.ks, page, ps, h, d);
+        if (d < p.D) part += qv[i] * kv_elem(p, false, page, ps, h, d);
       }
       const float s = wave_sum(part) * p.scale;
       const float mn = fmaxf(m, s);
@@ -93,7 +105,7 @@ __global__ __launch_bounds__(64) void generic_attention_kernel(const GenericPara
 #pragma unroll
       for (int i = 0; i < kMaxDimPerLane; ++i) {
         const int d = lane + 64 * i;
-        if (d < p.D) acc[i] = acc[i] * alpha + pw * kv_elem(p, p.vc, p.vs, page, ps, h, d);
+        if (d < p.D) acc[i] = acc[i] * alpha + pw * kv_elem(p, true, page, ps, h, d);
       }
       m = mn;
     }
@@ -123,12 +135,17 @@ static int32_t max_pages_visited(const memopt_attn_desc &d) {
 }
 
 static bool use_decode_int4(const memopt_attn_desc &d) {
-  if (!d.kv_is_int4 || d.q_len != 1 || d.block_size != 16) return false;
+  if (d.q_len != 1 || d.block_size != 16 || d.num_kv_blocks <= 0) return false;
   if (d.head_dim != 64 && d.head_dim != 128) return false;
+  if (!aligned_to(d.query, 16)) return false;
+  if (d.kv_format == MEMOPT_KV_INT4) return aligned_to(d.key_cache, 16);
+  if (d.kv_format != MEMOPT_KV_INT4_ROWS) return false;
+  // Per-lane offsets inside a (page, head) block are 32-bit.
+  if (15 * d.kv_token_stride + d.head_dim / 2 >= (1LL << 31)) return false;
+  if (15 * d.sc_token_stride + d.head_dim / 64 >= (1LL << 31)) return false;
   const int64_t bpl = d.head_dim / 8;
   if (!aligned_to(d.key_cache, bpl) || !aligned_to(d.value_cache, bpl)) return false;
   if (d.kv_page_stride % bpl || d.kv_head_stride % bpl || d.kv_token_stride % bpl) return false;
-  if (!aligned_to(d.query, 16)) return false;
   return true;
 }
 
@@ -139,9 +156,17 @@ static int validate(const memopt_attn_desc &d) {
                  "paged_attention: head_dim must be even and <= 256");
   MEMOPT_REQUIRE(d.block_size > 0, MEMOPT_ERR_INVALID, "paged_attention: block_size must be > 0");
   MEMOPT_REQUIRE(d.max_blocks_per_seq >= 0, MEMOPT_ERR_INVALID, "paged_attention: bad max_blocks_per_seq");
-  if (d.kv_is_int4) {
+  MEMOPT_REQUIRE(d.kv_format == MEMOPT_KV_FP16 || d.kv_format == MEMOPT_KV_INT4 ||
+                     d.kv_format == MEMOPT_KV_INT4_ROWS,
+                 MEMOPT_ERR_INVALID, "paged_attention: unknown kv_format");
+  if (d.kv_format != MEMOPT_KV_FP16) {
     MEMOPT_REQUIRE(d.head_dim % 64 == 0, MEMOPT_ERR_INVALID,
                    "paged_attention: INT4 caches need head_dim % 64 == 0");
+  }
+  if (d.kv_format == MEMOPT_KV_INT4) {
+    MEMOPT_REQUIRE(d.block_size == 16, MEMOPT_ERR_INVALID, "paged_attention: INT4 page pools use 16-token pages");
+  }
+  if (d.kv_format == MEMOPT_KV_INT4_ROWS) {
     MEMOPT_REQUIRE(d.key_scales && d.value_scales, MEMOPT_ERR_INVALID, "paged_attention: INT4 needs scales");
     MEMOPT_REQUIRE(d.scale_dtype == MEMOPT_SCALE_F32 || d.scale_dtype == MEMOPT_SCALE_F16, MEMOPT_ERR_INVALID,
                    "paged_attention: unknown scale dtype");
@@ -179,7 +204,8 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
   int rc = validate(d);
   if (rc != MEMOPT_OK) return rc;
   if (d.batch == 0 || d.q_len == 0 || d.num_heads == 0 || d.head_dim == 0) return MEMOPT_OK;
-  MEMOPT_REQUIRE(d.query && d.out && d.key_cache && d.value_cache && d.block_tables && d.context_lens,
+  MEMOPT_REQUIRE(d.query && d.out && d.key_cache && (d.value_cache || d.kv_format == MEMOPT_KV_INT4) &&
+                     d.block_tables && d.context_lens,
                  MEMOPT_ERR_INVALID, "paged_attention: null pointer");
   const int32_t W = effective_window(d.window_size, d.max_seq_len);
   const float scale = 1.0f / sqrtf((float)d.head_dim);
@@ -194,18 +220,36 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
     DecodeParams p;
     p.q = (const half_t *)d.query;
     p.out = (half_t *)d.out;
-    p.kc = (const uint8_t *)d.key_cache;
-    p.vc = (const uint8_t *)d.value_cache;
-    p.ks = d.key_scales;
-    p.vs = d.value_scales;
-    p.kv_ps = d.kv_page_stride;
-    p.kv_hs = d.kv_head_stride;
-    p.kv_ts = d.kv_token_stride;
-    p.sc_ps = d.sc_page_stride;
-    p.sc_hs = d.sc_head_stride;
-    p.sc_ts = d.sc_token_stride;
+    if (d.kv_format == MEMOPT_KV_INT4) {
+      const Int4Page f(d.head_dim);
+      const uint8_t *base = (const uint8_t *)d.key_cache;
+      p.pages = 1;
+      p.kc = base + f.kcodes;
+      p.vc = base + f.vcodes;
+      p.ks = base + f.kscales;
+      p.vs = base + f.vscales;
+      p.kv_ps = d.num_heads * f.block;   // bytes
+      p.kv_hs = f.block;
+      p.kv_ts = 0;
+      p.sc_ps = d.num_heads * f.block / 2;  // fp16 elements
+      p.sc_hs = f.block / 2;
+      p.sc_ts = 0;
+    } else {
+      p.pages = 0;
+      p.kc = (const uint8_t *)d.key_cache;
+      p.vc = (const uint8_t *)d.value_cache;
+      p.ks = d.key_scales;
+      p.vs = d.value_scales;
+      p.kv_ps = d.kv_page_stride;
+      p.kv_hs = d.kv_head_stride;
+      p.kv_ts = d.kv_token_stride;
+      p.sc_ps = d.sc_page_stride;
+      p.sc_hs = d.sc_head_stride;
+      p.sc_ts = d.sc_token_stride;
+    }
     p.bt = d.block_tables;
     p.ctx = d.context_lens;
+    p.nb = d.num_kv_blocks;
     p.M = d.max_blocks_per_seq;
     p.H = d.num_heads;
     p.W = W;
@@ -214,7 +258,7 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
     p.qk_scale_log2 = scale * 1.4426950408889634f;
     p.ws_o = (float *)d.workspace;
     p.ws_ml = splits > 1 ? (float *)d.workspace + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
-    return launch_decode_int4(p, d.batch, d.head_dim, d.scale_dtype, s);
+    return launch_decode_int4(p, d.batch, d.head_dim, d.kv_format == MEMOPT_KV_INT4 ? MEMOPT_SCALE_F16 : d.scale_dtype, s);
   }
 
   GenericParams g;
@@ -224,7 +268,7 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
   g.Lq = d.q_len;
   g.H = d.num_heads;
   g.D = d.head_dim;
-  g.int4 = d.kv_is_int4;
+  g.fmt = d.kv_format;
   g.scale_f16 = d.scale_dtype == MEMOPT_SCALE_F16;
   g.kc = d.key_cache;
   g.vc = d.value_cache;
@@ -263,7 +307,7 @@ int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_
   d.q_len = q_len;
   d.num_heads = num_heads;
   d.head_dim = head_dim;
-  d.kv_is_int4 = 0;
+  d.kv_format = MEMOPT_KV_FP16;
   d.key_cache = key_cache;
   d.value_cache = value_cache;
   d.block_size = block_size;

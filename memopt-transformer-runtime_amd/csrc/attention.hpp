@@ -37,6 +37,8 @@ struct DecodeParams {
   int64_t sc_ps, sc_hs, sc_ts;  // scale strides, elements
   const int32_t *bt;
   const int32_t *ctx;
+  int64_t nb;                   // pages in the pool (entries >= nb are skipped)
+  int32_t pages;                // 1: this build's INT4 page format (page_format.hpp)
   int32_t M, H, W, sinks, splits;
   float qk_scale_log2;  // (1/sqrt(D)) * log2(e)
   float *ws_o;          // [B, H, splits, D] (splits > 1)

@@ -36,8 +36,8 @@ struct PoolView {
   bool initialized = false;
   int64_t num_blocks = 0;
   int32_t block_size = 0, num_heads = 0, head_dim = 0, kv_format = MEMOPT_KV_FP16;
-  void *key = nullptr, *value = nullptr;              // fp16 rows or INT4 codes
-  void *key_scales = nullptr, *value_scales = nullptr;  // INT4 fp16 scales
+  void *key = nullptr, *value = nullptr;  // fp16 pools; INT4: key = page buffer, value unused
+  void *key_scales = nullptr, *value_scales = nullptr;  // unused (kept for the ABI)
 };
 // Snapshot of the live pool (taken under the pool lock).
 PoolView pool_snapshot();
@@ -65,6 +65,26 @@ __device__ __forceinline__ float half_mirror(float v) { return dpp_f32<0x141>(v)
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// v_bfi_b32: (mask & a) | (~mask & b) in one VALU op. The compiler splits the
+// equivalent C expression into AND + OR when `b` is a constant, so the
+// instruction is requested directly; `mask` is a wave-uniform constant.
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+  return r;
+}
+
+// Wave64 max all-reduce: DPP inside rows of 16, LDS crossbar across rows.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, xor1(v));
+  v = fmaxf(v, xor2(v));
+  v = fmaxf(v, half_mirror(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
 
 // Group-64 symmetric INT4 code of v with scale s (IEEE divide, roundf half
 // away from zero, +8 offset, clamp [0,15]) — TheRadDani/memopt-transformer-runtime

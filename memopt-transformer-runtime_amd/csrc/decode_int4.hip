@@ -5,26 +5,31 @@
 //
 // HBM-bound design for gfx950 (wave64):
 //  * one wave streams one (page, head) block per step: 16 tokens x D/2 bytes
-//    of K codes and of V codes (1 KiB each at D=128) are read with one
-//    16-byte load per lane; lane l owns token l/4 and dims
-//    [ (l%4)*D/4, (l%4+1)*D/4 ), i.e. half of one 64-dim scale group;
-//  * nibbles become exact fp16 (code-8) with one AND-OR against an fp16
-//    exponent bias (0x6400 -> 1024+n for bits 0-3, 0x5400 -> 64+n for bits
-//    4-7) and one packed subtract; q.k uses v_dot2_f32_f16 (fp32 accumulate);
-//  * each lane keeps its own online-softmax state (m, l, acc) for its token
-//    slot, rescaling lazily only when a score exceeds the running max by more
-//    than 2^8 in exp2 units, so the page loop has no cross-lane traffic
-//    except a 2-step DPP sum of the 4 partial dot products of a token;
-//  * waves of a workgroup interleave pages of one (b, h); workgroups split a
-//    sequence's visited pages (split-K) and a small combine kernel merges the
-//    (m, l, o) partials by log-sum-exp when splits > 1;
-//  * only pages that intersect the sink range or the window are visited and
-//    block-table entries < 0 (evicted pages) are skipped without loads.
+//    of K codes and of V codes (1 KiB each at D=128) with one 16-byte load per
+//    lane; lane l owns token l/4 and dims [(l%4)*D/4, (l%4+1)*D/4), which lie
+//    inside one 64-dim scale group;
+//  * each wave keeps U pages in flight (loads for U pages are issued before
+//    any of them is consumed) and a workgroup runs NW waves over interleaved
+//    pages of one (b, h), so a CU holds tens of KiB of outstanding reads;
+//  * K nibbles become fp16 (bias + code) with one v_bfi_b32 against an fp16
+//    exponent pattern (0x6400 -> 1024 + n for bits 0-3, 0x5400 -> 64 + n for
+//    bits 4-7) and feed v_dot2_f32_f16 directly; the constant bias sum
+//    q . (bias + 8) is subtracted once per token, which leaves q . (code - 8);
+//  * V nibbles are unpacked exactly to (code - 8) in fp16 and accumulated in
+//    fp32 with v_fma_mix_f32 against the softmax weight times the V scale;
+//  * the softmax running max is wave-uniform and lazily raised: it is updated
+//    (with a wave max and a rescale of the accumulators) only when some score
+//    exceeds it by more than 8 in log2 units, so the common page costs no
+//    cross-lane reduction; the 4 partial dots of a token are summed with 2 DPP
+//    moves;
+//  * only pages that intersect the sink range or the window are visited,
+//    block-table entries < 0 or >= num_kv_blocks are skipped, and split-K
+//    partials (m, l, o) are merged by a small log-sum-exp combine kernel.
+#include <cstdlib>
+
 #include "attention.hpp"
 
 namespace memopt {
-
-static constexpr int kDecodeWaves = 4;
 
 template <typename ST>
 __device__ __forceinline__ float load_scale(const void *p, int64_t i) {
@@ -50,23 +55,37 @@ struct LaneChunk<64> {
   __device__ __forceinline__ uint32_t word(int i) const { return i == 0 ? w.x : w.y; }
 };
 
-// Exact (code - 8) for the 8 nibbles of a word, as 4 fp16 pairs in the order
-// (e0,e4), (e1,e5), (e2,e6), (e3,e7) where e_i = bits 4i..4i+3.
-__device__ __forceinline__ void unpack_word(uint32_t w, half2_t h[4]) {
-  const half2_t b1024 = {(half_t)1032.0f, (half_t)1032.0f};
-  const half2_t b64 = {(half_t)72.0f, (half_t)72.0f};
+static constexpr uint32_t kLoMask = 0x000F000Fu, kHiMask = 0x00F000F0u;
+static constexpr uint32_t kMagic1024 = 0x64006400u, kMagic64 = 0x54005400u;
+
+// Biased fp16 pairs of the 8 nibbles of a word, order (e0,e4), (e1,e5),
+// (e2,e6), (e3,e7) with e_i = bits 4i..4i+3: values 1024+e for the first and
+// third pair, 64+e for the second and fourth.
+__device__ __forceinline__ void unpack_biased(uint32_t w, uint32_t r[4]) {
   const uint32_t w8 = w >> 8;
-  h[0] = as_half2((w & 0x000F000Fu) | 0x64006400u) - b1024;
-  h[1] = as_half2((w & 0x00F000F0u) | 0x54005400u) - b64;
-  h[2] = as_half2((w8 & 0x000F000Fu) | 0x64006400u) - b1024;
-  h[3] = as_half2((w8 & 0x00F000F0u) | 0x54005400u) - b64;
+  r[0] = bfi(kLoMask, w, kMagic1024);
+  r[1] = bfi(kHiMask, w, kMagic64);
+  r[2] = bfi(kLoMask, w8, kMagic1024);
+  r[3] = bfi(kHiMask, w8, kMagic64);
+}
+
+// Same pairs as exact (code - 8) values.
+__device__ __forceinline__ void unpack_exact(uint32_t w, half2_t h[4]) {
+  uint32_t r[4];
+  unpack_biased(w, r);
+  const half2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f};
+  const half2_t b72 = {(half_t)72.0f, (half_t)72.0f};
+  h[0] = as_half2(r[0]) - b1032;
+  h[1] = as_half2(r[1]) - b72;
+  h[2] = as_half2(r[2]) - b1032;
+  h[3] = as_half2(r[3]) - b72;
 }
 
 // Slot s of a lane's accumulator holds dim base + kSlotDim[s % 8] + 8*(s / 8).
 __device__ __constant__ int kSlotDim[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 
-template <int D, typename ST>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_int4_kernel(const DecodeParams p) {
+template <int D, typename ST, int NW, int U>
+__global__ __launch_bounds__(NW * 64) void decode_int4_kernel(const DecodeParams p) {
   constexpr int BPL = D / 8;   // code bytes per lane per page
   constexpr int DPL = D / 4;   // dims per lane
   constexpr int NWORD = BPL / 4;
@@ -78,8 +97,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_int4_kernel(const De
   const int t = lane >> 2, c = lane & 3;
   const int g = (c * DPL) / 64;  // scale group of this lane's dims
 
-  __shared__ float s_acc[kDecodeWaves][D];
-  __shared__ float s_ml[kDecodeWaves][2];
+  __shared__ float s_acc[NW][D];
+  __shared__ float s_ml[NW][2];
 
   const int32_t ctx = p.ctx[b];
   const KeyRange kr = key_range(ctx, ctx - 1, p.W, p.sinks, false);
@@ -93,19 +112,21 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_int4_kernel(const De
   const int32_t begin = (int32_t)((n_vis * split) / p.splits);
   const int32_t end = (int32_t)((n_vis * (split + 1)) / p.splits);
 
-  // q in permuted fp16 pairs: word k of this lane covers dims c*DPL + 8k + 0..7.
+  // q as fp16 pairs in unpack order + the bias sum q . (bias + 8).
   half2_t qp[NWORD][4];
+  float bias = 0.0f;
   {
     const half_t *qrow = p.q + ((int64_t)b * p.H + h) * D + c * DPL;
 #pragma unroll
     for (int k = 0; k < NWORD; ++k) {
       const uint4 u = *reinterpret_cast<const uint4 *>(qrow + 8 * k);
-      const half2_t a = as_half2(u.x), bb = as_half2(u.y), cc = as_half2(u.z), dd = as_half2(u.w);
-      // elements: a=(0,1) bb=(2,3) cc=(4,5) dd=(6,7)
-      qp[k][0] = half2_t{a.x, cc.x};
-      qp[k][1] = half2_t{a.y, cc.y};
-      qp[k][2] = half2_t{bb.x, dd.x};
-      qp[k][3] = half2_t{bb.y, dd.y};
+      const half2_t e01 = as_half2(u.x), e23 = as_half2(u.y), e45 = as_half2(u.z), e67 = as_half2(u.w);
+      qp[k][0] = half2_t{e01.x, e45.x};
+      qp[k][1] = half2_t{e01.y, e45.y};
+      qp[k][2] = half2_t{e23.x, e67.x};
+      qp[k][3] = half2_t{e23.y, e67.y};
+      bias = fmaf(1032.0f, (float)e01.x + (float)e45.x + (float)e23.x + (float)e67.x, bias);
+      bias = fmaf(72.0f, (float)e01.y + (float)e45.y + (float)e23.y + (float)e67.y, bias);
     }
   }
 
@@ -115,68 +136,85 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_int4_kernel(const De
   for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
 
   const int32_t *btrow = p.bt + (int64_t)b * p.M;
-  const int64_t khead = (int64_t)h * p.kv_hs + (int64_t)t * p.kv_ts + c * BPL;
-  const int64_t shead = (int64_t)h * p.sc_hs + (int64_t)t * p.sc_ts + g;
+  const uint8_t *kbase = p.kc + (int64_t)h * p.kv_hs;
+  const uint8_t *vbase = p.vc + (int64_t)h * p.kv_hs;
+  const int64_t sbase = (int64_t)h * p.sc_hs;
+  const uint32_t koff = (uint32_t)(t * p.kv_ts + c * BPL);
+  const uint32_t soff = (uint32_t)(t * p.sc_ts + g);
 
-  for (int32_t i = begin + wave; i < end; i += kDecodeWaves) {
-    const int32_t lp = (i < sink_pages) ? i : win_page0 + (i - sink_pages);
-    const int32_t phys = __builtin_amdgcn_readfirstlane(btrow[lp]);
-    if (phys < 0) continue;  // evicted / unlinked page
-    Chunk kw, vw;
-    kw.load(p.kc + (int64_t)phys * p.kv_ps + khead);
-    vw.load(p.vc + (int64_t)phys * p.kv_ps + khead);
-    const float sk = load_scale<ST>(p.ks, (int64_t)phys * p.sc_ps + shead);
-    const float sv = load_scale<ST>(p.vs, (int64_t)phys * p.sc_ps + shead);
-
-    float dot = 0.0f;
+  for (int32_t base = begin + wave * U; base < end; base += NW * U) {
+    int32_t lp[U];
+    bool ok[U];
+    Chunk kw[U], vw[U];
+    float sk[U], sv[U];
 #pragma unroll
-    for (int k = 0; k < NWORD; ++k) {
-      half2_t hk[4];
-      unpack_word(kw.word(k), hk);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) dot = __builtin_amdgcn_fdot2(hk[j], qp[k][j], dot, false);
+    for (int u = 0; u < U; ++u) {
+      const int32_t i = base + u;
+      lp[u] = (i < sink_pages) ? i : win_page0 + (i - sink_pages);
+      const int32_t phys = btrow[(i < end) ? lp[u] : 0];  // lp < M whenever i < end
+      ok[u] = (i < end) && phys >= 0 && phys < p.nb;
+      // Invalid pages read page 0 of this head (always mapped) and are masked.
+      const int64_t pg = ok[u] ? (int64_t)phys : 0;
+      kw[u].load(kbase + pg * p.kv_ps + koff);
+      vw[u].load(vbase + pg * p.kv_ps + koff);
+      sk[u] = load_scale<ST>(p.ks, sbase + pg * p.sc_ps + soff);
+      sv[u] = load_scale<ST>(p.vs, sbase + pg * p.sc_ps + soff);
     }
-    float s = dot * sk;
-    s += xor1(s);
-    s += xor2(s);
-    const int32_t tok = lp * 16 + t;
-    const bool valid = tok < kr.hi && (tok >= kr.win_lo || tok < kr.sink_end);
-    s = valid ? s * p.qk_scale_log2 : -INFINITY;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NWORD; ++k) {
+        uint32_t r[4];
+        unpack_biased(kw[u].word(k), r);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot = __builtin_amdgcn_fdot2(as_half2(r[j]), qp[k][j], dot, false);
+      }
+      float s = (dot - bias) * sk[u];
+      s += xor1(s);
+      s += xor2(s);
+      const int32_t tok = lp[u] * 16 + t;
+      const bool valid = ok[u] && tok < kr.hi && (tok >= kr.win_lo || tok < kr.sink_end);
+      s = valid ? s * p.qk_scale_log2 : -INFINITY;
 
-    if (__any(s > m + 8.0f)) {
-      const float mn = fmaxf(m, s);
-      const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
-      l *= alpha;
+      if (__any(s > m + 8.0f)) {  // wave-uniform, rare after the first pages
+        const float mn = fmaxf(m, wave_max(s));
+        const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
+        l *= alpha;
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) acc[d] *= alpha;
-      m = mn;
-    }
-    const float pw = (s == -INFINITY) ? 0.0f : fast_exp2(s - m);
-    l += pw;
-    const float wv = pw * sv;
+        for (int d = 0; d < DPL; ++d) acc[d] *= alpha;
+        m = mn;
+      }
+      const float pw = valid ? fast_exp2(s - m) : 0.0f;
+      l += pw;
+      const float wv = pw * sv[u];
 #pragma unroll
-    for (int k = 0; k < NWORD; ++k) {
-      half2_t hv[4];
-      unpack_word(vw.word(k), hv);
+      for (int k = 0; k < NWORD; ++k) {
+        half2_t hv[4];
+        unpack_exact(vw[u].word(k), hv);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[8 * k + 2 * j] = fmaf(wv, (float)hv[j].x, acc[8 * k + 2 * j]);
-        acc[8 * k + 2 * j + 1] = fmaf(wv, (float)hv[j].y, acc[8 * k + 2 * j + 1]);
+        for (int j = 0; j < 4; ++j) {
+          acc[8 * k + 2 * j] = fmaf(wv, (float)hv[j].x, acc[8 * k + 2 * j]);
+          acc[8 * k + 2 * j + 1] = fmaf(wv, (float)hv[j].y, acc[8 * k + 2 * j + 1]);
+        }
       }
     }
   }
 
-  // Merge the 16 token slots that share this lane's dims (lanes c, c+4, ...).
+  // Sum the 16 token slots sharing this lane's dims (lanes c, c+4, ..., c+60);
+  // m is wave-uniform, so partials add directly. l counts each token once per c.
+  l += dpp_f32<0x124>(l);  // row_ror:4
+  l += dpp_f32<0x128>(l);  // row_ror:8
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
 #pragma unroll
-  for (int off = 4; off < 64; off <<= 1) {
-    const float mo = shfl_xor(m, off), lo = shfl_xor(l, off);
-    const float mn = fmaxf(m, mo);
-    const float a = (m == mn) ? 1.0f : fast_exp2(m - mn);
-    const float bsc = (mo == mn) ? 1.0f : fast_exp2(mo - mn);
-    l = l * a + lo * bsc;
-#pragma unroll
-    for (int d = 0; d < DPL; ++d) acc[d] = acc[d] * a + shfl_xor(acc[d], off) * bsc;
-    m = mn;
+  for (int d = 0; d < DPL; ++d) {
+    float v = acc[d];
+    v += dpp_f32<0x124>(v);
+    v += dpp_f32<0x128>(v);
+    v += shfl_xor(v, 16);
+    v += shfl_xor(v, 32);
+    acc[d] = v;
   }
   if (t == 0) {
 #pragma unroll
@@ -187,13 +225,187 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_int4_kernel(const De
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += kDecodeWaves * 64) {
+  for (int d = threadIdx.x; d < D; d += NW * 64) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_ml[w][0]);
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_ml[w][0]);
     float lt = 0.0f, o = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
+      const float f = (s_ml[w][0] == -INFINITY) ? 0.0f : fast_exp2(s_ml[w][0] - mx);
+      lt += s_ml[w][1] * f;
+      o += s_acc[w][d] * f;
+    }
+    const int64_t bh = (int64_t)b * p.H + h;
+    if (p.splits == 1) {
+      p.out[bh * D + d] = (half_t)(lt > 0.0f ? o / lt : 0.0f);
+    } else {
+      const int64_t slot = bh * p.splits + split;
+      p.ws_o[slot * D + d] = o;
+      if (d == 0) {
+        p.ws_ml[slot * 2] = mx;
+        p.ws_ml[slot * 2 + 1] = lt;
+      }
+    }
+  }
+}
+
+// Decode over this build's INT4 page format (page_format.hpp): lane l = 8p + c
+// owns tokens (p, p+8) and dims [c*D/8, (c+1)*D/8) of a (page, head) block.
+// The two partial dots of a lane reduce over its 8-lane group with 3 DPP
+// moves; V accumulates both tokens per instruction with v_dot2_f32_f16
+// against the fp16 pair of softmax weights (times V scales).
+template <int D, int NW, int U>
+__global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const DecodeParams p) {
+  constexpr int BPL = D / 8;     // bytes per lane per code region
+  constexpr int DPL = D / 8;     // dims per lane
+  constexpr int KW = BPL / 8;    // K words per token
+  constexpr int VW = BPL / 4;    // V words (4 dims x 2 tokens each)
+  using Chunk = LaneChunk<D>;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int32_t b = blockIdx.z, h = blockIdx.y, split = blockIdx.x;
+  const int pp = lane >> 3, c = lane & 7;
+  const int g = (c * DPL) / 64;
+
+  __shared__ float s_acc[NW][D];
+  __shared__ float s_ml[NW][2];
+
+  const int32_t ctx = p.ctx[b];
+  const KeyRange kr = key_range(ctx, ctx - 1, p.W, p.sinks, false);
+  const int32_t last_page = min((kr.hi + 15) >> 4, p.M);
+  const int32_t sink_pages = min((kr.sink_end + 15) >> 4, last_page);
+  const int32_t win_page0 = max(kr.win_lo >> 4, sink_pages);
+  const int32_t n_win = max(0, last_page - win_page0);
+  const int64_t n_vis = (int64_t)sink_pages + n_win;
+  const int32_t begin = (int32_t)((n_vis * split) / p.splits);
+  const int32_t end = (int32_t)((n_vis * (split + 1)) / p.splits);
+
+  // q for this lane's dims as fp16 pairs in unpack order; the dot products
+  // start from -q . (bias + 8) so they end at q . (code - 8).
+  half2_t qp[KW][4];
+  float bias = 0.0f;
+  {
+    const half_t *qrow = p.q + ((int64_t)b * p.H + h) * D + c * DPL;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) {
+      const uint4 u = *reinterpret_cast<const uint4 *>(qrow + 8 * k);
+      const half2_t e01 = as_half2(u.x), e23 = as_half2(u.y), e45 = as_half2(u.z), e67 = as_half2(u.w);
+      qp[k][0] = half2_t{e01.x, e45.x};
+      qp[k][1] = half2_t{e01.y, e45.y};
+      qp[k][2] = half2_t{e23.x, e67.x};
+      qp[k][3] = half2_t{e23.y, e67.y};
+      bias = fmaf(1032.0f, (float)e01.x + (float)e45.x + (float)e23.x + (float)e67.x, bias);
+      bias = fmaf(72.0f, (float)e01.y + (float)e45.y + (float)e23.y + (float)e67.y, bias);
+    }
+  }
+
+  float m = -INFINITY, l = 0.0f;
+  float acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
+
+  const int32_t *btrow = p.bt + (int64_t)b * p.M;
+  const uint8_t *kbase = p.kc + (int64_t)h * p.kv_hs + lane * BPL;
+  const uint8_t *vbase = p.vc + (int64_t)h * p.kv_hs + lane * BPL;
+  const half_t *ksb = (const half_t *)p.ks + (int64_t)h * p.sc_hs + g * 16 + 2 * pp;
+  const half_t *vsb = (const half_t *)p.vs + (int64_t)h * p.sc_hs + g * 16 + 2 * pp;
+
+  for (int32_t base = begin + wave * U; base < end; base += NW * U) {
+    int32_t lp[U];
+    bool ok[U];
+    Chunk kw[U], vw[U];
+    half2_t sk[U], sv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int32_t i = base + u;
+      lp[u] = (i < sink_pages) ? i : win_page0 + (i - sink_pages);
+      const int32_t phys = btrow[(i < end) ? lp[u] : 0];  // lp < M whenever i < end
+      ok[u] = (i < end) && phys >= 0 && phys < p.nb;
+      const int64_t pg = ok[u] ? (int64_t)phys : 0;     // invalid: page 0, masked below
+      kw[u].load(kbase + pg * p.kv_ps);
+      vw[u].load(vbase + pg * p.kv_ps);
+      sk[u] = *reinterpret_cast<const half2_t *>(ksb + pg * p.sc_ps);
+      sv[u] = *reinterpret_cast<const half2_t *>(vsb + pg * p.sc_ps);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float d0 = -bias, d1 = -bias;
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        uint32_t r0[4], r1[4];
+        unpack_biased(kw[u].word(k), r0);
+        unpack_biased(kw[u].word(KW + k), r1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          d0 = __builtin_amdgcn_fdot2(as_half2(r0[j]), qp[k][j], d0, false);
+          d1 = __builtin_amdgcn_fdot2(as_half2(r1[j]), qp[k][j], d1, false);
+        }
+      }
+      float s0 = d0 * (float)sk[u].x, s1 = d1 * (float)sk[u].y;
+      s0 += xor1(s0);
+      s1 += xor1(s1);
+      s0 += xor2(s0);
+      s1 += xor2(s1);
+      s0 += half_mirror(s0);
+      s1 += half_mirror(s1);
+      const int32_t t0 = lp[u] * 16 + pp, t1 = t0 + 8;
+      const bool v0 = ok[u] && t0 < kr.hi && (t0 >= kr.win_lo || t0 < kr.sink_end);
+      const bool v1 = ok[u] && t1 < kr.hi && (t1 >= kr.win_lo || t1 < kr.sink_end);
+      s0 = v0 ? s0 * p.qk_scale_log2 : -INFINITY;
+      s1 = v1 ? s1 * p.qk_scale_log2 : -INFINITY;
+      const float smax = fmaxf(s0, s1);
+      if (__any(smax > m + 8.0f)) {  // wave-uniform, rare after the first pages
+        const float mn = fmaxf(m, wave_max(smax));
+        const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] *= alpha;
+        m = mn;
+      }
+      const float p0 = v0 ? fast_exp2(s0 - m) : 0.0f;
+      const float p1 = v1 ? fast_exp2(s1 - m) : 0.0f;
+      l += p0 + p1;
+      const half2_t wpair = {(half_t)(p0 * (float)sv[u].x), (half_t)(p1 * (float)sv[u].y)};
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        half2_t hv[4];
+        unpack_exact(vw[u].word(k), hv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[4 * k + j] = __builtin_amdgcn_fdot2(hv[j], wpair, acc[4 * k + j], false);
+      }
+    }
+  }
+
+  // Sum the 8 token-pair lanes sharing this lane's dims (lanes c, c+8, ...).
+  l += dpp_f32<0x128>(l);  // row_ror:8
+  l += shfl_xor(l, 16);
+  l += shfl_xor(l, 32);
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) {
+    float v = acc[d];
+    v += dpp_f32<0x128>(v);
+    v += shfl_xor(v, 16);
+    v += shfl_xor(v, 32);
+    acc[d] = v;
+  }
+  if (pp == 0) {
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) s_acc[wave][c * DPL + d] = acc[d];
+    if (c == 0) {
+      s_ml[wave][0] = m;
+      s_ml[wave][1] = l;
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += NW * 64) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_ml[w][0]);
+    float lt = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
       const float f = (s_ml[w][0] == -INFINITY) ? 0.0f : fast_exp2(s_ml[w][0] - mx);
       lt += s_ml[w][1] * f;
       o += s_acc[w][d] * f;
@@ -244,30 +456,76 @@ static int device_cus() {
   return cus;
 }
 
+// Launch shape (waves per workgroup, pages in flight per wave). The default
+// is (8, 2); MEMOPT_DECODE_SHAPE="NW,U" selects another compiled shape for
+// tuning sweeps.
+struct DecodeShape {
+  int nw, u;
+};
+static DecodeShape decode_shape() {
+  static DecodeShape s = {0, 0};
+  if (s.nw == 0) {
+    s = {8, 2};
+    if (const char *e = std::getenv("MEMOPT_DECODE_SHAPE")) {
+      int a = 0, c = 0;
+      if (std::sscanf(e, "%d,%d", &a, &c) == 2 &&
+          ((a == 4 && c == 2) || (a == 8 && c == 1) || (a == 8 && c == 2) || (a == 8 && c == 4) ||
+           (a == 16 && c == 2) || (a == 4 && c == 4)))
+        s = {a, c};
+    }
+  }
+  return s;
+}
+
 int decode_splits(int32_t batch, int32_t heads, int32_t max_pages_visited) {
   const int64_t units = (int64_t)batch * heads;
   if (units <= 0) return 1;
+  const DecodeShape sh = decode_shape();
   const int64_t target_wgs = 2LL * device_cus();
   int64_t s = (target_wgs + units - 1) / units;
-  // Keep at least 8 pages per wave.
-  const int64_t cap = max_pages_visited / (8 * kDecodeWaves);
+  // Keep at least 4 page batches per wave.
+  const int64_t cap = max_pages_visited / (4LL * sh.nw * sh.u);
   if (s > cap) s = cap;
   if (s < 1) s = 1;
   if (s > 64) s = 64;
+  if (const char *e = std::getenv("MEMOPT_DECODE_SPLITS")) {
+    const int v = std::atoi(e);
+    if (v >= 1 && v <= 64) s = v;
+  }
   return (int)s;
+}
+
+template <int D, typename ST>
+static void launch_shape(const DecodeParams &p, dim3 grid, DecodeShape sh, hipStream_t stream) {
+#define MEMOPT_DECODE_CASE(NW_, U_)                                                                   \
+  if (sh.nw == NW_ && sh.u == U_) {                                                                   \
+    if (p.pages)                                                                                      \
+      hipLaunchKernelGGL((decode_int4_pages_kernel<D, NW_, U_>), grid, dim3(NW_ * 64), 0, stream, p); \
+    else                                                                                              \
+      hipLaunchKernelGGL((decode_int4_kernel<D, ST, NW_, U_>), grid, dim3(NW_ * 64), 0, stream, p);  \
+    return;                                                                                           \
+  }
+  MEMOPT_DECODE_CASE(8, 2)
+  MEMOPT_DECODE_CASE(8, 1)
+  MEMOPT_DECODE_CASE(8, 4)
+  MEMOPT_DECODE_CASE(4, 2)
+  MEMOPT_DECODE_CASE(4, 4)
+  MEMOPT_DECODE_CASE(16, 2)
+#undef MEMOPT_DECODE_CASE
 }
 
 int launch_decode_int4(const DecodeParams &p, int32_t batch, int32_t D, int32_t scale_dtype,
                        hipStream_t stream) {
-  const dim3 grid(p.splits, p.H, batch), block(kDecodeWaves * 64);
+  const DecodeShape sh = decode_shape();
+  const dim3 grid(p.splits, p.H, batch);
   if (D == 128 && scale_dtype == MEMOPT_SCALE_F16)
-    hipLaunchKernelGGL((decode_int4_kernel<128, half_t>), grid, block, 0, stream, p);
+    launch_shape<128, half_t>(p, grid, sh, stream);
   else if (D == 128)
-    hipLaunchKernelGGL((decode_int4_kernel<128, float>), grid, block, 0, stream, p);
+    launch_shape<128, float>(p, grid, sh, stream);
   else if (scale_dtype == MEMOPT_SCALE_F16)
-    hipLaunchKernelGGL((decode_int4_kernel<64, half_t>), grid, block, 0, stream, p);
+    launch_shape<64, half_t>(p, grid, sh, stream);
   else
-    hipLaunchKernelGGL((decode_int4_kernel<64, float>), grid, block, 0, stream, p);
+    launch_shape<64, float>(p, grid, sh, stream);
   int rc = check_launch("paged_attention(decode_int4)");
   if (rc != MEMOPT_OK || p.splits == 1) return rc;
   hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((int64_t)batch * p.H)), dim3(128), 0, stream,

@@ -12,6 +12,7 @@
 //   * no seq_len cap (the reference rejects seq_len > 4096).
 // evict_cache: src/csrc/kv_cache.cu:379-483 (per (block, head) selection).
 #include "common.hpp"
+#include "page_format.hpp"
 
 namespace memopt {
 
@@ -27,8 +28,8 @@ struct RowZero {
   void *k, *v, *ks, *vs;
 };
 
-// Zero (page, pos, head) in both K and V. fp16: D halves; INT4: D/2 codes
-// of 0x88 (code 8 == value 0) and D/64 fp16 scales of 1.0, which is exactly
+// Zero (page, pos, head) in both K and V. fp16: D halves; INT4 pages: the
+// row's codes set to 8 (value 0) and its D/64 fp16 scales to 1.0, which is exactly
 // what quantizing a zero row produces (scale 1.0 for an all-zero group,
 // src/csrc/quantization.cu:168).
 __device__ void zero_row(const RowZero &z, int64_t page, int32_t pos, int32_t head) {
@@ -48,17 +49,18 @@ __device__ void zero_row(const RowZero &z, int64_t page, int32_t pos, int32_t he
       }
     }
   } else {
-    const int64_t row = (page * z.H + head) * z.bs + pos;
-    uint32_t *k = (uint32_t *)((uint8_t *)z.k + row * (z.D / 2));
-    uint32_t *v = (uint32_t *)((uint8_t *)z.v + row * (z.D / 2));
-    for (int d = 0; d < z.D / 8; ++d) {
-      k[d] = 0x88888888u;
-      v[d] = 0x88888888u;
+    const Int4Page f(z.D);
+    uint8_t *blk = (uint8_t *)z.k + (page * z.H + head) * f.block;
+    const int32_t dpl = z.D / 8;
+    for (int c = 0; c < 8; ++c) {
+      uint8_t *kb = blk + f.kcodes + f.k_byte(pos, c * dpl);
+      for (int w = 0; w < dpl / 8; ++w) reinterpret_cast<uint32_t *>(kb)[w] = 0x88888888u;
+      for (int u = 0; u < dpl / 4; ++u)
+        *reinterpret_cast<uint16_t *>(blk + f.vcodes + f.v_byte(pos, c * dpl + 4 * u)) = 0x8888u;
     }
-    half_t *ks = (half_t *)z.ks + row * (z.D / 64), *vs = (half_t *)z.vs + row * (z.D / 64);
-    for (int g = 0; g < z.D / 64; ++g) {
-      ks[g] = (half_t)1.0f;
-      vs[g] = (half_t)1.0f;
+    for (int g = 0; g < f.G; ++g) {
+      reinterpret_cast<half_t *>(blk + f.kscales)[f.scale_idx(pos, g)] = (half_t)1.0f;
+      reinterpret_cast<half_t *>(blk + f.vscales)[f.scale_idx(pos, g)] = (half_t)1.0f;
     }
   }
 }

@@ -72,10 +72,12 @@ int memopt_init_pool(int64_t num_blocks, int32_t block_size, int32_t num_heads,
   if (kv_format == MEMOPT_KV_INT4) {
     MEMOPT_REQUIRE(head_dim % 64 == 0, MEMOPT_ERR_INVALID,
                    "init_pool: INT4 pools need head_dim % 64 == 0 (group size 64)");
-    MEMOPT_REQUIRE(key_scales && value_scales, MEMOPT_ERR_INVALID,
-                   "init_pool: INT4 pools need key/value scale storage");
+    MEMOPT_REQUIRE(block_size == 16, MEMOPT_ERR_INVALID, "init_pool: INT4 pools use 16-token pages");
+    MEMOPT_REQUIRE(key_pool, MEMOPT_ERR_INVALID, "init_pool: null page buffer");
+    value_pool = key_scales = value_scales = nullptr;
+  } else {
+    MEMOPT_REQUIRE(key_pool && value_pool, MEMOPT_ERR_INVALID, "init_pool: null pool storage");
   }
-  MEMOPT_REQUIRE(key_pool && value_pool, MEMOPT_ERR_INVALID, "init_pool: null pool storage");
   PoolView v;
   v.initialized = true;
   v.num_blocks = num_blocks;

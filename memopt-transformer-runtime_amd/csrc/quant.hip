@@ -11,6 +11,7 @@
 // per step, fully coalesced. The same device routine quantizes token rows
 // straight into INT4 pages in write_cache (fused write + quantize).
 #include "common.hpp"
+#include "page_format.hpp"
 
 namespace memopt {
 
@@ -117,19 +118,19 @@ __global__ __launch_bounds__(kThreads) void write_fp16_scalar_kernel(
   }
 }
 
-// Fused write + quantize into INT4 pages. Chunk i = 8 elements of the
-// (token, head) row; page layout codes [nb, H, bs, D/2], scales [nb, H, bs, D/64].
+// Fused write + quantize into the INT4 page pool (page_format.hpp). Chunk i =
+// 8 elements (dims 8cc..8cc+7) of the (token, head) row; all 8 lanes of a
+// 64-element group take the same branch, as quantize8's DPP reduction needs.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void write_int4_kernel(
-    const half_t *__restrict__ keys, const half_t *__restrict__ values, uint8_t *__restrict__ kc,
-    uint8_t *__restrict__ vc, half_t *__restrict__ ks, half_t *__restrict__ vs,
-    const int32_t *__restrict__ slots, int64_t n_chunks, int32_t H, int32_t D, int32_t bs,
-    int64_t n_slots) {
+    const half_t *__restrict__ keys, const half_t *__restrict__ values, uint8_t *__restrict__ pool,
+    const int32_t *__restrict__ slots, int64_t n_chunks, int32_t H, int32_t D, int64_t n_slots) {
+  const Int4Page f(D);
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   const int32_t cpr = D / 8;  // chunks per (token, head) row
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
     const int64_t th = i / cpr;
-    const int32_t c = (int32_t)(i - th * cpr);
+    const int32_t cc = (int32_t)(i - th * cpr);
     const int64_t t = th / H;
     const int32_t h = (int32_t)(th - t * H);
     const int64_t slot = slots[t];
@@ -137,27 +138,19 @@ __global__ __launch_bounds__(kThreads) void write_int4_kernel(
     load8<VEC>(keys + i * 8, kv);
     load8<VEC>(values + i * 8, vv);
     float s_k, s_v;
-    // All 8 lanes of a group run quantize8 together (same token => same branch).
     const uint32_t wk = quantize8(kv, s_k);
     const uint32_t wv = quantize8(vv, s_v);
     if (slot < 0 || slot >= n_slots) continue;
-    const int64_t page = slot / bs, pos = slot - page * bs;
-    const int64_t rowid = (page * H + h) * bs + pos;  // (page, head, token) row
-    const int64_t cb = rowid * (D / 2) + (int64_t)c * 4;
-    if (VEC) {
-      *reinterpret_cast<uint32_t *>(kc + cb) = wk;
-      *reinterpret_cast<uint32_t *>(vc + cb) = wv;
-    } else {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        kc[cb + b] = (uint8_t)(wk >> (8 * b));
-        vc[cb + b] = (uint8_t)(wv >> (8 * b));
-      }
-    }
-    if ((c & 7) == 0) {
-      const int64_t si = rowid * (D / 64) + (c >> 3);
-      ks[si] = (half_t)s_k;
-      vs[si] = (half_t)s_v;
+    const int64_t page = slot >> 4;
+    const int32_t pos = (int32_t)(slot & 15), d0 = 8 * cc;
+    uint8_t *blk = pool + (page * H + h) * f.block;
+    *reinterpret_cast<uint32_t *>(blk + f.kcodes + f.k_byte(pos, d0)) = wk;
+    uint8_t *vb = blk + f.vcodes + f.v_byte(pos, d0);
+    *reinterpret_cast<uint16_t *>(vb) = (uint16_t)(wv & 0xFFFFu);
+    *reinterpret_cast<uint16_t *>(vb + 4) = (uint16_t)(wv >> 16);
+    if ((d0 & 63) == 0) {
+      reinterpret_cast<half_t *>(blk + f.kscales)[f.scale_idx(pos, d0 >> 6)] = (half_t)s_k;
+      reinterpret_cast<half_t *>(blk + f.vscales)[f.scale_idx(pos, d0 >> 6)] = (half_t)s_v;
     }
   }
 }
@@ -247,14 +240,12 @@ int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
     const bool vec = aligned(keys, 16) && aligned(values, 16);
     if (vec)
       hipLaunchKernelGGL(write_int4_kernel<true>, dim3(grid_for(n)), dim3(kThreads), 0, s,
-                         (const half_t *)keys, (const half_t *)values, (uint8_t *)p.key, (uint8_t *)p.value,
-                         (half_t *)p.key_scales, (half_t *)p.value_scales, slot_mapping, n, num_heads, head_dim,
-                         p.block_size, n_slots);
+                         (const half_t *)keys, (const half_t *)values, (uint8_t *)p.key, slot_mapping, n,
+                         num_heads, head_dim, n_slots);
     else
       hipLaunchKernelGGL(write_int4_kernel<false>, dim3(grid_for(n)), dim3(kThreads), 0, s,
-                         (const half_t *)keys, (const half_t *)values, (uint8_t *)p.key, (uint8_t *)p.value,
-                         (half_t *)p.key_scales, (half_t *)p.value_scales, slot_mapping, n, num_heads, head_dim,
-                         p.block_size, n_slots);
+                         (const half_t *)keys, (const half_t *)values, (uint8_t *)p.key, slot_mapping, n,
+                         num_heads, head_dim, n_slots);
   }
   return check_launch("write_cache");
 }

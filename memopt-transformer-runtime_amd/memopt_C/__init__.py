@@ -35,7 +35,7 @@ import torch  # must precede the HIP library so both share one HIP runtime
 
 __all__ = [
     "get_hello", "init_pool", "allocate_block", "free_block", "get_pool_tensors",
-    "get_key_pool", "get_value_pool", "get_pool_scales", "free_blocks_count",
+    "get_key_pool", "get_value_pool", "get_pool_scales", "get_int4_pages", "int4_layout", "free_blocks_count",
     "write_cache", "evict_cache", "evict_tokens", "free_evicted_blocks",
     "dynamic_sparse_attention", "PreparedAttention", "quantize_kv_cache_int4", "dequantize_kv_cache_int4",
     "library_path",
@@ -62,7 +62,7 @@ class AttnDesc(ctypes.Structure):
     _fields_ = [
         ("query", _vp), ("out", _vp),
         ("batch", _i32), ("q_len", _i32), ("num_heads", _i32), ("head_dim", _i32),
-        ("kv_is_int4", _i32),
+        ("kv_format", _i32),
         ("key_cache", _vp), ("value_cache", _vp), ("key_scales", _vp), ("value_scales", _vp),
         ("scale_dtype", _i32), ("block_size", _i32), ("num_kv_blocks", _i64),
         ("kv_page_stride", _i64), ("kv_head_stride", _i64), ("kv_token_stride", _i64),
@@ -98,7 +98,7 @@ _c_dsa = _sig("memopt_dynamic_sparse_attention",
 _c_ws = _sig("memopt_attention_workspace_size", [ctypes.POINTER(AttnDesc), ctypes.POINTER(_i64)])
 _c_attn = _sig("memopt_paged_attention", [ctypes.POINTER(AttnDesc), _vp])
 
-KV_FP16, KV_INT4 = 0, 1
+KV_FP16, KV_INT4, KV_INT4_ROWS = 0, 1, 2
 _FORMATS = {"fp16": KV_FP16, "int4": KV_INT4}
 
 
@@ -158,20 +158,41 @@ def init_pool(num_blocks: int, block_size: int, num_heads: int, head_dim: int,
         if not ok or (fmt == KV_INT4 and head_dim % 64):
             # Let the library produce the reference's message (and stay torn down).
             _check(_c_init_pool(num_blocks, block_size, num_heads, head_dim, fmt, 1, 1, 1, 1))
+        if fmt == KV_INT4 and block_size != 16:
+            _check(_c_init_pool(num_blocks, block_size, num_heads, head_dim, fmt, 1, None, None, None))
         dev = torch.device("cuda", torch.cuda.current_device())
         if fmt == KV_FP16:
             shape = (num_blocks, block_size, num_heads, head_dim)
             k = torch.zeros(shape, dtype=torch.float16, device=dev)
             v = torch.zeros(shape, dtype=torch.float16, device=dev)
-            ks = vs = None
+            _check(_c_init_pool(num_blocks, block_size, num_heads, head_dim, fmt, k.data_ptr(), v.data_ptr(),
+                                None, None))
+            _pool.update(k=k, v=v, pages=None)
         else:
-            k = torch.full((num_blocks, num_heads, block_size, head_dim // 2), 0x88, dtype=torch.uint8, device=dev)
-            v = torch.full_like(k, 0x88)
-            ks = torch.ones((num_blocks, num_heads, block_size, head_dim // 64), dtype=torch.float16, device=dev)
-            vs = torch.ones_like(ks)
-        _check(_c_init_pool(num_blocks, block_size, num_heads, head_dim, fmt, k.data_ptr(), v.data_ptr(),
-                            ks.data_ptr() if ks is not None else None, vs.data_ptr() if vs is not None else None))
-        _pool.update(k=k, v=v, ks=ks, vs=vs, fmt=fmt, nb=num_blocks, bs=block_size, h=num_heads, d=head_dim)
+            lay = int4_layout(head_dim)
+            pages = torch.empty((num_blocks, num_heads, lay["block"]), dtype=torch.uint8, device=dev)
+            pages.copy_(_empty_int4_block(head_dim, dev).expand_as(pages))
+            _check(_c_init_pool(num_blocks, block_size, num_heads, head_dim, fmt, pages.data_ptr(), None, None, None))
+            _pool.update(pages=pages, k=pages[:, :, lay["kcodes"]:lay["vcodes"]],
+                         v=pages[:, :, lay["vcodes"]:lay["kscales"]],
+                         ks=pages[:, :, lay["kscales"]:lay["vscales"]].view(torch.float16),
+                         vs=pages[:, :, lay["vscales"]:].view(torch.float16))
+        _pool.update(fmt=fmt, nb=num_blocks, bs=block_size, h=num_heads, d=head_dim)
+
+
+def int4_layout(head_dim: int) -> dict:
+    """Byte offsets of the regions of one (page, head) block of the INT4 page
+    pool (include/memopt_hip.h MEMOPT_KV_INT4)."""
+    D, G = head_dim, head_dim // 64
+    return {"kcodes": 0, "vcodes": 8 * D, "kscales": 16 * D, "vscales": 16 * D + 32 * G, "block": 16 * D + 64 * G}
+
+
+def _empty_int4_block(head_dim: int, dev) -> torch.Tensor:
+    """One (page, head) block of an empty row set: codes 8 (0x88), scales 1.0."""
+    lay = int4_layout(head_dim)
+    blk = torch.full((lay["block"],), 0x88, dtype=torch.uint8)
+    blk[lay["kscales"]:] = torch.ones((lay["block"] - lay["kscales"]) // 2, dtype=torch.float16).view(torch.uint8)
+    return blk.to(dev)
 
 
 def _pool_or_raise(fn: str) -> dict:
@@ -200,10 +221,19 @@ def free_blocks_count() -> int:
 def get_pool_tensors() -> Tuple[torch.Tensor, torch.Tensor]:
     """(key_pool, value_pool) aliases of the live storage (src/csrc/kv_cache.cu:190-193).
 
-    fp16 pools: [nb, bs, H, D] fp16. INT4 pools: codes [nb, H, bs, D/2] uint8.
+    fp16 pools: [nb, bs, H, D] fp16. INT4 pools: views of the K and V code
+    regions of the page buffer, uint8 [nb, H, 8*D] (codes in the page
+    layout); passing them to ``dynamic_sparse_attention`` attends over the pool.
     """
     p = _pool_or_raise("get_pool_tensors")
     return p["k"], p["v"]
+
+
+def get_int4_pages() -> torch.Tensor:
+    """The INT4 page buffer, uint8 [nb, H, 16*D + 64*(D/64)]."""
+    p = _pool_or_raise("get_int4_pages")
+    _require(p["fmt"] == KV_INT4, "get_int4_pages: pool is not an INT4 pool")
+    return p["pages"]
 
 
 def get_key_pool() -> torch.Tensor:
@@ -215,7 +245,7 @@ def get_value_pool() -> torch.Tensor:
 
 
 def get_pool_scales() -> Tuple[torch.Tensor, torch.Tensor]:
-    """fp16 group scales [nb, H, bs, D/64] of an INT4 pool."""
+    """fp16 group-scale regions of an INT4 pool, views [nb, H, 16*D/64] (page layout order)."""
     p = _pool_or_raise("get_pool_scales")
     _require(p["fmt"] == KV_INT4, "get_pool_scales: pool is not an INT4 pool")
     return p["ks"], p["vs"]
@@ -381,27 +411,35 @@ def dequantize_kv_cache_int4(q_cache: torch.Tensor, scales: torch.Tensor, group_
 # Attention — src/csrc/attention.cu:371-521
 # ---------------------------------------------------------------------------
 
-def _int4_layout(key_cache, key_scales, kv_layout, num_heads, head_dim):
-    """Resolve (block_size, num_blocks, code strides, scale strides, scale dtype)."""
-    if kv_layout is None:
-        kv_layout = "pages" if key_scales.dtype == torch.float16 else "token_major"
+def _int4_rows_layout(key_cache, key_scales, num_heads, head_dim):
+    """Token-major INT4 codes [nb, bs, H, D/2] (quantize_kv_cache_int4 of an fp16
+    pool) + f32/f16 scales [nb*bs*H*D/64]: (bs, nb, code strides, scale strides, scale dtype)."""
     G = head_dim // 64
-    if kv_layout == "pages":  # codes [nb, H, bs, D/2], scales [nb, H, bs, D/64]
-        nb, h, bs, dh = key_cache.shape
-        _require(h == num_heads and dh * 2 == head_dim, "dynamic_sparse_attention: INT4 page shape mismatch")
-        kv = (h * bs * dh, bs * dh, dh)
-        sc = (h * bs * G, bs * G, G)
-    elif kv_layout == "token_major":  # codes [nb, bs, H, D/2], scales [nb*bs*H*D/64]
-        nb, bs, h, dh = key_cache.shape
-        _require(h == num_heads and dh * 2 == head_dim, "dynamic_sparse_attention: INT4 cache shape mismatch")
-        kv = (bs * h * dh, dh, h * dh)
-        sc = (bs * h * G, G, h * G)
-    else:
-        raise RuntimeError(f"dynamic_sparse_attention: unknown kv_layout {kv_layout!r}")
-    _require(key_scales.numel() == nb * bs * num_heads * G, "dynamic_sparse_attention: scales size mismatch")
-    sdt = 1 if key_scales.dtype == torch.float16 else 0
+    nb, bs, h, dh = key_cache.shape
+    _require(h == num_heads and dh * 2 == head_dim, "dynamic_sparse_attention: INT4 cache shape mismatch")
+    _require(key_cache.is_contiguous(), "key_cache must be contiguous")
     _require(key_scales.dtype in (torch.float16, torch.float32), "dynamic_sparse_attention: scales must be f16/f32")
-    return bs, nb, kv, sc, sdt
+    _require(key_scales.numel() == nb * bs * num_heads * G, "dynamic_sparse_attention: scales size mismatch")
+    kv = (bs * h * dh, dh, h * dh)
+    sc = (bs * h * G, G, h * G)
+    return bs, nb, kv, sc, 1 if key_scales.dtype == torch.float16 else 0
+
+
+def _int4_pages_base(key_cache, value_cache, num_heads, head_dim):
+    """Base pointer and page count when the caches are the INT4 page buffer (or
+    its K/V code views from get_pool_tensors), else None."""
+    lay = int4_layout(head_dim)
+    if _pool and _pool["fmt"] == KV_INT4 and _pool["d"] == head_dim and _pool["h"] == num_heads:
+        base = _pool["pages"].data_ptr()
+        if key_cache.data_ptr() in (base, base + lay["kcodes"]) and \
+                value_cache.data_ptr() in (base, base + lay["vcodes"]):
+            return base, _pool["nb"], _pool["pages"]
+    if key_cache.dim() == 3 and key_cache.shape[1] == num_heads and key_cache.shape[2] == lay["block"]:
+        _require(key_cache.is_contiguous(), "INT4 page buffer must be contiguous")
+        _require(value_cache.data_ptr() == key_cache.data_ptr(),
+                 "dynamic_sparse_attention: pass the INT4 page buffer as both key_cache and value_cache")
+        return key_cache.data_ptr(), key_cache.shape[0], key_cache
+    return None
 
 
 def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size,
@@ -414,10 +452,9 @@ def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, m
     for t, n in ((query, "query"), (key_cache, "key_cache"), (value_cache, "value_cache"),
                  (block_tables, "block_tables"), (context_lens, "context_lens")):
         _require(isinstance(t, torch.Tensor) and t.is_cuda, f"{n} must be a CUDA tensor")
+    for t, n in ((query, "query"), (block_tables, "block_tables"), (context_lens, "context_lens")):
         _require(t.is_contiguous(), f"{n} must be contiguous")
     _require(query.dim() == 4, "query must be 4-D [batch, q_len, num_heads, head_dim]")
-    _require(key_cache.dim() == 4, "key_cache must be 4-D [num_kv_blocks, block_size, num_heads, head_dim]")
-    _require(value_cache.dim() == 4, "value_cache must be 4-D [num_kv_blocks, block_size, num_heads, head_dim]")
     _require(block_tables.dim() == 2, "block_tables must be 2-D [batch, max_blocks_per_seq]")
     _require(context_lens.dim() == 1, "context_lens must be 1-D [batch]")
     _require(query.dtype == torch.float16, "query must be fp16")
@@ -430,21 +467,38 @@ def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, m
         out = torch.empty_like(query)
     _require(out.shape == query.shape and out.dtype == torch.float16 and out.is_contiguous() and out.is_cuda,
              f"{fn}: out must be a contiguous fp16 CUDA tensor shaped like query")
-    int4 = key_cache.dtype == torch.uint8
-    if int4:
-        _require(value_cache.dtype == torch.uint8 and value_cache.shape == key_cache.shape,
-                 "value_cache must match key_cache (INT4 codes)")
-        if key_scales is None and _pool and _pool["fmt"] == KV_INT4 and \
-                key_cache.data_ptr() == _pool["k"].data_ptr() and value_cache.data_ptr() == _pool["v"].data_ptr():
-            key_scales, value_scales = _pool["ks"], _pool["vs"]
-        _require(key_scales is not None and value_scales is not None, f"{fn}: INT4 caches need key/value scales")
-        for t, n in ((key_scales, "key_scales"), (value_scales, "value_scales")):
-            _require(t.is_cuda and t.is_contiguous(), f"{n} must be a contiguous CUDA tensor")
-        _require(key_scales.dtype == value_scales.dtype and key_scales.shape == value_scales.shape,
-                 f"{fn}: key/value scales mismatch")
+    keep = (query, key_cache, value_cache, block_tables, context_lens, key_scales, value_scales)
+    fmt = KV_FP16
+    sc = (0, 0, 0)
+    sdt = 0
+    kv = (0, 0, 0)
+    base_k, base_v = key_cache.data_ptr(), value_cache.data_ptr()
+    if key_cache.dtype == torch.uint8:
+        _require(value_cache.dtype == torch.uint8, "value_cache must match key_cache (INT4 codes)")
         _require(D % 64 == 0, f"{fn}: INT4 caches need head_dim % 64 == 0")
-        bs, nb, kv, sc, sdt = _int4_layout(key_cache, key_scales, kv_layout, H, D)
+        pages = _int4_pages_base(key_cache, value_cache, H, D) if kv_layout in (None, "pages") else None
+        if pages is not None:
+            fmt = KV_INT4
+            base_k, nb, buf = pages
+            base_v = base_k
+            bs = 16
+            keep = keep + (buf,)
+        else:
+            _require(kv_layout in (None, "token_major"), f"{fn}: not an INT4 page buffer")
+            _require(key_cache.dim() == 4 and value_cache.shape == key_cache.shape and value_cache.is_contiguous(),
+                     "key_cache must be 4-D [num_kv_blocks, block_size, num_heads, head_dim/2] (INT4 codes)")
+            _require(key_scales is not None and value_scales is not None, f"{fn}: INT4 caches need key/value scales")
+            for t, n in ((key_scales, "key_scales"), (value_scales, "value_scales")):
+                _require(t.is_cuda and t.is_contiguous(), f"{n} must be a contiguous CUDA tensor")
+            _require(key_scales.dtype == value_scales.dtype and key_scales.shape == value_scales.shape,
+                     f"{fn}: key/value scales mismatch")
+            fmt = KV_INT4_ROWS
+            bs, nb, kv, sc, sdt = _int4_rows_layout(key_cache, key_scales, H, D)
     else:
+        for t, n in ((key_cache, "key_cache"), (value_cache, "value_cache")):
+            _require(t.is_contiguous(), f"{n} must be contiguous")
+        _require(key_cache.dim() == 4, "key_cache must be 4-D [num_kv_blocks, block_size, num_heads, head_dim]")
+        _require(value_cache.dim() == 4, "value_cache must be 4-D [num_kv_blocks, block_size, num_heads, head_dim]")
         _require(key_cache.dtype == torch.float16, "key_cache must be fp16")
         _require(value_cache.dtype == torch.float16, "value_cache must be fp16")
         nb, bs = key_cache.shape[0], key_cache.shape[1]
@@ -454,16 +508,14 @@ def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, m
         _require(value_cache.shape[2] == H, "value_cache num_heads mismatch")
         _require(value_cache.shape[3] == D, "value_cache head_dim mismatch")
         kv = (bs * H * D, D, H * D)
-        sc = (0, 0, 0)
-        sdt = 0
     if B == 0 or Lq == 0 or H == 0 or D == 0:
         return None, out, None, ()
     d = AttnDesc()
     d.query, d.out = query.data_ptr(), out.data_ptr()
     d.batch, d.q_len, d.num_heads, d.head_dim = B, Lq, H, D
-    d.kv_is_int4 = int(int4)
-    d.key_cache, d.value_cache = key_cache.data_ptr(), value_cache.data_ptr()
-    if int4:
+    d.kv_format = fmt
+    d.key_cache, d.value_cache = base_k, base_v
+    if fmt == KV_INT4_ROWS:
         d.key_scales, d.value_scales = key_scales.data_ptr(), value_scales.data_ptr()
     d.scale_dtype, d.block_size, d.num_kv_blocks = sdt, bs, nb
     d.kv_page_stride, d.kv_head_stride, d.kv_token_stride = kv
@@ -478,7 +530,6 @@ def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, m
     if need.value > 0:
         ws = torch.empty(need.value, dtype=torch.uint8, device=query.device)
         d.workspace, d.workspace_bytes = ws.data_ptr(), need.value
-    keep = (query, key_cache, value_cache, block_tables, context_lens, key_scales, value_scales)
     return d, out, ws, keep
 
 
@@ -492,12 +543,14 @@ def dynamic_sparse_attention(query: torch.Tensor, key_cache: torch.Tensor, value
     Reference semantics for fp16 caches with the default keywords:
     non-causal, keys [max(0, ctx-W), ctx), pages with block_tables < 0
     skipped, W <= 0 or W > max_seq_len -> max_seq_len, scale 1/sqrt(D),
-    no visible key -> 0. uint8 caches are INT4 codes: "pages" layout
-    ([nb, H, bs, D/2] + fp16 scales, the INT4 pool) or "token_major"
-    ([nb, bs, H, D/2] + fp32 scales, quantize_kv_cache_int4 of an fp16 pool);
-    when the codes are the live INT4 pool and no scales are given, the
-    pool's scales are used.
+    no visible key -> 0. uint8 caches are INT4: either the INT4 page pool
+    (its code views from ``get_pool_tensors()``, or a page buffer
+    [nb, H, 16*D + 64*D/64] passed as both caches; scales live in the
+    pages), or token-major codes [nb, bs, H, D/2] from
+    ``quantize_kv_cache_int4`` of an fp16 pool together with their
+    ``key_scales`` / ``value_scales`` (``kv_layout="token_major"``).
     """
+    _require(isinstance(query, torch.Tensor) and query.is_cuda, "query must be a CUDA tensor")
     with torch.cuda.device(query.device):
         d, out, ws, _keep = _attention_desc(query, key_cache, value_cache, block_tables, context_lens,
                                             max_seq_len, window_size, num_sink_tokens, causal, key_scales,
@@ -518,6 +571,7 @@ class PreparedAttention:
 
     def __init__(self, query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size, *,
                  num_sink_tokens=0, causal=False, key_scales=None, value_scales=None, kv_layout=None, out=None):
+        _require(isinstance(query, torch.Tensor) and query.is_cuda, "query must be a CUDA tensor")
         self.device = query.device
         with torch.cuda.device(self.device):
             self._d, self.out, self._ws, self._keep = _attention_desc(

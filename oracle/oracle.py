@@ -19,10 +19,12 @@ quantize_int4 / dequantize_int4
     groups, and the independent C restatement ``oracle/quant_ref.c``
     (libm ``roundf``).
 to_int4_pages / from_int4_pages
-    Layout change of the same group-64 codes into this build's INT4 page
-    format (codes [nb, H, bs, D/2], fp16 scales [nb, H, bs, D/64]); scales
-    are RNE fp16 of the fp32 scale. Pinned by round trip and by direct
-    comparison with ``quantize_int4`` of the token-major pool.
+    Placement of the same group-64 codes in this build's INT4 page buffer
+    ([nb, H, block], block = K codes | V codes | K scales | V scales, token
+    pairs interleaved for the wave64 decode kernel); scales are RNE fp16 of
+    the fp32 scale. This format has no reference counterpart; pinned by the
+    writer/reader round trip and by direct comparison with ``quantize_int4``
+    of the token-major pool.
 write_cache
     src/csrc/kv_cache.cu:228-260. Pinned by the invariant pool[slot] == row.
 paged_attention
@@ -168,27 +170,82 @@ def dequantize_int4_c(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
 # INT4 page format of this build
 # ---------------------------------------------------------------------------
 
-def to_int4_pages(pool: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
-    """fp16 pool [nb, bs, H, D] -> (codes u8 [nb, H, bs, D/2], scales f16 [nb, H, bs, D/64]).
+PAGE_TOKENS = 16
 
-    The groups are the reference's (page, token, head, 64-dim chunk) groups
-    (src/csrc/quantization.cu:115-116 on a contiguous [nb, bs, H, D] pool);
-    only their placement changes (head-major inside a page) and the scale is
-    stored as RNE fp16 of the fp32 scale.
+
+def int4_block_bytes(D: int) -> int:
+    """Bytes per (page, head) block: K codes 8D | V codes 8D | K scales 32G | V scales 32G."""
+    return 16 * D + 64 * (D // GROUP)
+
+
+def int4_page_maps(D: int):
+    """Byte offsets inside a block for the code byte of (token t, dims 2j..2j+1)
+    of K and of V, and fp16 indices of the (token, group) scales.
+
+    Layout (one wave64 reads a block; lane 8p+c owns tokens p and p+8 and the
+    D/8 dims starting at c*D/8, i.e. BPL = D/8 bytes of each code region):
+      K byte = lane*BPL + (t // 8)*(BPL/2) + r/2           (r = dim offset in the lane chunk)
+      V byte = lane*BPL + (r // 4)*4 + (t // 8)*2 + (r % 4)//2   (4-dim units, tokens interleaved)
+      scale  = g*16 + 2*(t % 8) + t // 8
+    Returns (k_off [16, D/2], v_off [16, D/2], s_idx [16, D/64]).
     """
-    nb, bs, H, D = pool.shape
-    packed, scales = quantize_int4(pool)
-    codes = packed.reshape(nb, bs, H, D // 2).transpose(0, 2, 1, 3).copy()
-    sc = scales.reshape(nb, bs, H, D // GROUP).transpose(0, 2, 1, 3).astype(np.float16).copy()
-    return codes, sc
+    dpl = bpl = D // 8
+    t = np.arange(PAGE_TOKENS)[:, None]
+    d = np.arange(0, D, 2)[None, :]
+    c, r = d // dpl, d % dpl
+    lane = 8 * (t % 8) + c
+    k_off = lane * bpl + (t // 8) * (bpl // 2) + r // 2
+    v_off = lane * bpl + (r // 4) * 4 + (t // 8) * 2 + (r % 4) // 2
+    g = np.arange(D // GROUP)[None, :]
+    s_idx = g * 16 + 2 * (t % 8) + t // 8
+    return k_off, v_off, s_idx
 
 
-def from_int4_pages(codes: np.ndarray, scales_f16: np.ndarray) -> np.ndarray:
-    """Dequantize INT4 pages back to an fp16 pool [nb, bs, H, D]."""
-    nb, H, bs, Dh = codes.shape
-    packed = codes.transpose(0, 2, 1, 3).copy()
-    sc = scales_f16.transpose(0, 2, 1, 3).copy()
-    return dequantize_int4(packed, sc)
+def to_int4_pages(k_pool: np.ndarray, v_pool: np.ndarray) -> np.ndarray:
+    """fp16 pools [nb, 16, H, D] (K, V) -> INT4 page buffer u8 [nb, H, block].
+
+    Codes are the reference's group-64 codes of the token-major pools
+    (src/csrc/quantization.cu:115-116 on a contiguous [nb, bs, H, D] tensor:
+    groups = (page, token, head, 64-dim chunk)); scales are stored as RNE
+    fp16 of the fp32 scale.
+    """
+    nb, bs, H, D = k_pool.shape
+    assert bs == PAGE_TOKENS and D % GROUP == 0
+    G = D // GROUP
+    k_off, v_off, s_idx = int4_page_maps(D)
+    out = np.zeros((nb, H, int4_block_bytes(D)), np.uint8)
+    for pool, code_base, scale_base, off in ((k_pool, 0, 16 * D, k_off), (v_pool, 8 * D, 16 * D + 32 * G, v_off)):
+        packed, scales = quantize_int4(pool)
+        codes = packed.reshape(nb, bs, H, D // 2).transpose(0, 2, 1, 3)          # [nb, H, t, j]
+        out[:, :, code_base + off.reshape(-1)] = codes.reshape(nb, H, -1)
+        sc = scales.reshape(nb, bs, H, G).transpose(0, 2, 1, 3).astype(np.float16)  # [nb, H, t, g]
+        sb = sc.view(np.uint8).reshape(nb, H, bs, G, 2)
+        idx = scale_base + 2 * s_idx
+        out[:, :, idx.reshape(-1)] = sb[..., 0].reshape(nb, H, -1)
+        out[:, :, idx.reshape(-1) + 1] = sb[..., 1].reshape(nb, H, -1)
+    return out
+
+
+def int4_pages_split(pages: np.ndarray, D: int):
+    """Page buffer -> (K codes, K fp16 scales, V codes, V fp16 scales) in the
+    reference's token-major order: codes [nb, 16, H, D/2], scales [nb, 16, H, D/64]."""
+    nb, H, blk = pages.shape
+    G = D // GROUP
+    k_off, v_off, s_idx = int4_page_maps(D)
+    res = []
+    for code_base, scale_base, off in ((0, 16 * D, k_off), (8 * D, 16 * D + 32 * G, v_off)):
+        codes = pages[:, :, code_base + off.reshape(-1)].reshape(nb, H, PAGE_TOKENS, D // 2)
+        idx = (scale_base + 2 * s_idx).reshape(-1)
+        sb = np.stack((pages[:, :, idx], pages[:, :, idx + 1]), axis=-1).reshape(nb, H, PAGE_TOKENS, G, 2)
+        sc = np.ascontiguousarray(sb).view(np.float16).reshape(nb, H, PAGE_TOKENS, G)
+        res += [codes.transpose(0, 2, 1, 3).copy(), sc.transpose(0, 2, 1, 3).copy()]
+    return tuple(res)
+
+
+def from_int4_pages(pages: np.ndarray, D: int):
+    """Dequantize an INT4 page buffer back to fp16 pools (K, V) [nb, 16, H, D]."""
+    kc, ks, vc, vs = int4_pages_split(pages, D)
+    return dequantize_int4(kc, ks), dequantize_int4(vc, vs)
 
 
 # ---------------------------------------------------------------------------
@@ -278,15 +335,13 @@ def paged_attention(query, key_cache, value_cache, block_tables, context_lens,
     return out.to(torch.float16).numpy()
 
 
-def paged_attention_int4(query, codes_k, scales_k, codes_v, scales_v, block_tables,
-                         context_lens, max_seq_len, window_size, num_sink_tokens=0,
-                         causal=False):
-    """Composition oracle of the fused INT4 path (the reference has no fused
-    INT4 attention; its INT4 path is dequantize_kv_cache_int4 followed by
-    dynamic_sparse_attention, src/csrc/quantization.cu:371-428 and
-    src/csrc/attention.cu:371). Pages in this build's INT4 page format."""
-    kp = from_int4_pages(codes_k, scales_k)
-    vp = from_int4_pages(codes_v, scales_v)
+def paged_attention_int4(query, pages, block_tables, context_lens, max_seq_len, window_size,
+                         num_sink_tokens=0, causal=False):
+    """Composition oracle of the fused INT4 path on an INT4 page buffer (the
+    reference has no fused INT4 attention; its INT4 path is
+    dequantize_kv_cache_int4 followed by dynamic_sparse_attention,
+    src/csrc/quantization.cu:371-428 and src/csrc/attention.cu:371)."""
+    kp, vp = from_int4_pages(pages, query.shape[-1])
     return paged_attention(query, kp, vp, block_tables, context_lens, max_seq_len,
                            window_size, num_sink_tokens, causal)
 
@@ -317,15 +372,23 @@ def keep_count(retain_ratio: float, L: int) -> int:
 
 
 def _zero_row(pools, phys: int, pos: int, head: int) -> None:
-    """Zero one (token, head) row of K and V in every pool format."""
-    fmt = pools["format"]
-    if fmt == "fp16":
+    """Zero one (token, head) row of K and V in every pool format (INT4 pages:
+    codes 8 and scale 1.0, what quantizing a zero row yields)."""
+    if pools["format"] == "fp16":
         pools["k"][phys, pos, head, :] = 0
         pools["v"][phys, pos, head, :] = 0
     else:
-        for c, s in (("k", "ks"), ("v", "vs")):
-            pools[c][phys, head, pos, :] = 0x88
-            pools[s][phys, head, pos, :] = np.float16(1.0)
+        D = pools["D"]
+        G = D // GROUP
+        k_off, v_off, s_idx = int4_page_maps(D)
+        blk = pools["pages"][phys, head]
+        blk[k_off[pos]] = 0x88
+        blk[8 * D + v_off[pos]] = 0x88
+        one = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+        for base in (16 * D, 16 * D + 32 * G):
+            for g in range(G):
+                i = base + 2 * s_idx[pos, g]
+                blk[i], blk[i + 1] = one[0], one[1]
 
 
 def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
@@ -335,8 +398,9 @@ def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
     Per (seq, head): sink scores := 1e38 (:722-726); keep = keep_count;
     tau = keep-th largest boosted score; tokens with boosted score < tau are
     evicted (ties at tau kept); every evicted (token, head) row is zeroed
-    (fp16: zeros; INT4 pages: codes 0x88 and scale 1.0 — what quantizing a
-    zero row yields). A logical block whose block_size positions are all
+    (fp16: zeros; INT4 pages: codes 8 and scale 1.0 — what quantizing a
+    zero row yields); pools = {"format": "fp16", "k", "v"} or
+    {"format": "int4", "pages", "D"}. A logical block whose block_size positions are all
     evicted in this head votes is_block_free[phys] += 1; the vote that
     reaches H sets block_tables[seq, lb] = -1 (:993-1014).
     Mutates block_tables, is_block_free and pools in place; returns the
@@ -460,33 +524,39 @@ def outlier_normal(gen, shape, frac: float, mult: float, std: float = 1.0):
 # Vectorized torch-CPU form of the INT4 decode path (CPU baseline timing)
 # ---------------------------------------------------------------------------
 
-def dequant_pages_torch(codes, scales):
-    """torch CPU: INT4 pages [n, H, bs, D/2] u8 + fp16 scales [n, H, bs, D/64]
-    -> fp16 [n, bs, H, D]; same values as :func:`from_int4_pages`."""
+def dequant_pages_torch(pages, D):
+    """torch: INT4 page blocks [n, H, block] u8 -> fp16 (K, V) [n, 16, H, D];
+    same values as :func:`from_int4_pages` (works on CPU or GPU tensors)."""
     import torch
-    c = codes.to(torch.int16)
-    n, H, bs, dh = c.shape
-    vals = torch.stack(((c & 0xF) - 8, (c >> 4) - 8), dim=-1).reshape(n, H, bs, dh * 2).float()
-    s = scales.float().repeat_interleave(GROUP, dim=-1)
-    return (vals * s).half().permute(0, 2, 1, 3).contiguous()
+    n, H, _ = pages.shape
+    G = D // GROUP
+    k_off, v_off, s_idx = (torch.as_tensor(a, device=pages.device) for a in int4_page_maps(D))
+    outs = []
+    for code_base, scale_base, off in ((0, 16 * D, k_off), (8 * D, 16 * D + 32 * G, v_off)):
+        b = pages[:, :, code_base + off.reshape(-1)].reshape(n, H, PAGE_TOKENS, D // 2).to(torch.int16)
+        vals = torch.stack(((b & 0xF) - 8, (b >> 4) - 8), dim=-1).reshape(n, H, PAGE_TOKENS, D).float()
+        idx = (scale_base + 2 * s_idx).reshape(-1)
+        sb = torch.stack((pages[:, :, idx], pages[:, :, idx + 1]), dim=-1).contiguous()
+        sc = sb.view(torch.float16).reshape(n, H, PAGE_TOKENS, G).float().repeat_interleave(GROUP, dim=-1)
+        outs.append((vals * sc).half().permute(0, 2, 1, 3).contiguous())
+    return outs[0], outs[1]
 
 
-def decode_int4_torch(q, codes_k, scales_k, codes_v, scales_v, block_tables, context_lens, window, sinks):
+def decode_int4_torch(q, pages, block_tables, context_lens, window, sinks):
     """The reference's CPU path for one decode step over INT4 pages (dequantize,
     gather, sinks U window selection, fp32 SDPA, fp16 cast — the torch-only
     route of src/memopt/triton_attention.py:473-550 after
-    src/csrc/quantization.cu:232-270), vectorized per sequence. torch tensors in,
-    fp16 [B, 1, H, D] out."""
+    src/csrc/quantization.cu:232-270), vectorized per sequence. torch CPU
+    tensors in, fp16 [B, 1, H, D] out."""
     import torch
     import torch.nn.functional as F
     B, _, H, D = q.shape
-    bs = codes_k.shape[2]
     out = torch.zeros(B, 1, H, D, dtype=torch.float16)
     for b in range(B):
         ctx = int(context_lens[b])
-        pages = block_tables[b, : (ctx + bs - 1) // bs].long()
-        k = dequant_pages_torch(codes_k[pages], scales_k[pages]).reshape(-1, H, D)[:ctx]
-        v = dequant_pages_torch(codes_v[pages], scales_v[pages]).reshape(-1, H, D)[:ctx]
+        pg = block_tables[b, : (ctx + PAGE_TOKENS - 1) // PAGE_TOKENS].long()
+        k, v = dequant_pages_torch(pages[pg], D)
+        k, v = k.reshape(-1, H, D)[:ctx], v.reshape(-1, H, D)[:ctx]
         j = torch.arange(ctx)
         keep = (j >= ctx - window) | (j < sinks)
         k, v = k[keep].float().permute(1, 0, 2)[None], v[keep].float().permute(1, 0, 2)[None]

@@ -94,6 +94,8 @@ def test_fp16_paged_vs_oracle(case):
 def test_int4_paged_vs_composition_oracle(case, layout):
     """Fused INT4 attention == dequantize_kv_cache_int4 -> attention (the reference's INT4 path)."""
     B, H, D, bs, ctx, Lq, msl, W, sinks, causal, unlink = case
+    if layout == "pages" and bs != 16:
+        pytest.skip("the INT4 page pool uses 16-token pages")
     nb = B * ((max(ctx) + bs - 1) // bs) + 3
     q, kp, vp, bt, cl = _random_case(12, B, H, D, bs, nb, ctx, Lq)
     if unlink:
@@ -101,15 +103,17 @@ def test_int4_paged_vs_composition_oracle(case, layout):
     if layout == "token_major":
         kc, ks = O.quantize_int4(kp)
         vc, vs = O.quantize_int4(vp)
-        kd, vd = O.dequantize_int4(kc, ks), O.dequantize_int4(vc, vs)
+        want = O.paged_attention(q, O.dequantize_int4(kc, ks), O.dequantize_int4(vc, vs), bt, cl, msl, W,
+                                 num_sink_tokens=sinks, causal=causal)
+        got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kc), to_dev(vc), to_dev(bt), to_dev(cl), msl, W,
+                                                num_sink_tokens=sinks, causal=causal, key_scales=to_dev(ks),
+                                                value_scales=to_dev(vs), kv_layout=layout)
     else:
-        kc, ks = O.to_int4_pages(kp)
-        vc, vs = O.to_int4_pages(vp)
-        kd, vd = O.from_int4_pages(kc, ks), O.from_int4_pages(vc, vs)
-    want = O.paged_attention(q, kd, vd, bt, cl, msl, W, num_sink_tokens=sinks, causal=causal)
-    got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kc), to_dev(vc), to_dev(bt), to_dev(cl), msl, W,
-                                            num_sink_tokens=sinks, causal=causal, key_scales=to_dev(ks),
-                                            value_scales=to_dev(vs), kv_layout=layout)
+        pages = O.to_int4_pages(kp, vp)
+        want = O.paged_attention_int4(q, pages, bt, cl, msl, W, num_sink_tokens=sinks, causal=causal)
+        pg = to_dev(pages)
+        got = memopt_C.dynamic_sparse_attention(to_dev(q), pg, pg, to_dev(bt), to_dev(cl), msl, W,
+                                                num_sink_tokens=sinks, causal=causal)
     assert_close(got, want, what=f"{layout} {case}")
 
 
@@ -136,9 +140,8 @@ def test_int4_pool_via_pool_getters():
     ctx = torch.full((BATCH,), T, dtype=torch.int32, device=dev())
     got = memopt_C.dynamic_sparse_attention(to_dev(q), memopt_C.get_key_pool(), memopt_C.get_value_pool(), bt, ctx,
                                             T, T)
-    kc, vc = (t.cpu().numpy() for t in memopt_C.get_pool_tensors())
-    ks, vs = (t.cpu().numpy() for t in memopt_C.get_pool_scales())
-    want = O.paged_attention_int4(q, kc, ks, vc, vs, bt.cpu().numpy(), ctx.cpu().numpy(), T, T)
+    want = O.paged_attention_int4(q, memopt_C.get_int4_pages().cpu().numpy(), bt.cpu().numpy(),
+                                  ctx.cpu().numpy(), T, T)
     assert_close(got, want)
 
 

@@ -6,21 +6,21 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_helpers import ATOL, RTOL, assert_close, dev, memopt_C, to_dev
+from gpu_helpers import assert_close, dev, memopt_C, to_dev
 
 pytestmark = pytest.mark.gpu
 
 
-def _int4(kp, vp):
-    kc, ks = O.to_int4_pages(kp)
-    vc, vs = O.to_int4_pages(vp)
-    return kc, ks, vc, vs
+def _decode_pages(q, pages, bt, cl, msl, W, sinks=0):
+    pg = to_dev(pages)
+    return memopt_C.dynamic_sparse_attention(to_dev(q), pg, pg, to_dev(bt), to_dev(cl), msl, W,
+                                             num_sink_tokens=sinks)
 
 
-def _decode(q, kc, ks, vc, vs, bt, cl, msl, W, sinks=0, layout="pages"):
+def _decode_rows(q, kc, ks, vc, vs, bt, cl, msl, W, sinks=0):
     return memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kc), to_dev(vc), to_dev(bt), to_dev(cl), msl, W,
                                              num_sink_tokens=sinks, key_scales=to_dev(ks), value_scales=to_dev(vs),
-                                             kv_layout=layout)
+                                             kv_layout="token_major")
 
 
 def test_config1_decode():
@@ -37,12 +37,12 @@ def test_config1_decode():
     vp, vs = O.quantize_int4(v)
     want = O.paged_attention(q, O.dequantize_int4(kp, ks), O.dequantize_int4(vp, vs), bt, cl, 1024, 1024,
                              num_sink_tokens=4)
-    got = _decode(q, kp, ks, vp, vs, bt, cl, 1024, 1024, 4, layout="token_major")
+    got = _decode_rows(q, kp, ks, vp, vs, bt, cl, 1024, 1024, 4)
     assert_close(got, want, what="config1 token_major")
     # INT4 page pool (fp16 scales)
-    kc, kss, vc, vss = _int4(k, v)
-    want_p = O.paged_attention_int4(q, kc, kss, vc, vss, bt, cl, 1024, 1024, num_sink_tokens=4)
-    assert_close(_decode(q, kc, kss, vc, vss, bt, cl, 1024, 1024, 4), want_p, what="config1 pages")
+    pages = O.to_int4_pages(k, v)
+    want_p = O.paged_attention_int4(q, pages, bt, cl, 1024, 1024, num_sink_tokens=4)
+    assert_close(_decode_pages(q, pages, bt, cl, 1024, 1024, 4), want_p, what="config1 pages")
 
 
 @pytest.mark.parametrize("B,H,D,ctx,W,sinks,unlink", [
@@ -64,11 +64,17 @@ def test_decode_vs_oracle(B, H, D, ctx, W, sinks, unlink):
     for i in range(unlink):
         bt[0, rng.integers(0, M)] = -1
     cl = np.array(ctx, np.int32)
-    kc, ks, vc, vs = _int4(kp, vp)
-    want = O.paged_attention_int4(q, kc, ks, vc, vs, bt, cl, 1 << 20, W, num_sink_tokens=sinks)
-    got = _decode(q, kc, ks, vc, vs, bt, cl, 1 << 20, W, sinks)
-    assert_close(got, want)
-    assert torch.equal(got, _decode(q, kc, ks, vc, vs, bt, cl, 1 << 20, W, sinks))  # deterministic
+    pages = O.to_int4_pages(kp, vp)
+    want = O.paged_attention_int4(q, pages, bt, cl, 1 << 20, W, num_sink_tokens=sinks)
+    got = _decode_pages(q, pages, bt, cl, 1 << 20, W, sinks)
+    assert_close(got, want, what="pages")
+    assert torch.equal(got, _decode_pages(q, pages, bt, cl, 1 << 20, W, sinks))  # deterministic
+    # same inputs through the token-major (reference byte order, fp32 scales) kernel
+    kc, ks = O.quantize_int4(kp)
+    vc, vs = O.quantize_int4(vp)
+    want_r = O.paged_attention(q, O.dequantize_int4(kc, ks), O.dequantize_int4(vc, vs), bt, cl, 1 << 20, W,
+                               num_sink_tokens=sinks)
+    assert_close(_decode_rows(q, kc, ks, vc, vs, bt, cl, 1 << 20, W, sinks), want_r, what="token_major")
 
 
 # ---------------------------------------------------------------------------
@@ -76,11 +82,10 @@ def test_decode_vs_oracle(B, H, D, ctx, W, sinks, unlink):
 # dequantized by the (separately bit-exact) surface dequantize kernel.
 # ---------------------------------------------------------------------------
 
-def dequant_pages_dev(codes, scales):
-    """INT4 pages [nb, H, bs, D/2] + fp16 scales -> fp16 pool [nb, bs, H, D]."""
-    c = codes.permute(0, 2, 1, 3).contiguous()
-    s = scales.permute(0, 2, 1, 3).contiguous().float().reshape(-1)
-    return memopt_C.dequantize_kv_cache_int4(c, s, 64)
+def dequant_pages_dev(pages, D):
+    """INT4 page buffer -> fp16 pools (K, V) [nb, 16, H, D] on the GPU; equals
+    oracle.from_int4_pages (checked in tests/test_oracle.py)."""
+    return O.dequant_pages_torch(pages, D)
 
 
 def reference_decode_dev(q, kpool, vpool, bt, ctx, W, sinks):
@@ -131,15 +136,14 @@ def test_config2_full_size():
     cl = torch.full((B,), ctx, dtype=torch.int32, device=dev())
     kc, vc = memopt_C.get_pool_tensors()
     got = memopt_C.dynamic_sparse_attention(q, kc, vc, bt, cl, ctx, ctx)
-    ks, vs = memopt_C.get_pool_scales()
-    want = reference_decode_dev(q, dequant_pages_dev(kc, ks), dequant_pages_dev(vc, vs), bt, cl, ctx, 0)
+    pages = memopt_C.get_int4_pages()
+    want = reference_decode_dev(q, *dequant_pages_dev(pages, D), bt, cl, ctx, 0)
     assert_close(got, want, what="config2")
     # CPU oracle on two sequences (composition through numpy)
     for b in (0, 11):
-        pages = bt[b].cpu().numpy()
-        sub = lambda t: t[torch.as_tensor(pages).long().to(dev())].cpu().numpy()
-        w = O.paged_attention_int4(q[b:b + 1].cpu().numpy(), sub(kc), sub(ks), sub(vc), sub(vs),
-                                   np.arange(len(pages), dtype=np.int32)[None], np.array([ctx], np.int32), ctx, ctx)
+        sub = pages[bt[b].long()].cpu().numpy()
+        w = O.paged_attention_int4(q[b:b + 1].cpu().numpy(), sub, np.arange(sub.shape[0], dtype=np.int32)[None],
+                                   np.array([ctx], np.int32), ctx, ctx)
         assert_close(got[b:b + 1], w, what=f"config2 oracle b={b}")
 
 
@@ -156,7 +160,6 @@ def test_config3_evict_then_sparse_decode():
     assert torch.equal(bt == -1, (ibf[bt0.long()] == H))
     cl = torch.full((B,), ctx, dtype=torch.int32, device=dev())
     kc, vc = memopt_C.get_pool_tensors()
-    ks, vs = memopt_C.get_pool_scales()
     got = memopt_C.dynamic_sparse_attention(q, kc, vc, bt, cl, ctx, W, num_sink_tokens=sinks)
-    want = reference_decode_dev(q, dequant_pages_dev(kc, ks), dequant_pages_dev(vc, vs), bt, cl, W, sinks)
+    want = reference_decode_dev(q, *dequant_pages_dev(memopt_C.get_int4_pages(), D), bt, cl, W, sinks)
     assert_close(got, want, what="config3")

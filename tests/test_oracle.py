@@ -184,18 +184,43 @@ def test_error_bound_half_step():
     assert codes.min() >= 1 and codes.max() <= 15  # finite inputs never reach code 0
 
 
-def test_int4_pages_layout():
+def test_int4_page_maps_are_bijections():
+    for D in (64, 128, 192):
+        k_off, v_off, s_idx = O.int4_page_maps(D)
+        assert np.array_equal(np.sort(k_off.reshape(-1)), np.arange(8 * D))
+        assert np.array_equal(np.sort(v_off.reshape(-1)), np.arange(8 * D))
+        assert np.array_equal(np.sort(s_idx.reshape(-1)), np.arange(16 * (D // 64)))
+
+
+def test_int4_page_layout_examples():
+    """Hand-derived placements: lane 8p+c holds tokens (p, p+8) and dims [c*D/8, (c+1)*D/8)."""
+    k_off, v_off, s_idx = O.int4_page_maps(128)
+    # token 9 (p=1, second of the pair), dims 18/19 (c=1, r=2): K lane 9, byte 16*9 + 8 + 1
+    assert k_off[9, 9] == 16 * 9 + 8 + 1
+    # V: same dims -> unit 0 of lane 9, token-pair half 1, byte 1 of the unit
+    assert v_off[9, 9] == 16 * 9 + 0 + 2 + 1
+    # token 3, dims 126/127 (c=7, r=14): V unit 3 of lane 31, first token, second byte
+    assert v_off[3, 63] == 16 * 31 + 12 + 0 + 1
+    assert s_idx[9, 1] == 16 + 2 * 1 + 1 and s_idx[3, 0] == 6
+
+
+def test_int4_pages_round_trip():
     rng = np.random.default_rng(6)
-    pool = rng.standard_normal((3, 16, 4, 128)).astype(np.float16)
-    codes, sc = O.to_int4_pages(pool)
-    assert codes.shape == (3, 4, 16, 64) and sc.shape == (3, 4, 16, 2) and sc.dtype == np.float16
-    packed, scales = O.quantize_int4(pool)
-    # (page 2, token 5, head 3) row == codes[2, 3, 5]
-    assert np.array_equal(codes[2, 3, 5], packed[2, 5, 3])
-    assert sc[1, 2, 7, 1] == np.float16(scales.reshape(3, 16, 4, 2)[1, 7, 2, 1])
-    back = O.from_int4_pages(codes, sc)
-    ref = O.dequantize_int4(packed, scales.astype(np.float16).astype(np.float32))
-    assert np.array_equal(back.view(np.uint16), ref.view(np.uint16))
+    kp = rng.standard_normal((3, 16, 4, 128)).astype(np.float16)
+    vp = (rng.standard_normal((3, 16, 4, 128)) * 5).astype(np.float16)
+    pages = O.to_int4_pages(kp, vp)
+    assert pages.shape == (3, 4, 2176)
+    kc, ks, vc, vs = O.int4_pages_split(pages, 128)
+    pk, sk = O.quantize_int4(kp)
+    pv, sv = O.quantize_int4(vp)
+    assert np.array_equal(kc, pk) and np.array_equal(vc, pv)
+    assert np.array_equal(ks.reshape(-1), sk.astype(np.float16)) and np.array_equal(vs.reshape(-1), sv.astype(np.float16))
+    kd, vd = O.from_int4_pages(pages, 128)
+    ref = O.dequantize_int4(pk, sk.astype(np.float16).astype(np.float32))
+    assert np.array_equal(kd.view(np.uint16), ref.view(np.uint16))
+    kt, vt = O.dequant_pages_torch(torch.as_tensor(pages), 128)
+    assert np.array_equal(kt.numpy().view(np.uint16), kd.view(np.uint16))
+    assert np.array_equal(vt.numpy().view(np.uint16), vd.view(np.uint16))
 
 
 # ---------------------------------------------------------------------------
@@ -305,20 +330,26 @@ def test_sdpa_fallback_matches_sink_window_rule():
 # ---------------------------------------------------------------------------
 
 def _pools(fmt, nb, bs, H, D, rng):
+    kp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    vp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
     if fmt == "fp16":
-        return {"format": "fp16", "k": rng.standard_normal((nb, bs, H, D)).astype(np.float16),
-                "v": rng.standard_normal((nb, bs, H, D)).astype(np.float16)}
-    return {"format": "int4", "k": rng.integers(0, 256, (nb, H, bs, D // 2)).astype(np.uint8),
-            "v": rng.integers(0, 256, (nb, H, bs, D // 2)).astype(np.uint8),
-            "ks": rng.uniform(0.1, 1, (nb, H, bs, D // 64)).astype(np.float16),
-            "vs": rng.uniform(0.1, 1, (nb, H, bs, D // 64)).astype(np.float16)}
+        return {"format": "fp16", "k": kp, "v": vp}
+    return {"format": "int4", "pages": O.to_int4_pages(kp, vp), "D": D}
+
+
+def _row(pools, p, s, h):
+    """K row (token s of page p, head h) as fp16 values, any pool format."""
+    if pools["format"] == "fp16":
+        return pools["k"][p, s, h]
+    return O.from_int4_pages(pools["pages"][p:p + 1], pools["D"])[0][0, s, h]
 
 
 @pytest.mark.parametrize("fmt", ["fp16", "int4"])
 @pytest.mark.parametrize("r,sinks", [(0.5, 4), (0.75, 0), (0.1, 2), (1.0, 4)])
 def test_evict_intended_brute_force(fmt, r, sinks):
     rng = np.random.default_rng(7)
-    N, H, L, bs, D = 2, 3, 40, 4, 64
+    N, H, L, D = 2, 3, 40, 64
+    bs = 4 if fmt == "fp16" else 16
     scores = rng.lognormal(size=(N, H, L)).astype(np.float32)
     scores[0, 1, 8:12] = 1e-9  # a block fully low in one head
     pools = _pools(fmt, 24, bs, H, D, rng)
@@ -336,14 +367,9 @@ def test_evict_intended_brute_force(fmt, r, sinks):
             assert ev[n, h].tolist() == want
             for t in range(L):
                 p, s = bt0[n, t // bs], t % bs
-                if fmt == "fp16":
-                    row = pools["k"][p, s, h]
-                    assert (row == 0).all() if want[t] else np.array_equal(row, pools0["k"][p, s, h])
-                else:
-                    row = pools["k"][p, h, s]
-                    assert (row == 0x88).all() if want[t] else np.array_equal(row, pools0["k"][p, h, s])
+                row = _row(pools, p, s, h)
+                assert (row == 0).all() if want[t] else np.array_equal(row, _row(pools0, p, s, h))
     # votes: block (seq 0, logical block 2) is fully evicted only in head 1 -> 1 vote, still linked
-    assert free[bt0[0, 2]] == (1 if ev[0, 1, 8:12].all() and not ev[0, 0, 8:12].all() else free[bt0[0, 2]])
     assert ((bt == -1) == (free[np.clip(bt0, 0, None)] == H)).all()
 
 
