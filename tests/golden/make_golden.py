@@ -36,16 +36,15 @@ def main():
     kp, ks = O.quantize_int4(k)
     vp, vs = O.quantize_int4(v)
     kd, vd = O.dequantize_int4(kp, ks), O.dequantize_int4(vp, vs)
-    kc, kps = O.to_int4_pages(k)
-    vc, vps = O.to_int4_pages(v)
+    pages = O.to_int4_pages(k, v)
     out_full = O.paged_attention(q, kd, vd, bt, ctx, 64, 64, num_sink_tokens=4)
     out_win = O.paged_attention(q, kd, vd, bt, ctx, 64, 24, num_sink_tokens=4)
-    out_pages = O.paged_attention_int4(q, kc, kps, vc, vps, bt, ctx, 64, 24, num_sink_tokens=4)
+    out_pages = O.paged_attention_int4(q, pages, bt, ctx, 64, 24, num_sink_tokens=4)
     np.savez_compressed(
         os.path.join(HERE, "config1_slice.npz"),
         k=k, v=v, q=q, block_tables=bt, context_lens=ctx,
         k_packed=kp, k_scales=ks, v_packed=vp, v_scales=vs, k_deq=kd, v_deq=vd,
-        k_codes_pages=kc, k_scales_pages=kps, v_codes_pages=vc, v_scales_pages=vps,
+        int4_pages=pages,
         out_full_sinks4=out_full, out_window24_sinks4=out_win, out_pages_window24_sinks4=out_pages,
     )
     # Known-answer groups (reference tests/test_quant.py:439-566 plus rounding ties).

@@ -163,3 +163,21 @@ def test_config3_evict_then_sparse_decode():
     got = memopt_C.dynamic_sparse_attention(q, kc, vc, bt, cl, ctx, W, num_sink_tokens=sinks)
     want = reference_decode_dev(q, *dequant_pages_dev(memopt_C.get_int4_pages(), D), bt, cl, W, sinks)
     assert_close(got, want, what="config3")
+
+
+def test_config1_slice_golden_fixture():
+    """Committed fixture: INT4 pages written on device == frozen bytes, and the
+    decode output over them matches the frozen oracle output."""
+    import os
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config1_slice.npz"))
+    nb, bs, H, D = f["k"].shape
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    slots = np.arange(nb * bs, dtype=np.int32)
+    rows = lambda a: to_dev(a.reshape(nb * bs, H, D))
+    memopt_C.write_cache(rows(f["k"]), rows(f["v"]), to_dev(np.zeros((1, 1), np.int32)), to_dev(slots))
+    got_pages = memopt_C.get_int4_pages().cpu().numpy()
+    assert np.array_equal(got_pages, f["int4_pages"])
+    kc, vc = memopt_C.get_pool_tensors()
+    out = memopt_C.dynamic_sparse_attention(to_dev(f["q"]), kc, vc, to_dev(f["block_tables"]),
+                                            to_dev(f["context_lens"]), 64, 24, num_sink_tokens=4)
+    assert_close(out, f["out_pages_window24_sinks4"], what="config1 slice fixture")

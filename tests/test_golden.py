@@ -20,9 +20,7 @@ def test_config1_slice_fixture():
     f = np.load(os.path.join(HERE, "config1_slice.npz"))
     kp, ks = O.quantize_int4(f["k"])
     assert np.array_equal(kp, f["k_packed"]) and np.array_equal(ks.view(np.uint32), f["k_scales"].view(np.uint32))
-    kc, kps = O.to_int4_pages(f["k"])
-    assert np.array_equal(kc, f["k_codes_pages"]) and np.array_equal(kps.view(np.uint16),
-                                                                       f["k_scales_pages"].view(np.uint16))
+    assert np.array_equal(O.to_int4_pages(f["k"], f["v"]), f["int4_pages"])
     out = O.paged_attention(f["q"], f["k_deq"], f["v_deq"], f["block_tables"], f["context_lens"], 64, 24,
                             num_sink_tokens=4)
     assert np.array_equal(out.view(np.uint16), f["out_window24_sinks4"].view(np.uint16))
