@@ -53,9 +53,12 @@ __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cas
 
 // DPP lane exchange inside quads / rows of 16 (no LDS traffic).
 // quad_perm xor-1 = [1,0,3,2] (0xB1), xor-2 = [2,3,0,1] (0x4E).
+// All source lanes of the patterns used here are active, so bound_ctrl is
+// irrelevant to the result; setting it lets the compiler fold the move into
+// the consuming VALU op as a DPP source modifier.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float xor1(float v) { return dpp_f32<0xB1>(v); }
 __device__ __forceinline__ float xor2(float v) { return dpp_f32<0x4E>(v); }
@@ -73,6 +76,17 @@ __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
   uint32_t r;
   asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
   return r;
+}
+
+// A wave-uniform pointer rebuilt from readfirstlane'd halves: the compiler
+// keeps it in SGPRs, so `p + lane_offset` becomes a scalar-base load with a
+// 32-bit VGPR offset instead of 64-bit per-lane address arithmetic.
+template <typename T>
+__device__ __forceinline__ const T *uniform_ptr(const T *p) {
+  const uint64_t a = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return (const T *)(((uint64_t)hi << 32) | lo);
 }
 
 // Wave64 max all-reduce: DPP inside rows of 16, LDS crossbar across rows.

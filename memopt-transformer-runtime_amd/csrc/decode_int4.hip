@@ -15,8 +15,10 @@
 //    exponent pattern (0x6400 -> 1024 + n for bits 0-3, 0x5400 -> 64 + n for
 //    bits 4-7) and feed v_dot2_f32_f16 directly; the constant bias sum
 //    q . (bias + 8) is subtracted once per token, which leaves q . (code - 8);
-//  * V nibbles are unpacked exactly to (code - 8) in fp16 and accumulated in
-//    fp32 with v_fma_mix_f32 against the softmax weight times the V scale;
+//  * V nibbles are unpacked the same way; the row-layout kernel subtracts the
+//    bias per element (exact fp16 code - 8) and accumulates with v_fma_mix_f32,
+//    the page-layout kernel accumulates bias + code with v_dot2_f32_f16 over a
+//    token pair and removes bias * (sum of weights) once at the end;
 //  * the softmax running max is wave-uniform and lazily raised: it is updated
 //    (with a wave max and a rescale of the accumulators) only when some score
 //    exceeds it by more than 8 in log2 units, so the common page costs no
@@ -36,6 +38,16 @@ __device__ __forceinline__ float load_scale(const void *p, int64_t i) {
   return (float)reinterpret_cast<const ST *>(p)[i];
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Raw buffer descriptor over one (page, head) block: scalar base, 32-bit
+// per-lane byte offsets (buffer_load ... offen), no per-lane 64-bit math.
+// dword3 0x00020000 = 32-bit data format, the untyped raw-buffer setting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const uint8_t *blk) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)blk, (short)0, 0x7FFFFFFF, 0x00020000);
+}
+
 template <int D>
 struct LaneChunk;
 template <>
@@ -43,6 +55,10 @@ struct LaneChunk<128> {
   uint4 w;
   static constexpr int kWords = 4;
   __device__ __forceinline__ void load(const uint8_t *p) { w = *reinterpret_cast<const uint4 *>(p); }
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    w = make_uint4(v.x, v.y, v.z, v.w);
+  }
   __device__ __forceinline__ uint32_t word(int i) const {
     return i == 0 ? w.x : (i == 1 ? w.y : (i == 2 ? w.z : w.w));
   }
@@ -52,6 +68,10 @@ struct LaneChunk<64> {
   uint2 w;
   static constexpr int kWords = 2;
   __device__ __forceinline__ void load(const uint8_t *p) { w = *reinterpret_cast<const uint2 *>(p); }
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    w = make_uint2(v.x, v.y);
+  }
   __device__ __forceinline__ uint32_t word(int i) const { return i == 0 ? w.x : w.y; }
 };
 
@@ -301,58 +321,80 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
     }
   }
 
-  float m = -INFINITY, l = 0.0f;
+  // acc accumulates weight * (bias + code) with the bias of unpack_biased
+  // (1024 for dims 4u, 4u+2; 64 for dims 4u+1, 4u+3); wsum = sum of the fp16
+  // weights actually used, so the bias is removed exactly once at the end.
+  float m = -INFINITY, l = 0.0f, wsum = 0.0f;
+  const half2_t kOnes = {(half_t)1.0f, (half_t)1.0f};
   float acc[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
 
   const int32_t *btrow = p.bt + (int64_t)b * p.M;
-  const uint8_t *kbase = p.kc + (int64_t)h * p.kv_hs + lane * BPL;
-  const uint8_t *vbase = p.vc + (int64_t)h * p.kv_hs + lane * BPL;
-  const half_t *ksb = (const half_t *)p.ks + (int64_t)h * p.sc_hs + g * 16 + 2 * pp;
-  const half_t *vsb = (const half_t *)p.vs + (int64_t)h * p.sc_hs + g * 16 + 2 * pp;
+  // Uniform (scalar) block base per page + 32-bit per-lane byte offsets.
+  const uint8_t *hbase = p.kc + (int64_t)h * p.kv_hs;
+  const uint32_t koff = lane * BPL;
+  const uint32_t voff = (uint32_t)(p.vc - p.kc) + lane * BPL;
+  const uint32_t ksoff = (uint32_t)((const uint8_t *)p.ks - p.kc) + 2 * (g * 16 + 2 * pp);
+  const uint32_t vsoff = (uint32_t)((const uint8_t *)p.vs - p.kc) + 2 * (g * 16 + 2 * pp);
+  const int32_t nb32 = (int32_t)min(p.nb, (int64_t)INT32_MAX);
 
-  for (int32_t base = begin + wave * U; base < end; base += NW * U) {
-    int32_t lp[U];
-    bool ok[U];
+  // Page batches of U pages are double-buffered: the loads of batch n+1 are
+  // in flight while batch n is consumed. Slots past `end` (and unlinked
+  // pages) load page 0 of this head, which is always mapped and L2-resident
+  // after the first touch, and are masked out.
+  struct Batch {
     Chunk kw[U], vw[U];
     half2_t sk[U], sv[U];
+    int32_t lp[U];
+    bool ok[U];
+  };
+  auto issue = [&](Batch &bt, int32_t base) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int32_t i = base + u;
-      lp[u] = (i < sink_pages) ? i : win_page0 + (i - sink_pages);
-      const int32_t phys = btrow[(i < end) ? lp[u] : 0];  // lp < M whenever i < end
-      ok[u] = (i < end) && phys >= 0 && phys < p.nb;
-      const int64_t pg = ok[u] ? (int64_t)phys : 0;     // invalid: page 0, masked below
-      kw[u].load(kbase + pg * p.kv_ps);
-      vw[u].load(vbase + pg * p.kv_ps);
-      sk[u] = *reinterpret_cast<const half2_t *>(ksb + pg * p.sc_ps);
-      sv[u] = *reinterpret_cast<const half2_t *>(vsb + pg * p.sc_ps);
+      bt.lp[u] = (i < sink_pages) ? i : win_page0 + (i - sink_pages);
+      const int32_t phys = btrow[(i < end) ? bt.lp[u] : 0];  // lp < M whenever i < end
+      bt.ok[u] = (i < end) && phys >= 0 && phys < nb32;
+      const int64_t pg = bt.ok[u] ? (int64_t)phys : 0;
+      const __amdgpu_buffer_rsrc_t r = block_rsrc(uniform_ptr(hbase + pg * p.kv_ps));
+      bt.kw[u].load(r, koff);
+      bt.vw[u].load(r, voff);
+      bt.sk[u] = as_half2(__builtin_amdgcn_raw_buffer_load_b32(r, (int)ksoff, 0, 0));
+      bt.sv[u] = as_half2(__builtin_amdgcn_raw_buffer_load_b32(r, (int)vsoff, 0, 0));
     }
+  };
+  auto consume = [&](const Batch &bt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float d0 = -bias, d1 = -bias;
 #pragma unroll
       for (int k = 0; k < KW; ++k) {
         uint32_t r0[4], r1[4];
-        unpack_biased(kw[u].word(k), r0);
-        unpack_biased(kw[u].word(KW + k), r1);
+        unpack_biased(bt.kw[u].word(k), r0);
+        unpack_biased(bt.kw[u].word(KW + k), r1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           d0 = __builtin_amdgcn_fdot2(as_half2(r0[j]), qp[k][j], d0, false);
           d1 = __builtin_amdgcn_fdot2(as_half2(r1[j]), qp[k][j], d1, false);
         }
       }
-      float s0 = d0 * (float)sk[u].x, s1 = d1 * (float)sk[u].y;
+      float s0 = d0 * (float)bt.sk[u].x, s1 = d1 * (float)bt.sk[u].y;
       s0 += xor1(s0);
       s1 += xor1(s1);
       s0 += xor2(s0);
       s1 += xor2(s1);
       s0 += half_mirror(s0);
       s1 += half_mirror(s1);
-      const int32_t t0 = lp[u] * 16 + pp, t1 = t0 + 8;
-      const bool v0 = ok[u] && t0 < kr.hi && (t0 >= kr.win_lo || t0 < kr.sink_end);
-      const bool v1 = ok[u] && t1 < kr.hi && (t1 >= kr.win_lo || t1 < kr.sink_end);
+      // Whole page inside the window (the common case): no per-token mask.
+      const int32_t tok0 = bt.lp[u] * 16;
+      const bool full = bt.ok[u] && tok0 >= kr.win_lo && tok0 + 16 <= kr.hi;
+      bool v0 = full, v1 = full;
+      if (!full) {  // wave-uniform
+        const int32_t t0 = tok0 + pp, t1 = t0 + 8;
+        v0 = bt.ok[u] && t0 < kr.hi && (t0 >= kr.win_lo || t0 < kr.sink_end);
+        v1 = bt.ok[u] && t1 < kr.hi && (t1 >= kr.win_lo || t1 < kr.sink_end);
+      }
       s0 = v0 ? s0 * p.qk_scale_log2 : -INFINITY;
       s1 = v1 ? s1 * p.qk_scale_log2 : -INFINITY;
       const float smax = fmaxf(s0, s1);
@@ -360,6 +402,7 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
         const float mn = fmaxf(m, wave_max(smax));
         const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
         l *= alpha;
+        wsum *= alpha;
 #pragma unroll
         for (int d = 0; d < DPL; ++d) acc[d] *= alpha;
         m = mn;
@@ -367,17 +410,37 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
       const float p0 = v0 ? fast_exp2(s0 - m) : 0.0f;
       const float p1 = v1 ? fast_exp2(s1 - m) : 0.0f;
       l += p0 + p1;
-      const half2_t wpair = {(half_t)(p0 * (float)sv[u].x), (half_t)(p1 * (float)sv[u].y)};
+      const half2_t wpair = {(half_t)(p0 * (float)bt.sv[u].x), (half_t)(p1 * (float)bt.sv[u].y)};
+      wsum = __builtin_amdgcn_fdot2(wpair, kOnes, wsum, false);
 #pragma unroll
       for (int k = 0; k < VW; ++k) {
-        half2_t hv[4];
-        unpack_exact(vw[u].word(k), hv);
+        uint32_t r[4];
+        unpack_biased(bt.vw[u].word(k), r);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[4 * k + j] = __builtin_amdgcn_fdot2(hv[j], wpair, acc[4 * k + j], false);
+        for (int j = 0; j < 4; ++j)
+          acc[4 * k + j] = __builtin_amdgcn_fdot2(as_half2(r[j]), wpair, acc[4 * k + j], false);
       }
     }
+  };
+
+  constexpr int32_t kStep = NW * U;
+  Batch ba, bb;
+  int32_t base = begin + wave * U;
+  issue(ba, base);
+  while (base < end) {
+    issue(bb, base + kStep);
+    consume(ba);
+    base += kStep;
+    if (base >= end) break;
+    issue(ba, base + kStep);
+    consume(bb);
+    base += kStep;
   }
 
+  // Remove the code bias: slot 4u+j of a V word holds dim 4u+j, biased by
+  // 1032 (j even) or 72 (j odd), i.e. (bias + 8) with the -8 code offset.
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) acc[d] = fmaf(-((d & 1) ? 72.0f : 1032.0f), wsum, acc[d]);
   // Sum the 8 token-pair lanes sharing this lane's dims (lanes c, c+8, ...).
   l += dpp_f32<0x128>(l);  // row_ror:8
   l += shfl_xor(l, 16);
@@ -456,16 +519,16 @@ static int device_cus() {
   return cus;
 }
 
-// Launch shape (waves per workgroup, pages in flight per wave). The default
-// is (8, 2); MEMOPT_DECODE_SHAPE="NW,U" selects another compiled shape for
-// tuning sweeps.
+// Launch shape (waves per workgroup, pages per double-buffered batch). The
+// default (4, 2) measured fastest on MI355X for 16 x 32 heads x 4096 tokens;
+// MEMOPT_DECODE_SHAPE="NW,U" selects another compiled shape for tuning sweeps.
 struct DecodeShape {
   int nw, u;
 };
 static DecodeShape decode_shape() {
   static DecodeShape s = {0, 0};
   if (s.nw == 0) {
-    s = {8, 2};
+    s = {4, 2};
     if (const char *e = std::getenv("MEMOPT_DECODE_SHAPE")) {
       int a = 0, c = 0;
       if (std::sscanf(e, "%d,%d", &a, &c) == 2 &&
@@ -505,10 +568,10 @@ static void launch_shape(const DecodeParams &p, dim3 grid, DecodeShape sh, hipSt
       hipLaunchKernelGGL((decode_int4_kernel<D, ST, NW_, U_>), grid, dim3(NW_ * 64), 0, stream, p);  \
     return;                                                                                           \
   }
+  MEMOPT_DECODE_CASE(4, 2)
   MEMOPT_DECODE_CASE(8, 2)
   MEMOPT_DECODE_CASE(8, 1)
   MEMOPT_DECODE_CASE(8, 4)
-  MEMOPT_DECODE_CASE(4, 2)
   MEMOPT_DECODE_CASE(4, 4)
   MEMOPT_DECODE_CASE(16, 2)
 #undef MEMOPT_DECODE_CASE
