@@ -261,6 +261,8 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
     return launch_decode_int4(p, d.batch, d.head_dim, d.kv_format == MEMOPT_KV_INT4 ? MEMOPT_SCALE_F16 : d.scale_dtype, s);
   }
 
+  if (prefill_supported(d)) return launch_prefill(d, W, scale * 1.4426950408889634f, s);
+
   GenericParams g;
   g.q = (const half_t *)d.query;
   g.out = (half_t *)d.out;

@@ -51,4 +51,9 @@ int decode_splits(int32_t batch, int32_t heads, int32_t max_pages_visited);
 int launch_decode_int4(const DecodeParams &p, int32_t batch, int32_t D, int32_t scale_dtype,
                        hipStream_t stream);
 
+// Multi-query (q_len >= 16) MFMA kernel over INT4 page pools or contiguous
+// fp16 pools with 16-multiple pages and D in {64, 128}.
+bool prefill_supported(const memopt_attn_desc &d);
+int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hipStream_t stream);
+
 }  // namespace memopt
