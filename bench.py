@@ -81,12 +81,12 @@ def setup_decode(torch, memopt_C, cfg, copies=2):
 
 
 def time_steps(torch, fn_list, steps, warmup):
-    """Returns (ms per step, mean per-launch ms, host wall ms per step).
+    """Returns (ms per step, host wall ms per step).
 
-    Pass 1 times `steps` back-to-back steps between two events (the step
-    rate). Pass 2 brackets each launch with its own event pair on the same
-    stream (the kernel duration for the roofline); it is a separate pass
-    because events between launches add gaps to the step rate.
+    `steps` launches run back to back on the current stream between two HIP
+    events recorded on that stream, so the per-step time is the kernel's
+    average duration (plus sub-microsecond dispatch gaps); it matches the
+    AverageNs of `rocprofv3 --kernel-trace --stats` over the same command.
     """
     stream = torch.cuda.current_stream()
     for i in range(warmup):
@@ -101,16 +101,7 @@ def time_steps(torch, fn_list, steps, warmup):
     t_end.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    region_ms = t_start.elapsed_time(t_end) / steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for i in range(steps):
-        starts[i].record(stream)
-        fn_list[i % len(fn_list)]()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    launch_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
-    return region_ms, launch_ms, wall_ms
+    return t_start.elapsed_time(t_end) / steps, wall_ms
 
 
 def cpu_baseline_decode(torch, O, memopt_C, tables, q, cl, cfg, budget_s=15.0):
@@ -150,13 +141,57 @@ def bench_kv_quant(torch, memopt_C, cfg, steps=20):
     v = torch.randn(T, H, D, device=dev, generator=g).half()
     slots = torch.arange(T, dtype=torch.int32, device=dev)
     bt = torch.zeros(1, 1, dtype=torch.int32, device=dev)
-    region_ms, launch_ms, _ = time_steps(torch, [lambda: memopt_C.write_cache(k, v, bt, slots, validate_slots=False)], steps, 3)
+    launch_ms, _ = time_steps(torch, [lambda: memopt_C.write_cache(k, v, bt, slots, validate_slots=False)], steps, 3)
     elems = 2 * T * H * D
     nbytes = elems * 2.53125
     return {"workload": "write_cache fused quantize, 2 x [16384, 32, 128] fp16 -> INT4 pages",
             "GB/s": round(nbytes / (launch_ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "bytes_per_elem": 2.53125}
+
+
+CFG4 = dict(batch=1, seq=16384, heads=32, head_dim=128, window=4096, sinks=4, block=16, std=0.5, seed=4)
+
+
+def prefill_flops(seq, heads, head_dim, window, sinks):
+    """4*D*H per (query, visible key) pair: QK^T and PV, 2 flops per MAC, causal
+    StreamingLLM mask (key <= pos and (key < sinks or key > pos - window))."""
+    total = 0
+    for pos in range(seq):
+        vis = min(pos + 1, window) + min(sinks, max(pos - window + 1, 0))
+        total += vis
+    return 4 * head_dim * heads * total
+
+
+def bench_prefill(torch, memopt_C, cfg, steps=10, warmup=3):
+    """Config 4: write_cache of 16384 tokens into INT4 pages, then causal paged
+    attention (window 4096, 4 sinks) for all 16384 queries on the MFMA path."""
+    S, H, D, bs = cfg["seq"], cfg["heads"], cfg["head_dim"], cfg["block"]
+    dev = torch.device("cuda", 0)
+    nb = S // bs
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(cfg["seed"])).to(torch.int32)
+    bt = perm[None].to(dev)
+    slots = (bt.long()[0, :, None] * bs + torch.arange(bs, device=dev)).reshape(-1).to(torch.int32)
+    g = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    k = (torch.randn(S, H, D, device=dev, generator=g) * cfg["std"]).half()
+    v = (torch.randn(S, H, D, device=dev, generator=g) * cfg["std"]).half()
+    q = (torch.randn(1, S, H, D, device=dev, generator=g) * cfg["std"]).half()
+    ctx = torch.tensor([S], dtype=torch.int32, device=dev)
+    write_ms, _ = time_steps(torch, [lambda: memopt_C.write_cache(k, v, bt, slots, validate_slots=False)], steps,
+                             warmup)
+    kc, vc = memopt_C.get_key_pool(), memopt_C.get_value_pool()
+    call = memopt_C.PreparedAttention(q, kc, vc, bt, ctx, S, cfg["window"], num_sink_tokens=cfg["sinks"],
+                                      causal=True)
+    launch_ms, _ = time_steps(torch, [call], steps, warmup)
+    flops = prefill_flops(S, H, D, cfg["window"], cfg["sinks"])
+    tflops = flops / (launch_ms * 1e-3) / 1e12
+    return {"workload": "BASELINE configs[3]: B 1, seq 16384, 32 heads, head_dim 128, INT4 16-token pages, "
+                        "causal window 4096 + 4 sinks, all 16384 queries",
+            "kernel": "prefill_kernel<128, true, 4, 1>", "kernel_ms": round(launch_ms, 4),
+            "flops": flops, "TFLOP/s": round(tflops, 1), "peak_TFLOP/s": MFMA_F16_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "write_cache_ms": round(write_ms, 4)}
 
 
 def main():
@@ -166,6 +201,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip secondary figures")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 5 plain 512 MiB device-to-device copies (scales rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the path is single-GPU; multi-GPU sharding is "
@@ -173,14 +210,23 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        n = 512 << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "launches": 5}))
+        return
     import memopt_C  # noqa: E402  (fails loudly if the HIP library is missing)
 
     cfg = CFG2
     calls, tables, q, cl = setup_decode(torch, memopt_C, cfg)
-    region_ms, launch_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup)
+    region_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup)
     nbytes = effective_kv_bytes(cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"])
     value = nbytes / (region_ms * 1e-3) / 1e9
-    achieved = nbytes / (launch_ms * 1e-3) / 1e9
+    achieved = value  # one decode launch per step
     line = {
         "metric": "INT4 paged decode-attn HBM GB/s (% peak); prefill MFMA util; KV-quant GB/s",
         "value": round(value, 1),
@@ -201,14 +247,15 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profile_traffic("decode_int4_config2_pmc.txt"),
-                     "kernel": "decode_int4_pages_kernel<128, 4, 2>", "kernel_ms": round(launch_ms, 5)},
+                     "kernel": "decode_int4_pages_kernel<128, 4, 2>", "kernel_ms": round(region_ms, 5)},
     }
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as O  # CPU baseline leg only
         line["cpu_baseline"] = cpu_baseline_decode(torch, O, memopt_C, tables, q, cl, cfg)
-    if not args.no_secondary:  # overwrites pool pages: runs last
-        line["secondary"] = {"kv_quant": bench_kv_quant(torch, memopt_C, cfg)}
+    if not args.no_secondary:  # re-initializes the pool: runs last
+        line["secondary"] = {"prefill": bench_prefill(torch, memopt_C, CFG4),
+                             "kv_quant": bench_kv_quant(torch, memopt_C, cfg)}
     print(json.dumps(line), flush=True)
 
 

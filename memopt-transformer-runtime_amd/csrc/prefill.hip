@@ -34,6 +34,7 @@ namespace memopt {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 static constexpr int kTileKeys = 64;
 
@@ -65,6 +66,12 @@ __device__ __forceinline__ int32_t vt_col(int32_t R) {
   return 32 * b + 16 * (g >> 1) + 8 * h + 4 * (g & 1) + q;
 }
 
+// Byte offset of V^T column byte `cb` in row d. 32-byte column blocks are
+// XOR-swizzled by bits 4-5 of the row so the staging writes (16 rows per
+// thread, 8 threads per row group) spread over the LDS banks; 16 consecutive
+// rows share one swizzle, which keeps the MFMA operand reads conflict-free.
+__device__ __forceinline__ int vt_swz(int cb, int d) { return cb ^ (32 * ((d >> 4) & 3)); }
+
 __device__ __forceinline__ bool key_visible(int32_t key, int32_t qpos, int32_t ctx, int32_t W, int32_t sinks,
                                             bool causal) {
   if (key >= ctx) return false;
@@ -72,54 +79,109 @@ __device__ __forceinline__ bool key_visible(int32_t key, int32_t qpos, int32_t c
   return key >= ctx - W || key < sinks;
 }
 
-template <int D, bool INT4, int NW>
-__global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p) {
+// One staging task per thread: (16-key chunk k, token pair pp, dim slice c)
+// of a 64-key tile; the registers below carry its raw data from the global
+// load (issued one tile ahead) to the LDS write.
+template <int D, bool INT4>
+struct Staged {
+  static constexpr int DPT = D / 8;  // dims per task
+  int32_t pg;
+  // INT4: K codes of tokens pp and pp+8 (DPT/8 words each), V codes (DPT/4
+  // words, each 4 dims x both tokens), scales (token pp, token pp+8).
+  // fp16: K and V rows of both tokens (DPT/8 16-byte vectors each).
+  uint32_t kw[INT4 ? DPT / 4 : 1], vw[INT4 ? DPT / 4 : 1];
+  uint32_t sk, sv;
+  u32x4 kr[INT4 ? 1 : 2 * (DPT / 8)], vr[INT4 ? 1 : 2 * (DPT / 8)];
+};
+
+// Value of lane l ^ 32 combined with lane l's: both halves of the pair.
+__device__ __forceinline__ float half_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D, bool INT4, int NW, int QB>
+__global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const PrefillParams p) {
+  static_assert(NW == 4, "one staging task per thread");
+  constexpr int QW = 32 * QB;               // queries per wave
   constexpr int KSTR = D * 2 + 16;          // K row stride in LDS (bytes), padded
   constexpr int VSTR = kTileKeys * 2 + 16;  // V^T row stride (bytes), padded
+  constexpr int KBUF = kTileKeys * KSTR, VBUF = D * VSTR;
   constexpr int NCH = D / 16;               // 16-dim chunks of the QK contraction
   constexpr int NDB = D / 32;               // 32-dim output blocks
   constexpr int DPT = D / 8;                // dims per staging task
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k[kTileKeys * KSTR];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_v[D * VSTR];
-  __shared__ int32_t s_pages[4];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k[2 * KBUF];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_v[2 * VBUF];
+  __shared__ int32_t s_pg[2][4];
 
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int32_t h = blockIdx.y, b = blockIdx.z;
+  // Workgroup -> (query tile, head, batch). Workgroups are dealt to the 8
+  // XCDs round-robin by linear id; the remap gives each XCD a contiguous
+  // range of (batch, head) so the window of a head is read into one L2, and
+  // walks query tiles last-first (the longest causal tiles start first).
+  const int32_t nqt = (p.Lq + QW * NW - 1) / (QW * NW);
+  int32_t wg = blockIdx.x;
+  const int32_t n8 = (int32_t)(gridDim.x & ~7u);
+  if (wg < n8) wg = (wg & 7) * (n8 >> 3) + (wg >> 3);
+  const int32_t qt = nqt - 1 - wg % nqt;
+  const int32_t h = (wg / nqt) % p.H, b = wg / (nqt * p.H);
   const int32_t ctx = p.ctx[b];
   const int32_t kv_lim = min(ctx, p.M * p.bs);
-  const int32_t q0 = blockIdx.x * 32 * NW;
-  const int32_t qw0 = q0 + 32 * wave;
-  const int32_t qi = qw0 + (lane & 31);
-  const bool q_ok = qi < p.Lq;
-  const int32_t qpos = ctx - p.Lq + qi;
+  const int32_t q0 = qt * QW * NW;
+  const int32_t qw0 = q0 + QW * wave;
   const bool causal = p.causal != 0;
-
-  // ---- Q fragments: chunk c, lane half hl -> 8 dims (INT4: unpack order) ----
-  half8_t qf[NCH];
+  const float cs = p.qk_scale_log2;
+  // lane column (lane & 31) of query block qb = query qw0 + 32 qb + (lane & 31)
+  bool q_ok[QB];
+  int32_t qpos[QB];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    half8_t v = {};
-    if (q_ok) {
-      const uint4 u = *reinterpret_cast<const uint4 *>(p.q + (((int64_t)b * p.Lq + qi) * p.H + h) * D + 16 * c + 8 * hl);
-      const half8_t n = __builtin_bit_cast(half8_t, u);
-      if (INT4) {
-        v[0] = n[0]; v[1] = n[4]; v[2] = n[1]; v[3] = n[5];
-        v[4] = n[2]; v[5] = n[6]; v[6] = n[3]; v[7] = n[7];
-      } else {
-        v = n;
-      }
-    }
-    qf[c] = v;
+  for (int qb = 0; qb < QB; ++qb) {
+    const int32_t qi = qw0 + 32 * qb + (lane & 31);
+    q_ok[qb] = qi < p.Lq;
+    qpos[qb] = ctx - p.Lq + qi;
   }
 
-  float16_t o[NDB];
+  // ---- Q fragments: chunk c, lane half hl -> 8 dims (INT4: unpack order) ----
+  half8_t qf[QB][NCH];
 #pragma unroll
-  for (int i = 0; i < NDB; ++i) o[i] = (float16_t){};
-  float m = -INFINITY, lsum = 0.0f;
+  for (int qb = 0; qb < QB; ++qb) {
+    const int32_t qi = qw0 + 32 * qb + (lane & 31);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      half8_t v = {};
+      if (q_ok[qb]) {
+        const uint4 u =
+            *reinterpret_cast<const uint4 *>(p.q + (((int64_t)b * p.Lq + qi) * p.H + h) * D + 16 * c + 8 * hl);
+        const half8_t n = __builtin_bit_cast(half8_t, u);
+        if (INT4) {
+          v[0] = n[0]; v[1] = n[4]; v[2] = n[1]; v[3] = n[5];
+          v[4] = n[2]; v[5] = n[6]; v[6] = n[3]; v[7] = n[7];
+        } else {
+          v = n;
+        }
+      }
+      qf[qb][c] = v;
+    }
+  }
 
-  // ---- key tiles visited by this workgroup ----
-  const int32_t qlast = min(q0 + 32 * NW, p.Lq) - 1;
+  float16_t o[QB][NDB];
+  float m[QB], negm[QB], lsum[QB];  // m: running max of scaled scores
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) o[qb][i] = (float16_t){};
+    m[qb] = -INFINITY;
+    negm[qb] = 0.0f;
+    lsum[qb] = 0.0f;
+  }
+
+  // ---- key tiles visited by this workgroup: sink tiles, then window tiles ----
+  const int32_t qlast = min(q0 + QW * NW, p.Lq) - 1;
   const int32_t pos_lo = ctx - p.Lq + q0, pos_hi = ctx - p.Lq + qlast;
   const int32_t hi = max(0, causal ? min(kv_lim, pos_hi + 1) : kv_lim);
   const int32_t win_lo = max(0, causal ? pos_lo - p.W + 1 : ctx - p.W);
@@ -128,200 +190,270 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p)
   const int32_t t_first = max(win_lo / kTileKeys, sink_tiles);
   const int32_t t_last = (hi + kTileKeys - 1) / kTileKeys;  // exclusive
   const int32_t n_tiles = sink_tiles + max(0, t_last - t_first);
-  // wave-level query span (for skipping and the unmasked fast path)
-  const int32_t wq_last = min(qw0 + 31, p.Lq - 1);
+  auto tile_base = [&](int32_t it) { return (it < sink_tiles ? it : t_first + (it - sink_tiles)) * kTileKeys; };
+  // wave-level query span (tile skipping and the unmasked fast path)
+  const int32_t wq_last = min(qw0 + QW - 1, p.Lq - 1);
   const int32_t wpos_lo = ctx - p.Lq + qw0, wpos_hi = ctx - p.Lq + wq_last;
 
-  for (int32_t it = 0; it < n_tiles; ++it) {
-    const int32_t tile = it < sink_tiles ? it : t_first + (it - sink_tiles);
-    const int32_t tb = tile * kTileKeys;
+  // ---- staging task of this thread ----
+  const int sk_k = tid >> 6, sk_pp = (tid >> 3) & 7, sk_c = tid & 7;
+  const int sk_R0 = 16 * sk_k + 2 * sk_pp;  // K rows of tokens pp (R0) and pp+8 (R0+1)
+  const int sk_vc0 = vt_col(sk_R0);         // V^T column of token pp; pp+8 is +1
+  Staged<D, INT4> st;
 
-    __syncthreads();  // previous tile's LDS reads are done
-    if (tid < 4) {
-      const int32_t key = tb + 16 * tid;
-      int32_t pg = -1;
+  // Page of this thread's 16-key chunk in tile `it` (-1: none / unlinked).
+  // Looked up one tile before its data is loaded, so the dependent loads
+  // never wait on the block-table read.
+  auto lookup = [&](int32_t it) __attribute__((always_inline)) {
+    int32_t pg = -1;
+    if (it < n_tiles) {
+      const int32_t key = tile_base(it) + 16 * sk_k;
       if (key < kv_lim) {
         const int32_t e = p.bt[(int64_t)b * p.M + key / p.bs];
         pg = (e >= 0 && e < p.nb) ? e : -1;
       }
-      s_pages[tid] = pg;
     }
-    __syncthreads();
+    return pg;
+  };
 
-    // ---- stage the tile: task = (16-key chunk k, pair pp, dim slice c) ----
-    for (int task = tid; task < 256; task += NW * 64) {
-      const int k = task >> 6, pp = (task >> 3) & 7, c = task & 7;
-      const int32_t pg = s_pages[k];
-      const int R0 = 16 * k + 2 * pp;  // rows of tokens pp and pp+8 of the chunk
-      uint8_t *krow0 = lds_k + R0 * KSTR + c * DPT * 2;
-      uint8_t *krow1 = krow0 + KSTR;
-      const int vc0 = vt_col(R0);       // V^T column of token pp; pp+8 is vc0 + 1
-      if (pg < 0) {
-        for (int i = 0; i < DPT / 8; ++i) {
-          *reinterpret_cast<uint4 *>(krow0 + 16 * i) = make_uint4(0, 0, 0, 0);
-          *reinterpret_cast<uint4 *>(krow1 + 16 * i) = make_uint4(0, 0, 0, 0);
-        }
-        for (int d = 0; d < DPT; ++d) *reinterpret_cast<uint32_t *>(lds_v + (c * DPT + d) * VSTR + vc0 * 2) = 0;
-        continue;
-      }
-      if (INT4) {
-        const Int4Page f(D);
-        const uint8_t *blk = p.pool + ((int64_t)pg * p.H + h) * f.block;
-        const int slot = 8 * pp + c;
-        const int g = (c * DPT) / 64;
-        const half2_t sk = *reinterpret_cast<const half2_t *>(blk + f.kscales + 2 * (g * 16 + 2 * pp));
-        const half2_t sv = *reinterpret_cast<const half2_t *>(blk + f.vscales + 2 * (g * 16 + 2 * pp));
-        const half2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f};
-        const half2_t b72 = {(half_t)72.0f, (half_t)72.0f};
-        // K: token pp = first BPL/2 bytes, token pp+8 = next BPL/2 (DPT/8 words each)
-        const uint32_t *kw = reinterpret_cast<const uint32_t *>(blk + f.kcodes + slot * f.BPL);
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const half2_t s2 = t2 ? half2_t{sk.y, sk.y} : half2_t{sk.x, sk.x};
-          uint8_t *dst = t2 ? krow1 : krow0;
-#pragma unroll
-          for (int wi = 0; wi < DPT / 8; ++wi) {
-            const uint32_t w = kw[t2 * (DPT / 8) + wi], w8 = w >> 8;
-            const half2_t h0 = (as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * s2;
-            const half2_t h1 = (as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * s2;
-            const half2_t h2 = (as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * s2;
-            const half2_t h3 = (as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * s2;
-            *reinterpret_cast<uint4 *>(dst + 16 * wi) = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
-          }
-        }
-        // V: DPT/4 words, each = 4 dims x tokens (pp, pp+8)
-        const uint32_t *vw = reinterpret_cast<const uint32_t *>(blk + f.vcodes + slot * f.BPL);
-#pragma unroll
-        for (int wi = 0; wi < DPT / 4; ++wi) {
-          const uint32_t w = vw[wi], w8 = w >> 8;
-          const half2_t h0 = (as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * sv;
-          const half2_t h1 = (as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * sv;
-          const half2_t h2 = (as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * sv;
-          const half2_t h3 = (as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * sv;
-          const int d0 = c * DPT + 4 * wi;
-          *reinterpret_cast<uint32_t *>(lds_v + (d0 + 0) * VSTR + vc0 * 2) = as_u32(h0);
-          *reinterpret_cast<uint32_t *>(lds_v + (d0 + 1) * VSTR + vc0 * 2) = as_u32(h1);
-          *reinterpret_cast<uint32_t *>(lds_v + (d0 + 2) * VSTR + vc0 * 2) = as_u32(h2);
-          *reinterpret_cast<uint32_t *>(lds_v + (d0 + 3) * VSTR + vc0 * 2) = as_u32(h3);
-        }
+  auto issue = [&](int32_t it, int32_t pg) __attribute__((always_inline)) {
+    const int32_t key = tile_base(it) + 16 * sk_k;
+    st.pg = pg;
+    // Unlinked pages load page 0 (nb > 0) and stage as zeros: INT4 through a
+    // zero scale, fp16 through a select.
+    const bool ok = pg >= 0;
+    const int64_t pgs = ok ? pg : 0;
+    if constexpr (INT4) {
+      const Int4Page f(D);
+      const uint8_t *blk = p.pool + (pgs * p.H + h) * f.block;
+      const int slot = 8 * sk_pp + sk_c, g = (sk_c * DPT) / 64;
+      if constexpr (DPT / 4 == 4) {
+        const u32x4 kk = *reinterpret_cast<const u32x4 *>(blk + f.kcodes + slot * f.BPL);
+        const u32x4 vv = *reinterpret_cast<const u32x4 *>(blk + f.vcodes + slot * f.BPL);
+        st.kw[0] = kk.x; st.kw[1] = kk.y; st.kw[2] = kk.z; st.kw[3] = kk.w;
+        st.vw[0] = vv.x; st.vw[1] = vv.y; st.vw[2] = vv.z; st.vw[3] = vv.w;
       } else {
-        const int32_t key0 = tb + 16 * k + pp;  // token pp of the chunk; pp+8 is key0 + 8
-        const half_t *kp = reinterpret_cast<const half_t *>(p.pool);
-        const half_t *vp = reinterpret_cast<const half_t *>(p.vpool);
-        const int32_t pos0 = key0 % p.bs, pos1 = (key0 + 8) % p.bs;
-        // chunk k lies in one page when bs % 16 == 0
-        const int64_t r0 = (((int64_t)pg * p.bs + pos0) * p.H + h) * D + c * DPT;
-        const int64_t r1 = (((int64_t)pg * p.bs + pos1) * p.H + h) * D + c * DPT;
+        const uint2 kk = *reinterpret_cast<const uint2 *>(blk + f.kcodes + slot * f.BPL);
+        const uint2 vv = *reinterpret_cast<const uint2 *>(blk + f.vcodes + slot * f.BPL);
+        st.kw[0] = kk.x; st.kw[1] = kk.y;
+        st.vw[0] = vv.x; st.vw[1] = vv.y;
+      }
+      const uint32_t sk = *reinterpret_cast<const uint32_t *>(blk + f.kscales + 2 * (g * 16 + 2 * sk_pp));
+      const uint32_t sv = *reinterpret_cast<const uint32_t *>(blk + f.vscales + 2 * (g * 16 + 2 * sk_pp));
+      st.sk = ok ? sk : 0u;
+      st.sv = ok ? sv : 0u;
+    } else {
+      const half_t *kp = reinterpret_cast<const half_t *>(p.pool);
+      const half_t *vp = reinterpret_cast<const half_t *>(p.vpool);
+      const int32_t pos0 = (key + sk_pp) % p.bs;  // chunk lies in one page (bs % 16 == 0)
+      const int64_t r0 = ((pgs * p.bs + pos0) * p.H + h) * D + sk_c * DPT;
+      const int64_t r1 = r0 + 8LL * p.H * D;
+      const u32x4 z = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < DPT / 8; ++i) {
-          *reinterpret_cast<uint4 *>(krow0 + 16 * i) = *reinterpret_cast<const uint4 *>(kp + r0 + 8 * i);
-          *reinterpret_cast<uint4 *>(krow1 + 16 * i) = *reinterpret_cast<const uint4 *>(kp + r1 + 8 * i);
-        }
-#pragma unroll
-        for (int i = 0; i < DPT / 8; ++i) {
-          const half8_t a = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4 *>(vp + r0 + 8 * i));
-          const half8_t bb = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4 *>(vp + r1 + 8 * i));
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            *reinterpret_cast<uint32_t *>(lds_v + (c * DPT + 8 * i + e) * VSTR + vc0 * 2) = as_u32(half2_t{a[e], bb[e]});
-        }
+      for (int i = 0; i < DPT / 8; ++i) {
+        const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kp + r0 + 8 * i);
+        const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kp + r1 + 8 * i);
+        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(vp + r0 + 8 * i);
+        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(vp + r1 + 8 * i);
+        st.kr[i] = ok ? k0 : z;
+        st.kr[DPT / 8 + i] = ok ? k1 : z;
+        st.vr[i] = ok ? v0 : z;
+        st.vr[DPT / 8 + i] = ok ? v1 : z;
       }
     }
-    __syncthreads();
+  };
 
-    // ---- this wave's share: skip tiles with no visible key for its queries ----
-    const bool is_sink_tile = tb < sink_end;
-    bool any_vis;
-    if (causal)
-      any_vis = tb <= wpos_hi && (is_sink_tile || tb + kTileKeys - 1 >= wpos_lo - p.W + 1) && qw0 < p.Lq;
-    else
-      any_vis = qw0 < p.Lq;
-    if (!any_vis) continue;
-    const bool pages_ok = s_pages[0] >= 0 && s_pages[1] >= 0 && s_pages[2] >= 0 && s_pages[3] >= 0;
-    const bool full = pages_ok && tb + kTileKeys <= kv_lim &&
-                      (causal ? (tb + kTileKeys - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1)
-                              : (tb >= ctx - p.W)) &&
-                      wq_last == qw0 + 31;
-
-    // S^T blocks: rows = keys (32 per block), columns = this wave's queries
-    float16_t s[2];
+  auto commit = [&](int buf) __attribute__((always_inline)) {
+    uint8_t *krow0 = lds_k + buf * KBUF + sk_R0 * KSTR + sk_c * DPT * 2;
+    uint8_t *krow1 = krow0 + KSTR;
+    uint8_t *vbase = lds_v + buf * VBUF + sk_c * DPT * VSTR + vt_swz(2 * sk_vc0, sk_c * DPT);
+    if (lane == 0) s_pg[buf][sk_k] = st.pg;
+    if constexpr (INT4) {
+      const half2_t sk = as_half2(st.sk), sv = as_half2(st.sv);
+      const half2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f};
+      const half2_t b72 = {(half_t)72.0f, (half_t)72.0f};
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      s[blk] = (float16_t){};
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const half2_t s2 = t2 ? half2_t{sk.y, sk.y} : half2_t{sk.x, sk.x};
+        uint8_t *dst = t2 ? krow1 : krow0;
+#pragma unroll
+        for (int wi = 0; wi < DPT / 8; ++wi) {
+          const uint32_t w = st.kw[t2 * (DPT / 8) + wi], w8 = w >> 8;
+          const half2_t h0 = (as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * s2;
+          const half2_t h1 = (as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * s2;
+          const half2_t h2 = (as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * s2;
+          const half2_t h3 = (as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * s2;
+          *reinterpret_cast<uint4 *>(dst + 16 * wi) = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
+        }
+      }
+#pragma unroll
+      for (int wi = 0; wi < DPT / 4; ++wi) {
+        const uint32_t w = st.vw[wi], w8 = w >> 8;
+        const half2_t h0 = (as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * sv;
+        const half2_t h1 = (as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * sv;
+        const half2_t h2 = (as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * sv;
+        const half2_t h3 = (as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * sv;
+        uint8_t *vd = vbase + 4 * wi * VSTR;
+        *reinterpret_cast<uint32_t *>(vd) = as_u32(h0);
+        *reinterpret_cast<uint32_t *>(vd + VSTR) = as_u32(h1);
+        *reinterpret_cast<uint32_t *>(vd + 2 * VSTR) = as_u32(h2);
+        *reinterpret_cast<uint32_t *>(vd + 3 * VSTR) = as_u32(h3);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPT / 8; ++i) {
+        *reinterpret_cast<u32x4 *>(krow0 + 16 * i) = st.kr[i];
+        *reinterpret_cast<u32x4 *>(krow1 + 16 * i) = st.kr[DPT / 8 + i];
+        const half8_t a = __builtin_bit_cast(half8_t, st.vr[i]);
+        const half8_t c = __builtin_bit_cast(half8_t, st.vr[DPT / 8 + i]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t *>(vbase + (8 * i + e) * VSTR) = as_u32(half2_t{a[e], c[e]});
+      }
+    }
+  };
+
+  int32_t pg_next = lookup(0);
+  if (n_tiles > 0) {
+    issue(0, pg_next);
+    commit(0);
+    pg_next = lookup(1);
+    if (n_tiles > 1) issue(1, pg_next);
+    pg_next = lookup(2);
+  }
+  __syncthreads();
+
+  // Per-lane V^T read addresses of the four 16-key chunks (swizzle included;
+  // odd 32-dim blocks flip chunk bit 1, see vt_swz).
+  int32_t va[4];
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc)
+    va[kc] = (lane & 31) * VSTR + vt_swz(32 * kc + 16 * hl, lane & 31);
+  const int32_t ka = (lane & 31) * KSTR + 16 * hl;
+
+  const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
+  for (int32_t it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    const int32_t tb = tile_base(it);
+    const uint8_t *kt = lds_k + buf * KBUF;
+    const uint8_t *vt = lds_v + buf * VBUF;
+    const bool is_sink_tile = tb < sink_end;
+    bool any_vis = qw0 < p.Lq;
+    if (causal)
+      any_vis = any_vis && tb <= wpos_hi && (is_sink_tile || tb + kTileKeys - 1 >= wpos_lo - p.W + 1);
+    const int32_t pg0 = s_pg[buf][0], pg1 = s_pg[buf][1], pg2 = s_pg[buf][2], pg3 = s_pg[buf][3];
+    const bool full = (pg0 | pg1 | pg2 | pg3) >= 0 && tb + kTileKeys <= kv_lim &&
+                      (causal ? (tb + kTileKeys - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
+                      wq_last == qw0 + QW - 1;
+
+    // S^T of one 32-key block (32 keys x 32 queries per query block; every K
+    // fragment feeds all QB query blocks).
+    auto qk = [&](int blk, float16_t (&sq)[QB]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) sq[qb] = (float16_t){};
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        const half8_t a = *reinterpret_cast<const half8_t *>(lds_k + (32 * blk + (lane & 31)) * KSTR + (16 * c + 8 * hl) * 2);
-        s[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c], s[blk], 0, 0, 0);
+        const half8_t a = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KSTR + ka + 32 * c);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          sq[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qb][c], sq[qb], 0, 0, 0);
       }
-    }
-    // scores in log2 units; masked entries -> -inf
-    float tmax = -INFINITY;
+    };
+    // Masks, raises the running max lazily, and packs the probabilities of
+    // one block to fp16 in PV operand order.
+    auto softmax = [&](int blk, float16_t (&sq)[QB], half8_t (&pb)[QB][2]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = s[blk][r] * p.qk_scale_log2;
+      for (int qb = 0; qb < QB; ++qb) {
+        float16_t &s = sq[qb];
         if (!full) {
-          const int R = 32 * blk + 8 * (r >> 2) + 4 * hl + (r & 3);
-          const int32_t key = tb + row_key(R);
-          const bool ok = q_ok && s_pages[R >> 4] >= 0 && key < kv_lim &&
-                          key_visible(key, qpos, ctx, p.W, p.sinks, causal);
-          v = ok ? v : -INFINITY;
+          const int32_t pgl = (blk == 0) ? pg0 : pg2, pgh = (blk == 0) ? pg1 : pg3;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int R = 32 * blk + 8 * (r >> 2) + 4 * hl + (r & 3);
+            const int32_t key = tb + row_key(R);
+            const bool ok = q_ok[qb] && ((r >> 3) ? pgh : pgl) >= 0 && key < kv_lim &&
+                            key_visible(key, qpos[qb], ctx, p.W, p.sinks, causal);
+            s[r] = ok ? s[r] : -INFINITY;
+          }
         }
-        s[blk][r] = v;
-        tmax = fmaxf(tmax, v);
-      }
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    if (__any(tmax > m + 8.0f)) {  // lazy rescale: p stays <= 2^8 between raises
-      const float mn = fmaxf(m, tmax);
-      const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
-      lsum *= alpha;
+        float tmax = s[0];
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
+        tmax = half_max(tmax) * cs;
+        if (__any(tmax > m[qb] + 8.0f)) {  // lazy rescale: p stays <= 2^8 between raises
+          const float mn = fmaxf(m[qb], tmax);
+          const float alpha = (mn == m[qb]) ? 1.0f : fast_exp2(m[qb] - mn);
+          lsum[qb] *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      m = mn;
-    }
-    half8_t pb[4];
+          for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-#pragma unroll
-      for (int g2 = 0; g2 < 2; ++g2) {
-        half8_t v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = s[blk][8 * g2 + e];
-          const float pw = (full || x != -INFINITY) ? fast_exp2(x - m) : 0.0f;
-          lsum += pw;
-          v[e] = (half_t)pw;
+            for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+          m[qb] = mn;
+          negm[qb] = (mn == -INFINITY) ? 0.0f : -mn;
         }
-        pb[2 * blk + g2] = v;
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const half2_t pp2 = {(half_t)fast_exp2(fmaf(s[8 * g2 + e], cs, negm[qb])),
+                                 (half_t)fast_exp2(fmaf(s[8 * g2 + e + 1], cs, negm[qb]))};
+            lsum[qb] = __builtin_amdgcn_fdot2(pp2, ones, lsum[qb], false);
+            pb[qb][g2][e] = pp2.x;
+            pb[qb][g2][e + 1] = pp2.y;
+          }
+        }
       }
+    };
+    // O^T += V^T P^T over one block's two 16-key chunks
+    auto pv = [&](int blk, half8_t (&pb)[QB][2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+          const int kc = (2 * blk + g2) ^ (2 * (db & 1));
+          const half8_t a = *reinterpret_cast<const half8_t *>(vt + 32 * db * VSTR + va[kc]);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[qb][g2], o[qb][db], 0, 0, 0);
+        }
+      }
+    };
+
+    // Order: S(0) | staging of the next tile | softmax(0) | S(1) | PV(0) |
+    // softmax(1) | PV(1): the staging VALU runs under S(0), softmax(1)
+    // under PV(0).
+    float16_t sa[QB], sc[QB];
+    half8_t pa[QB][2], pc[QB][2];
+    if (any_vis) qk(0, sa);
+    if (it + 1 < n_tiles) commit(buf ^ 1);
+    if (it + 2 < n_tiles) issue(it + 2, pg_next);
+    pg_next = lookup(it + 3);
+    if (any_vis) {
+      softmax(0, sa, pa);
+      qk(1, sc);
+      pv(0, pa);
+      softmax(1, sc, pc);
+      pv(1, pc);
     }
-    // O^T += V^T P^T over the four 16-key chunks
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l = half_sum(lsum[qb]);
+    if (!q_ok[qb]) continue;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int32_t qi = qw0 + 32 * qb + (lane & 31);
+    half_t *orow = p.out + (((int64_t)b * p.Lq + qi) * p.H + h) * D;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const half8_t a = *reinterpret_cast<const half8_t *>(lds_v + (32 * db + (lane & 31)) * VSTR + (16 * kc + 8 * hl) * 2);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kc], o[db], 0, 0, 0);
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * db + 8 * g + 4 * hl;
+        const half2_t x = {(half_t)(o[qb][db][4 * g] * inv), (half_t)(o[qb][db][4 * g + 1] * inv)};
+        const half2_t y = {(half_t)(o[qb][db][4 * g + 2] * inv), (half_t)(o[qb][db][4 * g + 3] * inv)};
+        *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(as_u32(x), as_u32(y));
       }
-    }
-  }
-
-  lsum += __shfl_xor(lsum, 32, 64);
-  if (!q_ok) return;
-  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  half_t *orow = p.out + (((int64_t)b * p.Lq + qi) * p.H + h) * D;
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = 32 * db + 8 * g + 4 * hl;
-      const half2_t a = {(half_t)(o[db][4 * g] * inv), (half_t)(o[db][4 * g + 1] * inv)};
-      const half2_t c = {(half_t)(o[db][4 * g + 2] * inv), (half_t)(o[db][4 * g + 3] * inv)};
-      *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(as_u32(a), as_u32(c));
     }
   }
 }
@@ -329,7 +461,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p)
 bool prefill_supported(const memopt_attn_desc &d) {
   auto al16 = [](const void *x) { return ((uintptr_t)x & 15) == 0; };
   if (d.q_len < 16 || (d.head_dim != 64 && d.head_dim != 128)) return false;
-  if (d.num_heads > 65535 || d.batch > 65535 || d.num_kv_blocks <= 0) return false;
+  if (d.num_kv_blocks <= 0) return false;
   if (!al16(d.query) || !al16(d.out) || !al16(d.key_cache)) return false;
   if (d.kv_format == MEMOPT_KV_INT4) return d.block_size == 16;
   if (d.kv_format != MEMOPT_KV_FP16 || d.block_size % 16 != 0 || !al16(d.value_cache)) return false;
@@ -355,15 +487,17 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
   p.sinks = d.num_sink_tokens < 0 ? 0 : d.num_sink_tokens;
   p.causal = d.causal;
   p.qk_scale_log2 = qk_scale_log2;
-  constexpr int NW = 4;
-  const dim3 grid((unsigned)((d.q_len + 32 * NW - 1) / (32 * NW)), d.num_heads, d.batch);
+  constexpr int NW = 4, QB = 1;
+  const int64_t n_wg = (int64_t)((d.q_len + 32 * QB * NW - 1) / (32 * QB * NW)) * d.num_heads * d.batch;
+  MEMOPT_REQUIRE(n_wg < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "paged_attention: too many query tiles");
+  const dim3 grid((unsigned)n_wg);
   const bool int4 = d.kv_format == MEMOPT_KV_INT4;
   if (d.head_dim == 128) {
-    if (int4) hipLaunchKernelGGL((prefill_kernel<128, true, NW>), grid, dim3(NW * 64), 0, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<128, false, NW>), grid, dim3(NW * 64), 0, stream, p);
+    if (int4) hipLaunchKernelGGL((prefill_kernel<128, true, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<128, false, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
   } else {
-    if (int4) hipLaunchKernelGGL((prefill_kernel<64, true, NW>), grid, dim3(NW * 64), 0, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<64, false, NW>), grid, dim3(NW * 64), 0, stream, p);
+    if (int4) hipLaunchKernelGGL((prefill_kernel<64, true, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<64, false, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
   }
   return check_launch("paged_attention(prefill)");
 }
