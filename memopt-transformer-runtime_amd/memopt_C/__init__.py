@@ -12,9 +12,11 @@ reference behaviour):
   * ``get_key_pool()`` / ``get_value_pool()`` — called by the reference's
     ``DynamicAttention`` (src/memopt/attention.py:330-331) but missing from
     its extension;
-  * ``init_pool(..., kv_format="int4")`` — INT4 page pool (codes
-    [nb, H, bs, D/2] u8 + fp16 scales [nb, H, bs, D/64]); ``write_cache`` then
-    quantizes on the fly and ``get_pool_scales()`` returns the scales;
+  * ``init_pool(..., kv_format="int4")`` — INT4 page pool: one u8 buffer
+    [nb, H, 17*D] of (page, head) blocks holding K codes, V codes, K scales
+    and V scales (layout in csrc/page_format.hpp); ``write_cache`` then
+    quantizes on the fly, ``get_int4_pages()`` returns the buffer and
+    ``get_pool_scales()`` the fp16 scale regions;
   * ``dynamic_sparse_attention(..., *, num_sink_tokens=0, causal=False,
     key_scales=None, value_scales=None, kv_layout=None)`` — INT4 caches are
     dequantized just in time inside the kernel;
