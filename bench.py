@@ -194,6 +194,87 @@ def bench_prefill(torch, memopt_C, cfg, steps=10, warmup=3):
             "write_cache_ms": round(write_ms, 4)}
 
 
+CFG3 = dict(batch=16, heads=32, head_dim=128, ctx=8192, block=16, retain=0.75, sinks=4, window=2048,
+            outlier_frac=0.005, outlier_mult=10.0, seed=3)
+CFG5 = dict(batch=4, heads=32, head_dim=128, ctx=131072, block=16, retain=0.75, sinks=4, spare_pages=4096,
+            outlier_frac=0.01, outlier_mult=8.0, seed=5)
+
+
+def fill_pages(torch, memopt_C, bt, cfg, gen):
+    """write_cache of seeded K/V (N(0,1) with outliers) for every sequence of `bt`, one sequence at a time."""
+    B, H, D, ctx, bs = bt.shape[0], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
+    dev = bt.device
+    for b in range(B):
+        slots = (bt[b].long()[:, None] * bs + torch.arange(bs, device=dev)).reshape(-1)[:ctx].to(torch.int32)
+        kv = []
+        for _ in range(2):
+            x = torch.randn(ctx, H, D, device=dev, generator=gen)
+            m = torch.rand(ctx, H, D, device=dev, generator=gen) < cfg["outlier_frac"]
+            kv.append(torch.where(m, x * cfg["outlier_mult"], x).half())
+            del x, m
+        memopt_C.write_cache(kv[0], kv[1], bt, slots.contiguous())
+        del kv
+
+
+def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, steps=20, warmup=3):
+    """evict_tokens (intended top-k, sinks kept) on LogNormal(0,1) scores, then
+    INT4 decode over sinks U window. `copies` independent page sets (each
+    filled and evicted on its own) are decoded in turn so that a working set
+    smaller than the 256 MB last-level cache is not re-read from it. Returns
+    the eviction time and the decode rate on the bytes of the pages the
+    decode actually visits."""
+    B, H, D, ctx, bs = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
+    dev = torch.device("cuda", 0)
+    nbps = ctx // bs
+    nb = copies * B * nbps + cfg.get("spare_pages", 0)
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    if fifo_trace:
+        # allocate everything, free it in a seeded random order, then allocate
+        # the sequences' pages from the FIFO: a fragmented block table
+        got = [memopt_C.allocate_block() for _ in range(nb)]
+        order = torch.randperm(nb, generator=torch.Generator().manual_seed(cfg["seed"])).tolist()
+        for i in order:
+            memopt_C.free_block(got[i])
+        pages = torch.tensor([memopt_C.allocate_block() for _ in range(copies * B * nbps)], dtype=torch.int32)
+    else:
+        pages = torch.randperm(nb, generator=torch.Generator().manual_seed(cfg["seed"]))[:copies * B * nbps]
+        pages = pages.to(torch.int32)
+    gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    first_win = max(0, ctx - window) // bs
+    vis = torch.zeros(nbps, dtype=torch.bool)
+    vis[first_win:] = True
+    vis[:(cfg["sinks"] + bs - 1) // bs] = True
+    per_page = H * (2 * bs * (D // 2) + 2 * bs * 2 * (D // 64))
+    calls, evict_ms, unlinked, nbytes = [], [], 0, 0
+    cl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    kc, vc = memopt_C.get_pool_tensors()
+    for c in range(copies):
+        bt = pages[c * B * nbps:(c + 1) * B * nbps].reshape(B, nbps).to(dev)
+        fill_pages(torch, memopt_C, bt, cfg, gen)
+        q = torch.randn(B, 1, H, D, device=dev, generator=gen).half()
+        scores = torch.exp(torch.randn(B, H, ctx, device=dev, generator=gen))
+        ibf = torch.zeros(nb, dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        memopt_C.evict_tokens(scores, bt, ibf, cfg["retain"], cfg["sinks"])
+        e1.record()
+        torch.cuda.synchronize()
+        evict_ms.append(e0.elapsed_time(e1))
+        unlinked += int((bt == -1).sum())
+        nbytes += int(((bt.cpu() >= 0) & vis[None]).sum()) * per_page
+        calls.append(memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, window, num_sink_tokens=cfg["sinks"]))
+        del scores
+    nbytes //= copies  # bytes per step (copies are equal up to unlinked pages)
+    ms, _ = time_steps(torch, calls, steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": "decode_int4_pages_kernel<128, 4, 2>", "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
+            "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "evict_tokens_ms": round(sum(evict_ms) / len(evict_ms), 4), "pages_unlinked": unlinked,
+            "page_sets_rotated": copies,
+            "block_tables": "seeded FIFO alloc/free trace" if fifo_trace else "seeded random permutation"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,8 +335,15 @@ def main():
         import oracle as O  # CPU baseline leg only
         line["cpu_baseline"] = cpu_baseline_decode(torch, O, memopt_C, tables, q, cl, cfg)
     if not args.no_secondary:  # re-initializes the pool: runs last
-        line["secondary"] = {"prefill": bench_prefill(torch, memopt_C, CFG4),
-                             "kv_quant": bench_kv_quant(torch, memopt_C, cfg)}
+        sec = {"prefill": bench_prefill(torch, memopt_C, CFG4)}
+        sec["sparse_decode_config3"] = dict(
+            workload="BASELINE configs[2]: B 16, ctx 8192, evict_tokens r 0.75 + 4 sinks, decode window 2048",
+            **bench_sparse_decode(torch, memopt_C, CFG3, CFG3["window"], fifo_trace=False, copies=3))
+        sec["long_context_config5"] = dict(
+            workload="BASELINE configs[4]: B 4, ctx 131072, 32768 pages, evict_tokens r 0.75 + 4 sinks, full window",
+            **bench_sparse_decode(torch, memopt_C, CFG5, CFG5["ctx"], fifo_trace=True))
+        sec["kv_quant"] = bench_kv_quant(torch, memopt_C, cfg)
+        line["secondary"] = sec
     print(json.dumps(line), flush=True)
 
 

@@ -165,6 +165,55 @@ def test_config3_evict_then_sparse_decode():
     assert_close(got, want, what="config3")
 
 
+def test_config5_long_context_fragmented_pool():
+    """Config 5: B4, ctx 131072 (8192 pages per sequence, 32768 in use) in a
+    pool with spare pages, block tables from a seeded FIFO alloc/free trace;
+    evict_tokens(r=0.75, 4 sinks) on LogNormal scores (no length cap), then
+    decode over the full context with 4 sinks."""
+    B, H, D, ctx, sinks = 4, 32, 128, 131072, 4
+    nbps, spare = ctx // 16, 4096
+    nb = B * nbps + spare
+    memopt_C.init_pool(nb, 16, H, D, kv_format="int4")
+    got = [memopt_C.allocate_block() for _ in range(nb)]
+    assert got == list(range(nb)) and memopt_C.allocate_block() == -1
+    for i in torch.randperm(nb, generator=torch.Generator().manual_seed(5)).tolist():
+        memopt_C.free_block(got[i])
+    pages = [memopt_C.allocate_block() for _ in range(B * nbps)]
+    assert len(set(pages)) == B * nbps and memopt_C.free_blocks_count() == spare
+    bt = torch.tensor(pages, dtype=torch.int32).reshape(B, nbps).to(dev())
+    g = torch.Generator(device=dev()).manual_seed(5)
+    for b in range(B):
+        slots = (bt[b].long()[:, None] * 16 + torch.arange(16, device=dev())).reshape(-1).to(torch.int32)
+        k = torch.randn(ctx, H, D, device=dev(), generator=g)
+        k = torch.where(torch.rand(ctx, H, D, device=dev(), generator=g) < 0.01, k * 8, k).half()
+        v = torch.randn(ctx, H, D, device=dev(), generator=g)
+        v = torch.where(torch.rand(ctx, H, D, device=dev(), generator=g) < 0.01, v * 8, v).half()
+        memopt_C.write_cache(k, v, bt, slots)
+        del k, v
+    q = torch.randn(B, 1, H, D, device=dev(), generator=g).half()
+    scores = torch.exp(torch.randn(B, H, ctx, device=dev(), generator=g))
+    ibf = torch.zeros(nb, dtype=torch.int32, device=dev())
+    bt0 = bt.clone()
+    memopt_C.evict_tokens(scores, bt, ibf, 0.75, sinks)
+    assert torch.equal(bt == -1, ibf[bt0.long()] == H)
+    # keep count per (seq, head): exactly ceil(0.75 * L) rows survive (LogNormal scores have no ties)
+    kpool, vpool = dequant_pages_dev(memopt_C.get_int4_pages()[bt0[0].long()], D)
+    zero_rows = (kpool.reshape(ctx, H, D) == 0).all(dim=-1)      # [ctx, H] of sequence 0
+    assert torch.equal(zero_rows.sum(dim=0).cpu(), torch.full((H,), ctx - int(np.ceil(np.float32(0.75) * ctx))))
+    assert not zero_rows[:sinks].any()
+    del kpool, vpool, zero_rows
+    cl = torch.full((B,), ctx, dtype=torch.int32, device=dev())
+    kc, vc = memopt_C.get_pool_tensors()
+    out = memopt_C.dynamic_sparse_attention(q, kc, vc, bt, cl, ctx, ctx, num_sink_tokens=sinks)
+    for b in range(B):  # one sequence at a time to bound the reference's memory
+        used = bt0[b].long()
+        kp, vp = dequant_pages_dev(memopt_C.get_int4_pages()[used], D)
+        local = torch.where(bt[b] >= 0, torch.arange(nbps, device=dev(), dtype=torch.int32), -1)[None]
+        want = reference_decode_dev(q[b:b + 1], kp, vp, local, cl[b:b + 1], ctx, sinks)
+        assert_close(out[b:b + 1], want, what=f"config5 b={b}")
+        del kp, vp
+
+
 def test_config1_slice_golden_fixture():
     """Committed fixture: INT4 pages written on device == frozen bytes, and the
     decode output over them matches the frozen oracle output."""
