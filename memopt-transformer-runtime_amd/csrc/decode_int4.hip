@@ -526,16 +526,13 @@ struct DecodeShape {
   int nw, u;
 };
 static DecodeShape decode_shape() {
-  static DecodeShape s = {0, 0};
-  if (s.nw == 0) {
-    s = {4, 2};
-    if (const char *e = std::getenv("MEMOPT_DECODE_SHAPE")) {
-      int a = 0, c = 0;
-      if (std::sscanf(e, "%d,%d", &a, &c) == 2 &&
-          ((a == 4 && c == 2) || (a == 8 && c == 1) || (a == 8 && c == 2) || (a == 8 && c == 4) ||
-           (a == 16 && c == 2) || (a == 4 && c == 4)))
-        s = {a, c};
-    }
+  DecodeShape s = {4, 2};
+  if (const char *e = std::getenv("MEMOPT_DECODE_SHAPE")) {
+    int a = 0, c = 0;
+    if (std::sscanf(e, "%d,%d", &a, &c) == 2 &&
+        ((a == 4 && c == 2) || (a == 8 && c == 1) || (a == 8 && c == 2) || (a == 8 && c == 4) ||
+         (a == 16 && c == 2) || (a == 4 && c == 4)))
+      s = {a, c};
   }
   return s;
 }
