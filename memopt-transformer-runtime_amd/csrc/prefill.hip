@@ -27,6 +27,8 @@
 //  * tiles wholly inside every query's visible range skip the mask; the
 //    running max is raised lazily (rescale only when exceeded by > 8 in log2
 //    units).
+#include <cstdlib>
+
 #include "attention.hpp"
 #include "page_format.hpp"
 
@@ -36,7 +38,6 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-static constexpr int kTileKeys = 64;
 
 struct PrefillParams {
   const half_t *q;
@@ -70,7 +71,8 @@ __device__ __forceinline__ int32_t vt_col(int32_t R) {
 // XOR-swizzled by bits 4-5 of the row so the staging writes (16 rows per
 // thread, 8 threads per row group) spread over the LDS banks; 16 consecutive
 // rows share one swizzle, which keeps the MFMA operand reads conflict-free.
-__device__ __forceinline__ int vt_swz(int cb, int d) { return cb ^ (32 * ((d >> 4) & 3)); }
+template <int SW>
+__device__ __forceinline__ int vt_swz(int cb, int d) { return cb ^ (SW * ((d >> 4) & 3)); }
 
 __device__ __forceinline__ bool key_visible(int32_t key, int32_t qpos, int32_t ctx, int32_t W, int32_t sinks,
                                             bool causal) {
@@ -82,16 +84,21 @@ __device__ __forceinline__ bool key_visible(int32_t key, int32_t qpos, int32_t c
 // One staging task per thread: (16-key chunk k, token pair pp, dim slice c)
 // of a 64-key tile; the registers below carry its raw data from the global
 // load (issued one tile ahead) to the LDS write.
-template <int D, bool INT4>
+template <int D, bool INT4, bool SPLIT>
 struct Staged {
   static constexpr int DPT = D / 8;  // dims per task
   int32_t pg;
-  // INT4: K codes of tokens pp and pp+8 (DPT/8 words each), V codes (DPT/4
-  // words, each 4 dims x both tokens), scales (token pp, token pp+8).
-  // fp16: K and V rows of both tokens (DPT/8 16-byte vectors each).
-  uint32_t kw[INT4 ? DPT / 4 : 1], vw[INT4 ? DPT / 4 : 1];
-  uint32_t sk, sv;
-  u32x4 kr[INT4 ? 1 : 2 * (DPT / 8)], vr[INT4 ? 1 : 2 * (DPT / 8)];
+  // INT4: K codes of tokens pp and pp+8 (DPT/8 words each) at w[KO..], V
+  // codes (DPT/4 words, each 4 dims x both tokens) at w[VO..], scales
+  // (token pp, token pp+8) in sc[KO] / sc[VO ? 1 : 0].
+  // fp16: K and V rows of both tokens (DPT/8 16-byte vectors each), r[KO..]
+  // and r[VR..]. When a thread stages only K or only V (SPLIT), both parts
+  // share the same registers.
+  static constexpr int NW_ = INT4 ? DPT / 4 : 1, NR_ = INT4 ? 1 : 2 * (DPT / 8);
+  static constexpr int VO = SPLIT ? 0 : NW_, VR = SPLIT ? 0 : NR_, VS = SPLIT ? 0 : 1;
+  uint32_t w[SPLIT ? NW_ : 2 * NW_];
+  uint32_t sc[SPLIT ? 1 : 2];
+  u32x4 r[SPLIT ? NR_ : 2 * NR_];
 };
 
 // Value of lane l ^ 32 combined with lane l's: both halves of the pair.
@@ -104,19 +111,30 @@ __device__ __forceinline__ float half_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int D, bool INT4, int NW, int QB>
-__global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const PrefillParams p) {
-  static_assert(NW == 4, "one staging task per thread");
+template <int D, bool INT4, int NW, int QB, int TK>
+__global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) : 1) void prefill_kernel(
+    const PrefillParams p) {
+  // TK keys per tile = TK/16 chunks of 16 tokens; TK*4 staging tasks of
+  // (chunk, token pair, dim slice). With as many threads as tasks a thread
+  // stages the K and V parts of its task; with twice as many, the first half
+  // of the threads stages K and the second half V.
+  constexpr int NCK = TK / 16, NBLK = TK / 32, NTASK = TK * 4;
+  static_assert(TK == 32 || TK == 64, "32- or 64-key tiles");
+  static_assert(NW * 64 == NTASK || NW * 64 == 2 * NTASK, "one task or half a task per thread");
+  constexpr bool SPLIT_KV = NW * 64 == 2 * NTASK;
+  // V^T column swizzle granularity: 32-byte blocks for 128-byte rows, 16-byte
+  // blocks for 64-byte rows (rows of TK fp16 keys).
+  constexpr int SW = TK == 64 ? 32 : 16;
   constexpr int QW = 32 * QB;               // queries per wave
   constexpr int KSTR = D * 2 + 16;          // K row stride in LDS (bytes), padded
-  constexpr int VSTR = kTileKeys * 2 + 16;  // V^T row stride (bytes), padded
-  constexpr int KBUF = kTileKeys * KSTR, VBUF = D * VSTR;
+  constexpr int VSTR = TK * 2 + 16;  // V^T row stride (bytes), padded
+  constexpr int KBUF = TK * KSTR, VBUF = D * VSTR;
   constexpr int NCH = D / 16;               // 16-dim chunks of the QK contraction
   constexpr int NDB = D / 32;               // 32-dim output blocks
   constexpr int DPT = D / 8;                // dims per staging task
   __shared__ __attribute__((aligned(16))) uint8_t lds_k[2 * KBUF];
   __shared__ __attribute__((aligned(16))) uint8_t lds_v[2 * VBUF];
-  __shared__ int32_t s_pg[2][4];
+  __shared__ int32_t s_pg[2][NCK];
 
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -186,20 +204,23 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
   const int32_t hi = max(0, causal ? min(kv_lim, pos_hi + 1) : kv_lim);
   const int32_t win_lo = max(0, causal ? pos_lo - p.W + 1 : ctx - p.W);
   const int32_t sink_end = min(p.sinks, hi);  // p.sinks >= 0
-  const int32_t sink_tiles = (sink_end + kTileKeys - 1) / kTileKeys;
-  const int32_t t_first = max(win_lo / kTileKeys, sink_tiles);
-  const int32_t t_last = (hi + kTileKeys - 1) / kTileKeys;  // exclusive
+  const int32_t sink_tiles = (sink_end + TK - 1) / TK;
+  const int32_t t_first = max(win_lo / TK, sink_tiles);
+  const int32_t t_last = (hi + TK - 1) / TK;  // exclusive
   const int32_t n_tiles = sink_tiles + max(0, t_last - t_first);
-  auto tile_base = [&](int32_t it) { return (it < sink_tiles ? it : t_first + (it - sink_tiles)) * kTileKeys; };
+  auto tile_base = [&](int32_t it) { return (it < sink_tiles ? it : t_first + (it - sink_tiles)) * TK; };
   // wave-level query span (tile skipping and the unmasked fast path)
   const int32_t wq_last = min(qw0 + QW - 1, p.Lq - 1);
   const int32_t wpos_lo = ctx - p.Lq + qw0, wpos_hi = ctx - p.Lq + wq_last;
 
   // ---- staging task of this thread ----
-  const int sk_k = tid >> 6, sk_pp = (tid >> 3) & 7, sk_c = tid & 7;
+  const int task = tid % NTASK;
+  const bool do_k = !SPLIT_KV || tid < NTASK, do_v = !SPLIT_KV || tid >= NTASK;  // wave-uniform
+  const int sk_k = task >> 6, sk_pp = (task >> 3) & 7, sk_c = task & 7;
   const int sk_R0 = 16 * sk_k + 2 * sk_pp;  // K rows of tokens pp (R0) and pp+8 (R0+1)
   const int sk_vc0 = vt_col(sk_R0);         // V^T column of token pp; pp+8 is +1
-  Staged<D, INT4> st;
+  using St = Staged<D, INT4, SPLIT_KV>;
+  St st0, st1;  // two tiles in flight between global load and LDS
 
   // Page of this thread's 16-key chunk in tile `it` (-1: none / unlinked).
   // Looked up one tile before its data is loaded, so the dependent loads
@@ -216,7 +237,7 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
     return pg;
   };
 
-  auto issue = [&](int32_t it, int32_t pg) __attribute__((always_inline)) {
+  auto issue = [&](int32_t it, int32_t pg, Staged<D, INT4, SPLIT_KV> &st) __attribute__((always_inline)) {
     const int32_t key = tile_base(it) + 16 * sk_k;
     st.pg = pg;
     // Unlinked pages load page 0 (nb > 0) and stage as zeros: INT4 through a
@@ -227,21 +248,28 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
       const Int4Page f(D);
       const uint8_t *blk = p.pool + (pgs * p.H + h) * f.block;
       const int slot = 8 * sk_pp + sk_c, g = (sk_c * DPT) / 64;
-      if constexpr (DPT / 4 == 4) {
-        const u32x4 kk = *reinterpret_cast<const u32x4 *>(blk + f.kcodes + slot * f.BPL);
-        const u32x4 vv = *reinterpret_cast<const u32x4 *>(blk + f.vcodes + slot * f.BPL);
-        st.kw[0] = kk.x; st.kw[1] = kk.y; st.kw[2] = kk.z; st.kw[3] = kk.w;
-        st.vw[0] = vv.x; st.vw[1] = vv.y; st.vw[2] = vv.z; st.vw[3] = vv.w;
-      } else {
-        const uint2 kk = *reinterpret_cast<const uint2 *>(blk + f.kcodes + slot * f.BPL);
-        const uint2 vv = *reinterpret_cast<const uint2 *>(blk + f.vcodes + slot * f.BPL);
-        st.kw[0] = kk.x; st.kw[1] = kk.y;
-        st.vw[0] = vv.x; st.vw[1] = vv.y;
+      if (do_k) {
+        if constexpr (DPT / 4 == 4) {
+          const u32x4 kk = *reinterpret_cast<const u32x4 *>(blk + f.kcodes + slot * f.BPL);
+          st.w[0] = kk.x; st.w[1] = kk.y; st.w[2] = kk.z; st.w[3] = kk.w;
+        } else {
+          const uint2 kk = *reinterpret_cast<const uint2 *>(blk + f.kcodes + slot * f.BPL);
+          st.w[0] = kk.x; st.w[1] = kk.y;
+        }
+        const uint32_t sk = *reinterpret_cast<const uint32_t *>(blk + f.kscales + 2 * (g * 16 + 2 * sk_pp));
+        st.sc[0] = ok ? sk : 0u;
       }
-      const uint32_t sk = *reinterpret_cast<const uint32_t *>(blk + f.kscales + 2 * (g * 16 + 2 * sk_pp));
-      const uint32_t sv = *reinterpret_cast<const uint32_t *>(blk + f.vscales + 2 * (g * 16 + 2 * sk_pp));
-      st.sk = ok ? sk : 0u;
-      st.sv = ok ? sv : 0u;
+      if (do_v) {
+        if constexpr (DPT / 4 == 4) {
+          const u32x4 vv = *reinterpret_cast<const u32x4 *>(blk + f.vcodes + slot * f.BPL);
+          st.w[St::VO] = vv.x; st.w[St::VO + 1] = vv.y; st.w[St::VO + 2] = vv.z; st.w[St::VO + 3] = vv.w;
+        } else {
+          const uint2 vv = *reinterpret_cast<const uint2 *>(blk + f.vcodes + slot * f.BPL);
+          st.w[St::VO] = vv.x; st.w[St::VO + 1] = vv.y;
+        }
+        const uint32_t sv = *reinterpret_cast<const uint32_t *>(blk + f.vscales + 2 * (g * 16 + 2 * sk_pp));
+        st.sc[St::VS] = ok ? sv : 0u;
+      }
     } else {
       const half_t *kp = reinterpret_cast<const half_t *>(p.pool);
       const half_t *vp = reinterpret_cast<const half_t *>(p.vpool);
@@ -251,34 +279,38 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
       const u32x4 z = {0, 0, 0, 0};
 #pragma unroll
       for (int i = 0; i < DPT / 8; ++i) {
-        const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kp + r0 + 8 * i);
-        const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kp + r1 + 8 * i);
-        const u32x4 v0 = *reinterpret_cast<const u32x4 *>(vp + r0 + 8 * i);
-        const u32x4 v1 = *reinterpret_cast<const u32x4 *>(vp + r1 + 8 * i);
-        st.kr[i] = ok ? k0 : z;
-        st.kr[DPT / 8 + i] = ok ? k1 : z;
-        st.vr[i] = ok ? v0 : z;
-        st.vr[DPT / 8 + i] = ok ? v1 : z;
+        if (do_k) {
+          const u32x4 k0 = *reinterpret_cast<const u32x4 *>(kp + r0 + 8 * i);
+          const u32x4 k1 = *reinterpret_cast<const u32x4 *>(kp + r1 + 8 * i);
+          st.r[i] = ok ? k0 : z;
+          st.r[DPT / 8 + i] = ok ? k1 : z;
+        }
+        if (do_v) {
+          const u32x4 v0 = *reinterpret_cast<const u32x4 *>(vp + r0 + 8 * i);
+          const u32x4 v1 = *reinterpret_cast<const u32x4 *>(vp + r1 + 8 * i);
+          st.r[St::VR + i] = ok ? v0 : z;
+          st.r[St::VR + DPT / 8 + i] = ok ? v1 : z;
+        }
       }
     }
   };
 
-  auto commit = [&](int buf) __attribute__((always_inline)) {
+  auto commit = [&](int buf, const Staged<D, INT4, SPLIT_KV> &st) __attribute__((always_inline)) {
     uint8_t *krow0 = lds_k + buf * KBUF + sk_R0 * KSTR + sk_c * DPT * 2;
     uint8_t *krow1 = krow0 + KSTR;
-    uint8_t *vbase = lds_v + buf * VBUF + sk_c * DPT * VSTR + vt_swz(2 * sk_vc0, sk_c * DPT);
-    if (lane == 0) s_pg[buf][sk_k] = st.pg;
+    uint8_t *vbase = lds_v + buf * VBUF + sk_c * DPT * VSTR + vt_swz<SW>(2 * sk_vc0, sk_c * DPT);
+    if (lane == 0 && do_k) s_pg[buf][sk_k] = st.pg;
     if constexpr (INT4) {
-      const half2_t sk = as_half2(st.sk), sv = as_half2(st.sv);
+      const half2_t sk = as_half2(st.sc[0]), sv = as_half2(st.sc[St::VS]);
       const half2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f};
       const half2_t b72 = {(half_t)72.0f, (half_t)72.0f};
 #pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
+      for (int t2 = 0; t2 < 2 && do_k; ++t2) {
         const half2_t s2 = t2 ? half2_t{sk.y, sk.y} : half2_t{sk.x, sk.x};
         uint8_t *dst = t2 ? krow1 : krow0;
 #pragma unroll
         for (int wi = 0; wi < DPT / 8; ++wi) {
-          const uint32_t w = st.kw[t2 * (DPT / 8) + wi], w8 = w >> 8;
+          const uint32_t w = st.w[t2 * (DPT / 8) + wi], w8 = w >> 8;
           const half2_t h0 = (as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * s2;
           const half2_t h1 = (as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * s2;
           const half2_t h2 = (as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * s2;
@@ -287,8 +319,8 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
         }
       }
 #pragma unroll
-      for (int wi = 0; wi < DPT / 4; ++wi) {
-        const uint32_t w = st.vw[wi], w8 = w >> 8;
+      for (int wi = 0; wi < DPT / 4 && do_v; ++wi) {
+        const uint32_t w = st.w[St::VO + wi], w8 = w >> 8;
         const half2_t h0 = (as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * sv;
         const half2_t h1 = (as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * sv;
         const half2_t h2 = (as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * sv;
@@ -302,10 +334,13 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
     } else {
 #pragma unroll
       for (int i = 0; i < DPT / 8; ++i) {
-        *reinterpret_cast<u32x4 *>(krow0 + 16 * i) = st.kr[i];
-        *reinterpret_cast<u32x4 *>(krow1 + 16 * i) = st.kr[DPT / 8 + i];
-        const half8_t a = __builtin_bit_cast(half8_t, st.vr[i]);
-        const half8_t c = __builtin_bit_cast(half8_t, st.vr[DPT / 8 + i]);
+        if (do_k) {
+          *reinterpret_cast<u32x4 *>(krow0 + 16 * i) = st.r[i];
+          *reinterpret_cast<u32x4 *>(krow1 + 16 * i) = st.r[DPT / 8 + i];
+        }
+        if (!do_v) continue;
+        const half8_t a = __builtin_bit_cast(half8_t, st.r[St::VR + i]);
+        const half8_t c = __builtin_bit_cast(half8_t, st.r[St::VR + DPT / 8 + i]);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           *reinterpret_cast<uint32_t *>(vbase + (8 * i + e) * VSTR) = as_u32(half2_t{a[e], c[e]});
@@ -313,26 +348,29 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
     }
   };
 
-  int32_t pg_next = lookup(0);
+  // Tiles 0, 2, 4, ... are loaded through st0 and tiles 1, 3, ... through
+  // st1; loads run two tiles ahead of the LDS write, the page lookup three.
   if (n_tiles > 0) {
-    issue(0, pg_next);
-    commit(0);
-    pg_next = lookup(1);
-    if (n_tiles > 1) issue(1, pg_next);
-    pg_next = lookup(2);
+    issue(0, lookup(0), st0);
+    commit(0, st0);
+    if (n_tiles > 1) issue(1, lookup(1), st1);
+    if (n_tiles > 2) issue(2, lookup(2), st0);
   }
+  int32_t pg_next = lookup(3);
   __syncthreads();
 
-  // Per-lane V^T read addresses of the four 16-key chunks (swizzle included;
-  // odd 32-dim blocks flip chunk bit 1, see vt_swz).
-  int32_t va[4];
+  // Per-lane V^T read addresses of the 16-key chunks, swizzle included; in
+  // odd 32-dim blocks the swizzle also flips chunk bit log2(SW / 16).
+  int32_t va[NCK];
 #pragma unroll
-  for (int kc = 0; kc < 4; ++kc)
-    va[kc] = (lane & 31) * VSTR + vt_swz(32 * kc + 16 * hl, lane & 31);
+  for (int kc = 0; kc < NCK; ++kc)
+    va[kc] = (lane & 31) * VSTR + vt_swz<SW>(32 * kc + 16 * hl, lane & 31);
   const int32_t ka = (lane & 31) * KSTR + 16 * hl;
 
   const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
-  for (int32_t it = 0; it < n_tiles; ++it) {
+  // One tile: compute on LDS buffer it & 1 while staging tile it + 1 from
+  // `sx` into the other buffer and loading tile it + 3 into `sx`.
+  auto step = [&](int32_t it, Staged<D, INT4, SPLIT_KV> &sx) __attribute__((always_inline)) {
     const int buf = it & 1;
     const int32_t tb = tile_base(it);
     const uint8_t *kt = lds_k + buf * KBUF;
@@ -340,10 +378,15 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
     const bool is_sink_tile = tb < sink_end;
     bool any_vis = qw0 < p.Lq;
     if (causal)
-      any_vis = any_vis && tb <= wpos_hi && (is_sink_tile || tb + kTileKeys - 1 >= wpos_lo - p.W + 1);
-    const int32_t pg0 = s_pg[buf][0], pg1 = s_pg[buf][1], pg2 = s_pg[buf][2], pg3 = s_pg[buf][3];
-    const bool full = (pg0 | pg1 | pg2 | pg3) >= 0 && tb + kTileKeys <= kv_lim &&
-                      (causal ? (tb + kTileKeys - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
+      any_vis = any_vis && tb <= wpos_hi && (is_sink_tile || tb + TK - 1 >= wpos_lo - p.W + 1);
+    int32_t pgs[NCK], pg_all = 0;
+#pragma unroll
+    for (int k = 0; k < NCK; ++k) {
+      pgs[k] = s_pg[buf][k];
+      pg_all |= pgs[k];
+    }
+    const bool full = pg_all >= 0 && tb + TK <= kv_lim &&
+                      (causal ? (tb + TK - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
                       wq_last == qw0 + QW - 1;
 
     // S^T of one 32-key block (32 keys x 32 queries per query block; every K
@@ -366,12 +409,11 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
       for (int qb = 0; qb < QB; ++qb) {
         float16_t &s = sq[qb];
         if (!full) {
-          const int32_t pgl = (blk == 0) ? pg0 : pg2, pgh = (blk == 0) ? pg1 : pg3;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int R = 32 * blk + 8 * (r >> 2) + 4 * hl + (r & 3);
             const int32_t key = tb + row_key(R);
-            const bool ok = q_ok[qb] && ((r >> 3) ? pgh : pgl) >= 0 && key < kv_lim &&
+            const bool ok = q_ok[qb] && pgs[2 * blk + (r >> 3)] >= 0 && key < kv_lim &&
                             key_visible(key, qpos[qb], ctx, p.W, p.sinks, causal);
             s[r] = ok ? s[r] : -INFINITY;
           }
@@ -410,7 +452,7 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
       for (int db = 0; db < NDB; ++db) {
 #pragma unroll
         for (int g2 = 0; g2 < 2; ++g2) {
-          const int kc = (2 * blk + g2) ^ (2 * (db & 1));
+          const int kc = (2 * blk + g2) ^ ((SW / 16) * (db & 1));
           const half8_t a = *reinterpret_cast<const half8_t *>(vt + 32 * db * VSTR + va[kc]);
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
@@ -421,21 +463,27 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void prefill_kernel(const
 
     // Order: S(0) | staging of the next tile | softmax(0) | S(1) | PV(0) |
     // softmax(1) | PV(1): the staging VALU runs under S(0), softmax(1)
-    // under PV(0).
+    // under PV(0). 32-key tiles have block 0 only.
     float16_t sa[QB], sc[QB];
     half8_t pa[QB][2], pc[QB][2];
     if (any_vis) qk(0, sa);
-    if (it + 1 < n_tiles) commit(buf ^ 1);
-    if (it + 2 < n_tiles) issue(it + 2, pg_next);
-    pg_next = lookup(it + 3);
+    if (it + 1 < n_tiles) commit(buf ^ 1, sx);
+    if (it + 3 < n_tiles) issue(it + 3, pg_next, sx);
+    pg_next = lookup(it + 4);
     if (any_vis) {
       softmax(0, sa, pa);
-      qk(1, sc);
+      if constexpr (NBLK == 2) qk(1, sc);
       pv(0, pa);
-      softmax(1, sc, pc);
-      pv(1, pc);
+      if constexpr (NBLK == 2) {
+        softmax(1, sc, pc);
+        pv(1, pc);
+      }
     }
     __syncthreads();
+  };
+  for (int32_t it = 0; it < n_tiles; it += 2) {  // unrolled by two: static register sets
+    step(it, st1);
+    if (it + 1 < n_tiles) step(it + 1, st0);
   }
 
 #pragma unroll
@@ -487,18 +535,29 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
   p.sinks = d.num_sink_tokens < 0 ? 0 : d.num_sink_tokens;
   p.causal = d.causal;
   p.qk_scale_log2 = qk_scale_log2;
-  constexpr int NW = 4, QB = 1;
-  const int64_t n_wg = (int64_t)((d.q_len + 32 * QB * NW - 1) / (32 * QB * NW)) * d.num_heads * d.batch;
+  int nw = 4, tk = 64;
+  if (const char *e = std::getenv("MEMOPT_PREFILL_WAVES")) nw = std::atoi(e) == 8 ? 8 : 4;
+  if (const char *e = std::getenv("MEMOPT_PREFILL_TILE")) tk = std::atoi(e) == 32 ? 32 : 64;
+  if (tk == 32) nw = 4;
+  const int64_t n_wg = (int64_t)((d.q_len + 32 * nw - 1) / (32 * nw)) * d.num_heads * d.batch;
   MEMOPT_REQUIRE(n_wg < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "paged_attention: too many query tiles");
   const dim3 grid((unsigned)n_wg);
   const bool int4 = d.kv_format == MEMOPT_KV_INT4;
+#define MEMOPT_PREFILL_LAUNCH(D_, NW_, TK_)                                                                       \
+  do {                                                                                                          \
+    if (int4) hipLaunchKernelGGL((prefill_kernel<D_, true, NW_, 1, TK_>), grid, dim3(NW_ * 64), 0, stream, p);  \
+    else hipLaunchKernelGGL((prefill_kernel<D_, false, NW_, 1, TK_>), grid, dim3(NW_ * 64), 0, stream, p);      \
+  } while (0)
   if (d.head_dim == 128) {
-    if (int4) hipLaunchKernelGGL((prefill_kernel<128, true, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<128, false, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
+    if (tk == 32) MEMOPT_PREFILL_LAUNCH(128, 4, 32);
+    else if (nw == 8) MEMOPT_PREFILL_LAUNCH(128, 8, 64);
+    else MEMOPT_PREFILL_LAUNCH(128, 4, 64);
   } else {
-    if (int4) hipLaunchKernelGGL((prefill_kernel<64, true, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
-    else hipLaunchKernelGGL((prefill_kernel<64, false, NW, QB>), grid, dim3(NW * 64), 0, stream, p);
+    if (tk == 32) MEMOPT_PREFILL_LAUNCH(64, 4, 32);
+    else if (nw == 8) MEMOPT_PREFILL_LAUNCH(64, 8, 64);
+    else MEMOPT_PREFILL_LAUNCH(64, 4, 64);
   }
+#undef MEMOPT_PREFILL_LAUNCH
   return check_launch("paged_attention(prefill)");
 }
 
