@@ -100,32 +100,60 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Group-64 symmetric INT4 code of v with scale s (IEEE divide, roundf half
-// away from zero, +8 offset, clamp [0,15]) — TheRadDani/memopt-transformer-runtime
-// src/csrc/quantization.cu:183-186. NaN quotients give code 8, like the
-// float->int conversion of the reference (v_cvt_i32_f32(NaN) = 0).
-__device__ __forceinline__ uint32_t int4_code(float v, float s) {
-  const float r = roundf(v / s);
-  int iq = (int)r + 8;
-  iq = iq < 0 ? 0 : (iq > 15 ? 15 : iq);
-  return (uint32_t)iq;
+// Group-64 symmetric INT4 codes, TheRadDani/memopt-transformer-runtime
+// src/csrc/quantization.cu:168, :183-186: scale = absmax > 0 ? absmax / 7 : 1
+// (IEEE), code = clamp((int)roundf(v / scale) + 8, 0, 15) with roundf half
+// away from zero; NaN quotients give code 8, like the float->int conversion
+// of the reference (v_cvt_i32_f32(NaN) = 0).
+
+// Scale of a 64-element group whose absmax is spread over LANES consecutive
+// lanes (4 or 8, aligned): DPP max inside the lane group, then absmax / 7.
+template <int LANES>
+__device__ __forceinline__ float group_scale(float a) {
+  a = fmaxf(a, xor1(a));
+  a = fmaxf(a, xor2(a));
+  if (LANES == 8) a = fmaxf(a, half_mirror(a));
+  return (a > 0.0f) ? (a / 7.0f) : 1.0f;
+}
+
+// Codes of N elements with one scale, packed 8 per word (element i of word
+// k in bits 4i..4i+3, i.e. byte j = code[2j] | code[2j+1] << 4).
+// RN(v / scale) without a full IEEE division per element (Markstein): with
+// y = RN(1 / scale) from one IEEE division and q0 = RN(v * y) within an ulp
+// of v / scale, r = v - q0 * scale is exact in one fma and
+// RN(q0 + r * y) = RN(v / scale). No overflow or underflow is possible here
+// (|v| <= 65504, scale in [absmax / 7, 9358]); NaN/inf inputs still end in a
+// NaN quotient and code 8.
+template <int N>
+__device__ __forceinline__ void int4_pack(const float *v, float scale, uint32_t *w) {
+  const float y = 1.0f / scale;
+#pragma unroll
+  for (int k = 0; k < N / 8; ++k) {
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = v[8 * k + i];
+      const float q0 = __fmul_rn(x, y);
+      const float r = fmaf(-q0, scale, x);
+      const float q = fmaf(r, y, q0);
+      int iq = (int)roundf(q) + 8;
+      iq = iq < 0 ? 0 : (iq > 15 ? 15 : iq);
+      acc |= (uint32_t)iq << (4 * i);
+    }
+    w[k] = acc;
+  }
 }
 
 // Quantizes 8 consecutive elements (one 16-byte lane chunk of a 64-element
-// group spread over 8 lanes) into one packed word (element i in bits 4i..4i+3,
-// i.e. byte j = code[2j] | code[2j+1] << 4). Returns the packed word and sets
-// `scale` to the group's fp32 scale. Lanes 8k..8k+7 must hold one group.
+// group spread over 8 lanes) into one packed word and sets `scale` to the
+// group's fp32 scale. Lanes 8k..8k+7 must hold one group.
 __device__ __forceinline__ uint32_t quantize8(const float v[8], float &scale) {
   float a = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
-  a = fmaxf(a, xor1(a));
-  a = fmaxf(a, xor2(a));
-  a = fmaxf(a, half_mirror(a));
-  scale = (a > 0.0f) ? (a / 7.0f) : 1.0f;
-  uint32_t w = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) w |= int4_code(v[i], scale) << (4 * i);
+  scale = group_scale<8>(a);
+  uint32_t w;
+  int4_pack<8>(v, scale, &w);
   return w;
 }
 

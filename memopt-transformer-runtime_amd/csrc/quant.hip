@@ -155,6 +155,114 @@ __global__ __launch_bounds__(kThreads) void write_int4_kernel(
   }
 }
 
+// Fused write + quantize, one wave per (group of 16 tokens, head, K or V).
+//  * Full page: when the group's 16 slots are one aligned page (slot of token
+//    t0 + i = 16 P + i), the wave builds the (page, head) block in its page
+//    layout: lane l = 8p + c quantizes tokens p and p + 8 over the dims
+//    [c*D/8, (c+1)*D/8) and stores exactly the bytes it owns, K and V codes as
+//    one 16-byte (D = 128) or 8-byte (D = 64) store each, the group scales as
+//    one 4-byte store per token pair. 64-groups span 4 (D = 128) or 8 (D = 64)
+//    lanes.
+//  * Otherwise (decode appends, ragged tails, arbitrary slots) it scatters
+//    8-element chunks like write_int4_kernel.
+// 32-bit indexing: requires T * H * D < 2^31 (checked by the caller).
+template <int D>
+__global__ __launch_bounds__(kThreads) void write_int4_pages_kernel(
+    const half_t *__restrict__ keys, const half_t *__restrict__ values, uint8_t *__restrict__ pool,
+    const int32_t *__restrict__ slots, uint32_t T, uint32_t H, int64_t n_slots) {
+  constexpr int DPL = D / 8;    // dims per lane per token in the page layout
+  constexpr int GL = 64 / DPL;  // lanes per 64-group
+  constexpr int CPR = D / 8;    // 8-element chunks per (token, head) row
+  constexpr int KW = DPL / 8;   // packed words per token and lane
+  const Int4Page f(D);
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wid2 = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const bool is_v = wid2 & 1;  // wave-uniform
+  const uint32_t wid = wid2 >> 1;
+  const uint32_t g = wid / H, h = wid - g * H;
+  const uint32_t t0 = g * 16;
+  if (t0 >= T) return;  // wave-uniform
+  const size_t rowstride = (size_t)H * D;  // elements per token
+  const half_t *__restrict__ src = is_v ? values : keys;
+  const int64_t codes_off = is_v ? f.vcodes : f.kcodes, scales_off = is_v ? f.vscales : f.kscales;
+
+  int32_t sl = -1;
+  if (lane < 16 && t0 + lane < T) sl = slots[t0 + lane];
+  const int32_t s0 = __builtin_amdgcn_readfirstlane(sl);
+  const bool mine = lane >= 16 || sl == s0 + (int32_t)lane;
+  const bool full = __all(mine) && s0 >= 0 && (s0 & 15) == 0 && (int64_t)s0 + 16 <= n_slots;
+
+  if (full) {
+    const int p = lane >> 3, c = lane & 7;
+    const size_t off = (size_t)t0 * rowstride + (size_t)h * D + c * DPL;
+    float x[2][DPL];
+#pragma unroll
+    for (int tk = 0; tk < 2; ++tk) {
+      const size_t o = off + (size_t)(p + 8 * tk) * rowstride;
+#pragma unroll
+      for (int k = 0; k < KW; ++k) unpack_half8(*reinterpret_cast<const uint4 *>(src + o + 8 * k), &x[tk][8 * k]);
+    }
+    uint32_t wd[2][KW];
+    float sc[2];
+#pragma unroll
+    for (int tk = 0; tk < 2; ++tk) {
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) a = fmaxf(a, fabsf(x[tk][i]));
+      sc[tk] = group_scale<GL>(a);
+      int4_pack<DPL>(x[tk], sc[tk], wd[tk]);
+    }
+    uint8_t *blk = pool + ((int64_t)(s0 >> 4) * H + h) * f.block;
+    uint32_t out[2 * KW];
+    if (!is_v) {
+      // K: token p's bytes, then token p + 8's
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        out[k] = wd[0][k];
+        out[KW + k] = wd[1][k];
+      }
+    } else {
+      // V unit u (4 dims) = 2 bytes of token p, then 2 bytes of token p + 8
+#pragma unroll
+      for (int u = 0; u < 2 * KW; ++u) {
+        const uint32_t lo = wd[0][u >> 1] >> (16 * (u & 1)), hi = wd[1][u >> 1] >> (16 * (u & 1));
+        out[u] = (lo & 0xFFFFu) | (hi << 16);
+      }
+    }
+    if constexpr (D == 128)
+      *reinterpret_cast<uint4 *>(blk + codes_off + lane * f.BPL) = make_uint4(out[0], out[1], out[2], out[3]);
+    else
+      *reinterpret_cast<uint2 *>(blk + codes_off + lane * f.BPL) = make_uint2(out[0], out[1]);
+    if (c % GL == 0)
+      *reinterpret_cast<uint32_t *>(blk + scales_off + 2 * f.scale_idx(p, (c * DPL) / 64)) =
+          as_u32(half2_t{(half_t)sc[0], (half_t)sc[1]});
+    return;
+  }
+
+#pragma unroll
+  for (int u = 0; u < 16 * CPR / 64; ++u) {
+    const uint32_t j = u * 64 + lane;
+    const uint32_t t = t0 + j / CPR, cc = j % CPR;
+    if (t >= T) continue;  // a token's CPR (>= 8) chunks leave together: 64-groups stay whole
+    float x[8];
+    unpack_half8(*reinterpret_cast<const uint4 *>(src + (size_t)t * rowstride + (size_t)h * D + cc * 8), x);
+    float sc;
+    const uint32_t w = quantize8(x, sc);
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= n_slots) continue;
+    const int32_t pos = (int32_t)(slot & 15), d0 = 8 * (int32_t)cc;
+    uint8_t *blk = pool + ((slot >> 4) * H + h) * f.block;
+    if (!is_v) {
+      *reinterpret_cast<uint32_t *>(blk + f.kcodes + f.k_byte(pos, d0)) = w;
+    } else {
+      uint8_t *vb = blk + f.vcodes + f.v_byte(pos, d0);
+      *reinterpret_cast<uint16_t *>(vb) = (uint16_t)(w & 0xFFFFu);
+      *reinterpret_cast<uint16_t *>(vb + 4) = (uint16_t)(w >> 16);
+    }
+    if ((d0 & 63) == 0) reinterpret_cast<half_t *>(blk + scales_off)[f.scale_idx(pos, d0 >> 6)] = (half_t)sc;
+  }
+}
+
 }  // namespace memopt
 
 using namespace memopt;
@@ -238,7 +346,18 @@ int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
   } else {
     const int64_t n = num_tokens * row / 8;
     const bool vec = aligned(keys, 16) && aligned(values, 16);
-    if (vec)
+    if (vec && num_tokens * row < (1LL << 31) && (head_dim == 64 || head_dim == 128)) {
+      const int64_t waves = (num_tokens + 15) / 16 * num_heads * 2;
+      const unsigned grid = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
+      if (head_dim == 128)
+        hipLaunchKernelGGL(write_int4_pages_kernel<128>, dim3(grid), dim3(kThreads), 0, s, (const half_t *)keys,
+                           (const half_t *)values, (uint8_t *)p.key, slot_mapping, (uint32_t)num_tokens,
+                           (uint32_t)num_heads, n_slots);
+      else
+        hipLaunchKernelGGL(write_int4_pages_kernel<64>, dim3(grid), dim3(kThreads), 0, s, (const half_t *)keys,
+                           (const half_t *)values, (uint8_t *)p.key, slot_mapping, (uint32_t)num_tokens,
+                           (uint32_t)num_heads, n_slots);
+    } else if (vec)
       hipLaunchKernelGGL(write_int4_kernel<true>, dim3(grid_for(n)), dim3(kThreads), 0, s,
                          (const half_t *)keys, (const half_t *)values, (uint8_t *)p.key, slot_mapping, n,
                          num_heads, head_dim, n_slots);

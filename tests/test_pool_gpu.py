@@ -75,6 +75,28 @@ def test_write_cache_int4_pages_bit_exact(D):
     assert gk.shape == (nb, H, 8 * D) and gv.shape == (nb, H, 8 * D)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("order", ["scrambled", "shifted"])
+def test_write_cache_int4_scatter_orders_bit_exact(D, order):
+    """Slots that do not form aligned 16-token pages (scrambled across the pool,
+    or pages filled from position 1) take the chunk-scatter path; groups that
+    do form a page take the page path; both must give the oracle's bytes."""
+    rng = np.random.default_rng(2)
+    nb, bs, H, T = 12, 16, 3, 130
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    k = (rng.standard_normal((T, H, D)) * np.where(rng.random((T, H, D)) < 0.01, 8, 1)).astype(np.float16)
+    v = rng.standard_normal((T, H, D)).astype(np.float16)
+    if order == "scrambled":
+        slots = rng.permutation(nb * bs)[:T].astype(np.int32)
+    else:
+        slots = (np.arange(T) + 1).astype(np.int32)  # every group straddles two pages
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)), to_dev(slots))
+    wk, wv = np.zeros((nb, bs, H, D), np.float16), np.zeros((nb, bs, H, D), np.float16)
+    O.write_cache(wk, k, slots)
+    O.write_cache(wv, v, slots)
+    same_bits(memopt_C.get_int4_pages(), O.to_int4_pages(wk, wv))
+
+
 def test_write_cache_out_of_bounds_raises():
     memopt_C.init_pool(2, 16, 2, 64)
     k = torch.zeros(1, 2, 64, dtype=torch.float16, device=dev())
