@@ -142,6 +142,8 @@ def _clib():
         lib.oracle_quantize_int4.restype = None
         lib.oracle_dequantize_int4.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
         lib.oracle_dequantize_int4.restype = None
+        lib.oracle_markstein_mismatches.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64]
+        lib.oracle_markstein_mismatches.restype = ctypes.c_int64
         _CLIB = lib
     return _CLIB
 
@@ -164,6 +166,15 @@ def dequantize_int4_c(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     _clib().oracle_dequantize_int4(p.ctypes.data, s.ctypes.data, s.size, out.ctypes.data)
     shape = tuple(packed.shape[:-1]) + (packed.shape[-1] * 2,)
     return out.astype(np.float16).reshape(shape)
+
+
+def markstein_mismatches(values: np.ndarray, scales: np.ndarray) -> int:
+    """Checker of the device quantizer's division shortcut (oracle/quant_ref.c):
+    number of (v, s) pairs, |v| <= 7 s, whose fma-refined quotient differs
+    from the IEEE quotient v / s in value."""
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    sc = np.ascontiguousarray(scales, dtype=np.float32)
+    return int(_clib().oracle_markstein_mismatches(v.ctypes.data, v.size, sc.ctypes.data, sc.size))
 
 
 # ---------------------------------------------------------------------------

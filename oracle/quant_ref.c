@@ -45,3 +45,30 @@ void oracle_dequantize_int4(const uint8_t *packed, const float *scales,
     }
   }
 }
+
+/*
+ * Checker for the division shortcut of the device quantizer (not part of the
+ * reference): for each scale s[j] and every finite fp16 value v with
+ * |v| <= 7 * s[j] (given as fp32 in `v`), compares the Markstein quotient
+ *   y = RN(1/s); q0 = RN(v*y); r = fma(-q0, s, v); q = fma(r, y, q0)
+ * with the IEEE quotient RN(v/s) by value (the shortcut turns -0 into +0;
+ * both give code 8). Returns the number of mismatches (0 expected).
+ */
+int64_t oracle_markstein_mismatches(const float *v, int64_t nv, const float *s, int64_t ns) {
+  int64_t bad = 0;
+  for (int64_t j = 0; j < ns; ++j) {
+    const float sc = s[j];
+    const float y = 1.0f / sc;
+    const float lim = 7.0f * sc * 1.0001f;
+    for (int64_t i = 0; i < nv; ++i) {
+      const float x = v[i];
+      if (fabsf(x) > lim) continue;
+      const float q0 = x * y;
+      const float r = fmaf(-q0, sc, x);
+      const float q = fmaf(r, y, q0);
+      const float want = x / sc;
+      if (q != want) ++bad;
+    }
+  }
+  return bad;
+}

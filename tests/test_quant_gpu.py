@@ -176,3 +176,51 @@ def test_dequant_error_scales_mismatch():
     p, s = memopt_C.quantize_kv_cache_int4(make((4, 128), "uniform_unit").to(dev()), G)
     with pytest.raises(RuntimeError):
         memopt_C.dequantize_kv_cache_int4(p, s[:-1].contiguous(), G)
+
+
+def _boundary_groups(seed=31, n_scales=400):
+    """Groups whose elements sit on, and 1-3 fp16 ulps around, every rounding
+    boundary (k + 0.5) * scale of the group's own scale, for many absmax values:
+    the inputs where an inexact quotient v / scale would flip a code."""
+    rng = np.random.default_rng(seed)
+    groups = []
+    for _ in range(n_scales):
+        a = np.float16(rng.uniform(1e-3, 200.0) * rng.choice([1, -1]))
+        s = np.float32(abs(np.float32(a))) / np.float32(7.0)
+        vals = []
+        for k in range(-7, 7):
+            mid = np.float16(np.float32(k + 0.5) * s)
+            for d in (-3, -2, -1, 0, 1, 2, 3):
+                v = np.nextafter(mid, np.float16(np.inf if d > 0 else -np.inf), dtype=np.float16) if d else mid
+                for _ in range(abs(d) - 1 if d else 0):
+                    v = np.nextafter(v, np.float16(np.inf if d > 0 else -np.inf), dtype=np.float16)
+                if abs(np.float32(v)) <= abs(np.float32(a)):
+                    vals.append(v)
+        vals = np.array(vals, np.float16)
+        for i in range(0, len(vals), 63):
+            g = np.zeros(64, np.float16)
+            g[0] = a
+            chunk = vals[i:i + 63]
+            g[1:1 + len(chunk)] = chunk
+            groups.append(g)
+    return np.stack(groups)
+
+
+def test_quantize_rounding_boundaries_bit_exact():
+    """Codes at (and next to) the .5 boundaries of v / scale equal the oracle's
+    (IEEE division + roundf), through the surface quantize and write_cache."""
+    x = _boundary_groups()
+    want_p, want_s = O.quantize_int4(x)
+    got_p, got_s = memopt_C.quantize_kv_cache_int4(to_dev(x), 64)
+    same_bits(got_p, want_p)
+    same_bits(got_s, want_s)
+    # same groups through the fused page writer (rows of [tokens, 1 head, 64])
+    T = x.shape[0] - x.shape[0] % 16
+    rows = x[:T].reshape(T, 1, 64)
+    nb = T // 16
+    memopt_C.init_pool(nb, 16, 1, 64, kv_format="int4")
+    slots = np.arange(T, dtype=np.int32)
+    memopt_C.write_cache(to_dev(rows), to_dev(rows[::-1].copy()), to_dev(np.zeros((1, 1), np.int32)), to_dev(slots))
+    wk = rows.reshape(nb, 16, 1, 64)
+    wv = rows[::-1].reshape(nb, 16, 1, 64)
+    same_bits(memopt_C.get_int4_pages(), O.to_int4_pages(wk, wv))
