@@ -227,6 +227,7 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
     dev = torch.device("cuda", 0)
     nbps = ctx // bs
     nb = copies * B * nbps + cfg.get("spare_pages", 0)
+    memopt_C.init_pool(1, bs, H, D, kv_format="int4")  # identical parameters would keep the old free list
     memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
     if fifo_trace:
         # allocate everything, free it in a seeded random order, then allocate
