@@ -67,6 +67,18 @@ __device__ __forceinline__ float half_mirror(float v) { return dpp_f32<0x141>(v)
 // Generic wave64 butterfly through the LDS crossbar (ds_bpermute / swizzle).
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// v(lane) + v(lane ^ 16) and v(lane) + v(lane ^ 32) in registers (gfx950
+// v_permlane16_swap / v_permlane32_swap: the two results of a swap of v with
+// itself hold both lanes of each pair).
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // v_bfi_b32: (mask & a) | (~mask & b) in one VALU op. The compiler splits the

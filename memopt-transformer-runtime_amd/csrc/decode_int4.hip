@@ -225,15 +225,15 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_kernel(const DecodeParams
   // m is wave-uniform, so partials add directly. l counts each token once per c.
   l += dpp_f32<0x124>(l);  // row_ror:4
   l += dpp_f32<0x128>(l);  // row_ror:8
-  l += shfl_xor(l, 16);
-  l += shfl_xor(l, 32);
+  l = xor16_sum(l);
+  l = xor32_sum(l);
 #pragma unroll
   for (int d = 0; d < DPL; ++d) {
     float v = acc[d];
     v += dpp_f32<0x124>(v);
     v += dpp_f32<0x128>(v);
-    v += shfl_xor(v, 16);
-    v += shfl_xor(v, 32);
+    v = xor16_sum(v);
+    v = xor32_sum(v);
     acc[d] = v;
   }
   if (t == 0) {
@@ -443,14 +443,14 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
   for (int d = 0; d < DPL; ++d) acc[d] = fmaf(-((d & 1) ? 72.0f : 1032.0f), wsum, acc[d]);
   // Sum the 8 token-pair lanes sharing this lane's dims (lanes c, c+8, ...).
   l += dpp_f32<0x128>(l);  // row_ror:8
-  l += shfl_xor(l, 16);
-  l += shfl_xor(l, 32);
+  l = xor16_sum(l);
+  l = xor32_sum(l);
 #pragma unroll
   for (int d = 0; d < DPL; ++d) {
     float v = acc[d];
     v += dpp_f32<0x128>(v);
-    v += shfl_xor(v, 16);
-    v += shfl_xor(v, 32);
+    v = xor16_sum(v);
+    v = xor32_sum(v);
     acc[d] = v;
   }
   if (pp == 0) {
