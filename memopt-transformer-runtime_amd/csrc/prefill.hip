@@ -182,20 +182,28 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
         } else {
           v = n;
         }
+        // scores come out of the MFMA in log2 units: Q is pre-scaled by
+        // log2(e) / sqrt(D) (an extra fp16 rounding of q, ~2^-12 relative)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] * cs);
       }
       qf[qb][c] = v;
     }
   }
 
   float16_t o[QB][NDB];
-  float m[QB], negm[QB], lsum[QB];  // m: running max of scaled scores
+  // m: running max of the scores (log2 units), -inf until the first visible
+  // key. The S accumulators start from `mtile` = -m (0 while m is -inf), so
+  // the MFMA returns score - m directly.
+  float m[QB], lsum[QB];
+  float16_t mtile[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
     for (int i = 0; i < NDB; ++i) o[qb][i] = (float16_t){};
     m[qb] = -INFINITY;
-    negm[qb] = 0.0f;
     lsum[qb] = 0.0f;
+    mtile[qb] = (float16_t){};
   }
 
   // ---- key tiles visited by this workgroup: sink tiles, then window tiles ----
@@ -392,14 +400,26 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
     // S^T of one 32-key block (32 keys x 32 queries per query block; every K
     // fragment feeds all QB query blocks).
     auto qk = [&](int blk, float16_t (&sq)[QB]) __attribute__((always_inline)) {
+      if constexpr (INT4) {  // all K-fragment reads first, then the MFMA chain
+        half8_t a[NCH];
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) sq[qb] = (float16_t){};
+        for (int c = 0; c < NCH; ++c) a[c] = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KSTR + ka + 32 * c);
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const half8_t a = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KSTR + ka + 32 * c);
+        for (int c = 0; c < NCH; ++c) {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          sq[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qb][c], sq[qb], 0, 0, 0);
+          for (int qb = 0; qb < QB; ++qb)
+            sq[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[qb][c], c == 0 ? mtile[qb] : sq[qb], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, NCH, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NCH * QB, 0);
+      } else {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const half8_t a = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KSTR + ka + 32 * c);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            sq[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qb][c], c == 0 ? mtile[qb] : sq[qb], 0, 0, 0);
+        }
       }
     };
     // Masks, raises the running max lazily, and packs the probabilities of
@@ -418,27 +438,35 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
             s[r] = ok ? s[r] : -INFINITY;
           }
         }
-        float tmax = s[0];
+        float tmax = s[0];  // relative to m (absolute while m is -inf)
 #pragma unroll
         for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
-        tmax = half_max(tmax) * cs;
-        if (__any(tmax > m[qb] + 8.0f)) {  // lazy rescale: p stays <= 2^8 between raises
-          const float mn = fmaxf(m[qb], tmax);
+        tmax = half_max(tmax);
+        // lazy rescale: p stays <= 2^8 between raises; the first visible key
+        // always raises
+        const bool raise = (m[qb] == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
+        if (__any(raise)) {
+          const float base = (m[qb] == -INFINITY) ? 0.0f : m[qb];
+          const float mn = fmaxf(m[qb], base + tmax);
           const float alpha = (mn == m[qb]) ? 1.0f : fast_exp2(m[qb] - mn);
+          const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
           lsum[qb] *= alpha;
 #pragma unroll
           for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qb][db][r] *= alpha;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[r] -= delta;
           m[qb] = mn;
-          negm[qb] = (mn == -INFINITY) ? 0.0f : -mn;
+          const float nb = (mn == -INFINITY) ? 0.0f : -mn;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mtile[qb][r] = nb;
         }
 #pragma unroll
         for (int g2 = 0; g2 < 2; ++g2) {
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
-            const half2_t pp2 = {(half_t)fast_exp2(fmaf(s[8 * g2 + e], cs, negm[qb])),
-                                 (half_t)fast_exp2(fmaf(s[8 * g2 + e + 1], cs, negm[qb]))};
+            const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e]), (half_t)fast_exp2(s[8 * g2 + e + 1])};
             lsum[qb] = __builtin_amdgcn_fdot2(pp2, ones, lsum[qb], false);
             pb[qb][g2][e] = pp2.x;
             pb[qb][g2][e + 1] = pp2.y;
@@ -448,15 +476,37 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
     };
     // O^T += V^T P^T over one block's two 16-key chunks
     auto pv = [&](int blk, half8_t (&pb)[QB][2]) __attribute__((always_inline)) {
+      if constexpr (INT4) {
+        // all V^T-fragment reads first, then the MFMAs (the fp16 path has no
+        // registers to spare for this)
+        half8_t a[NDB][2];
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-          const int kc = (2 * blk + g2) ^ ((SW / 16) * (db & 1));
-          const half8_t a = *reinterpret_cast<const half8_t *>(vt + 32 * db * VSTR + va[kc]);
+          for (int g2 = 0; g2 < 2; ++g2) {
+            const int kc = (2 * blk + g2) ^ ((SW / 16) * (db & 1));
+            a[db][g2] = *reinterpret_cast<const half8_t *>(vt + 32 * db * VSTR + va[kc]);
+          }
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[qb][g2], o[qb][db], 0, 0, 0);
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+              o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[db][g2], pb[qb][g2], o[qb][db], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NDB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * NDB * QB, 0);
+      } else {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+          for (int g2 = 0; g2 < 2; ++g2) {
+            const int kc = (2 * blk + g2) ^ ((SW / 16) * (db & 1));
+            const half8_t a = *reinterpret_cast<const half8_t *>(vt + 32 * db * VSTR + va[kc]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+              o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[qb][g2], o[qb][db], 0, 0, 0);
+          }
         }
       }
     };
