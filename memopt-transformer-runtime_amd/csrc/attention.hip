@@ -195,6 +195,7 @@ int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes
     int32_t splits;
     return decode_workspace(*desc, &splits, bytes);
   }
+  if (desc->batch > 0 && prefill_supported(*desc)) *bytes = prefill_workspace_bytes(*desc);
   return MEMOPT_OK;
 }
 

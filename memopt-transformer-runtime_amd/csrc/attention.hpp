@@ -54,6 +54,8 @@ int launch_decode_int4(const DecodeParams &p, int32_t batch, int32_t D, int32_t 
 // Multi-query (q_len >= 16) MFMA kernel over INT4 page pools or contiguous
 // fp16 pools with 16-multiple pages and D in {64, 128}.
 bool prefill_supported(const memopt_attn_desc &d);
+// Workspace of the staged prefill path (0: the path stages in-kernel).
+int64_t prefill_workspace_bytes(const memopt_attn_desc &d);
 int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hipStream_t stream);
 
 }  // namespace memopt

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_kernel(const DecodeParams
       }
       const float pw = valid ? fast_exp2(s - m) : 0.0f;
       l += pw;
-      const float wv = pw * sv[u];
+      const float wv = valid ? pw * sv[u] : 0.0f;  // a scale past the context may be NaN
 #pragma unroll
       for (int k = 0; k < NWORD; ++k) {
         half2_t hv[4];
@@ -390,10 +390,13 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
       const int32_t tok0 = bt.lp[u] * 16;
       const bool full = bt.ok[u] && tok0 >= kr.win_lo && tok0 + 16 <= kr.hi;
       bool v0 = full, v1 = full;
+      half2_t sv = bt.sv[u];
       if (!full) {  // wave-uniform
         const int32_t t0 = tok0 + pp, t1 = t0 + 8;
         v0 = bt.ok[u] && t0 < kr.hi && (t0 >= kr.win_lo || t0 < kr.sink_end);
         v1 = bt.ok[u] && t1 < kr.hi && (t1 >= kr.win_lo || t1 < kr.sink_end);
+        // Masked tokens may carry any scale bits (NaN past the context).
+        sv = half2_t{v0 ? sv.x : (half_t)0.0f, v1 ? sv.y : (half_t)0.0f};
       }
       s0 = v0 ? s0 * p.qk_scale_log2 : -INFINITY;
       s1 = v1 ? s1 * p.qk_scale_log2 : -INFINITY;
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
       const float p0 = v0 ? fast_exp2(s0 - m) : 0.0f;
       const float p1 = v1 ? fast_exp2(s1 - m) : 0.0f;
       l += p0 + p1;
-      const half2_t wpair = {(half_t)(p0 * (float)bt.sv[u].x), (half_t)(p1 * (float)bt.sv[u].y)};
+      const half2_t wpair = {(half_t)(p0 * (float)sv.x), (half_t)(p1 * (float)sv.y)};
       wsum = __builtin_amdgcn_fdot2(wpair, kOnes, wsum, false);
 #pragma unroll
       for (int k = 0; k < VW; ++k) {

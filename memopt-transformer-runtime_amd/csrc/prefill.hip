@@ -252,6 +252,9 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
     // zero scale, fp16 through a select.
     const bool ok = pg >= 0;
     const int64_t pgs = ok ? pg : 0;
+    // V of tokens at or past the context length stages as zeros (a page's
+    // unused tail may hold NaN bits, and P = 0 must not meet them in PV).
+    const bool ok0 = ok && key + sk_pp < kv_lim, ok1 = ok && key + sk_pp + 8 < kv_lim;
     if constexpr (INT4) {
       const Int4Page f(D);
       const uint8_t *blk = p.pool + (pgs * p.H + h) * f.block;
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
           st.w[St::VO] = vv.x; st.w[St::VO + 1] = vv.y;
         }
         const uint32_t sv = *reinterpret_cast<const uint32_t *>(blk + f.vscales + 2 * (g * 16 + 2 * sk_pp));
-        st.sc[St::VS] = ok ? sv : 0u;
+        st.sc[St::VS] = (ok0 ? sv & 0xFFFFu : 0u) | (ok1 ? sv & 0xFFFF0000u : 0u);
       }
     } else {
       const half_t *kp = reinterpret_cast<const half_t *>(p.pool);
@@ -296,8 +299,8 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
         if (do_v) {
           const u32x4 v0 = *reinterpret_cast<const u32x4 *>(vp + r0 + 8 * i);
           const u32x4 v1 = *reinterpret_cast<const u32x4 *>(vp + r1 + 8 * i);
-          st.r[St::VR + i] = ok ? v0 : z;
-          st.r[St::VR + DPT / 8 + i] = ok ? v1 : z;
+          st.r[St::VR + i] = ok0 ? v0 : z;
+          st.r[St::VR + DPT / 8 + i] = ok1 ? v1 : z;
         }
       }
     }
@@ -556,6 +559,385 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Staged variant: a pre-pass writes every 16-token chunk a call can touch in
+// the exact LDS operand layout (K rows in page pair order with dims in unpack
+// order, V^T columns in PV operand order), so the attention kernel fills LDS
+// with global_load_lds (16 bytes per lane, no VGPRs, no VALU) and spends its
+// VALU on the softmax only.
+// ---------------------------------------------------------------------------
+
+// Column of token p (p = 0..7) inside a 16-token chunk of V^T; token p + 8 is
+// the next column (vt_col of K-tile row 2p).
+__device__ __forceinline__ int chunk_vcol(int p) { return 8 * ((p >> 1) & 1) + 4 * (p >> 2) + 2 * (p & 1); }
+
+// Workspace block of one (sequence, 16-token chunk, head): 2*16*D fp16 =
+// K part [16 rows][D] then V^T part [D rows][16 columns]; followed, after all
+// blocks, by one int32 per (sequence, chunk): 1 if its page is linked.
+template <int D>
+struct StageLayout {
+  static constexpr int64_t kBlock = 2 * 16 * D * 2;  // bytes
+  static constexpr int64_t kVPart = 16 * D * 2;      // byte offset of V^T in a block
+};
+
+// One wave per (sequence b, chunk lc, head h); lane l = 8p + c owns tokens
+// (p, p + 8) x dims [c*D/8, (c+1)*D/8), as in the INT4 page format.
+template <int D, bool INT4>
+__global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams p, uint8_t *__restrict__ ws,
+                                                            int32_t MC, int32_t units) {
+  constexpr int DPL = D / 8;
+  using L = StageLayout<D>;
+  const int lane = threadIdx.x & 63;
+  const int32_t unit = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= units) return;  // wave-uniform
+  const int32_t h = unit % p.H, bl = unit / p.H, lc = bl % MC, b = bl / MC;
+  const int pp = lane >> 3, c = lane & 7;
+  const int32_t kv_lim = min(p.ctx[b], p.M * p.bs);
+  const int32_t key0 = lc * 16;
+  int32_t pg = -1;
+  if (key0 < kv_lim) {
+    const int32_t e = p.bt[(int64_t)b * p.M + key0 / p.bs];
+    pg = (e >= 0 && e < p.nb) ? e : -1;
+  }
+  uint8_t *blk = ws + (int64_t)unit * L::kBlock;
+  uint32_t kw0[DPL / 2], kw1[DPL / 2];  // K halves of tokens pp, pp + 8 (unpack order), as packed pairs
+  uint32_t vw[DPL];                     // V: dim d -> {token pp, token pp + 8}
+  if (pg < 0) {
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) kw0[i] = kw1[i] = 0;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) vw[i] = 0;
+  } else if constexpr (INT4) {
+    const Int4Page f(D);
+    const uint8_t *src = p.pool + ((int64_t)pg * p.H + h) * f.block;
+    const int slot = 8 * pp + c, g = (c * DPL) / 64;
+    const half2_t sk = as_half2(*reinterpret_cast<const uint32_t *>(src + f.kscales + 2 * (g * 16 + 2 * pp)));
+    const half2_t sv = as_half2(*reinterpret_cast<const uint32_t *>(src + f.vscales + 2 * (g * 16 + 2 * pp)));
+    const half2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f}, b72 = {(half_t)72.0f, (half_t)72.0f};
+    const uint32_t *kc32 = reinterpret_cast<const uint32_t *>(src + f.kcodes + slot * f.BPL);
+    const uint32_t *vc32 = reinterpret_cast<const uint32_t *>(src + f.vcodes + slot * f.BPL);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const half2_t s2 = t2 ? half2_t{sk.y, sk.y} : half2_t{sk.x, sk.x};
+      uint32_t *dst = t2 ? kw1 : kw0;
+#pragma unroll
+      for (int wi = 0; wi < DPL / 8; ++wi) {
+        const uint32_t w = kc32[t2 * (DPL / 8) + wi], w8 = w >> 8;
+        dst[4 * wi + 0] = as_u32((as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * s2);
+        dst[4 * wi + 1] = as_u32((as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * s2);
+        dst[4 * wi + 2] = as_u32((as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * s2);
+        dst[4 * wi + 3] = as_u32((as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * s2);
+      }
+    }
+#pragma unroll
+    for (int wi = 0; wi < DPL / 4; ++wi) {
+      const uint32_t w = vc32[wi], w8 = w >> 8;
+      vw[4 * wi + 0] = as_u32((as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * sv);
+      vw[4 * wi + 1] = as_u32((as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * sv);
+      vw[4 * wi + 2] = as_u32((as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * sv);
+      vw[4 * wi + 3] = as_u32((as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * sv);
+    }
+  } else {
+    const half_t *kp = reinterpret_cast<const half_t *>(p.pool);
+    const half_t *vp = reinterpret_cast<const half_t *>(p.vpool);
+    const int32_t pos0 = key0 % p.bs;  // a 16-token chunk lies in one page (bs % 16 == 0)
+    const int64_t r0 = (((int64_t)pg * p.bs + pos0 + pp) * p.H + h) * D + c * DPL;
+    const int64_t r1 = r0 + 8LL * p.H * D;
+#pragma unroll
+    for (int i = 0; i < DPL / 8; ++i) {
+      const half8_t k0 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(kp + r0 + 8 * i));
+      const half8_t k1 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(kp + r1 + 8 * i));
+      const half8_t v0 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(vp + r0 + 8 * i));
+      const half8_t v1 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(vp + r1 + 8 * i));
+      // K in unpack order (0,4,1,5,2,6,3,7) within each 8-dim group
+      kw0[4 * i + 0] = as_u32(half2_t{k0[0], k0[4]}); kw0[4 * i + 1] = as_u32(half2_t{k0[1], k0[5]});
+      kw0[4 * i + 2] = as_u32(half2_t{k0[2], k0[6]}); kw0[4 * i + 3] = as_u32(half2_t{k0[3], k0[7]});
+      kw1[4 * i + 0] = as_u32(half2_t{k1[0], k1[4]}); kw1[4 * i + 1] = as_u32(half2_t{k1[1], k1[5]});
+      kw1[4 * i + 2] = as_u32(half2_t{k1[2], k1[6]}); kw1[4 * i + 3] = as_u32(half2_t{k1[3], k1[7]});
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vw[8 * i + e] = as_u32(half2_t{v0[e], v1[e]});
+    }
+  }
+  // Tokens at or past the context length stage as zeros: a page's unused
+  // tail may hold any bits (NaN included), and P = 0 must not meet them in PV.
+  if (key0 + pp >= kv_lim) {
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) kw0[i] = 0;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) vw[i] &= 0xFFFF0000u;
+  }
+  if (key0 + pp + 8 >= kv_lim) {
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) kw1[i] = 0;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) vw[i] &= 0x0000FFFFu;
+  }
+  // V dims come out of the INT4 unpack in order d, d+1, d+2, d+3 per word; K
+  // words are already in unpack order for both sources.
+  uint8_t *krow0 = blk + (2 * pp) * (2 * D) + c * DPL * 2;
+#pragma unroll
+  for (int i = 0; i < DPL / 8; ++i) {
+    *reinterpret_cast<u32x4 *>(krow0 + 16 * i) = u32x4{kw0[4 * i], kw0[4 * i + 1], kw0[4 * i + 2], kw0[4 * i + 3]};
+    *reinterpret_cast<u32x4 *>(krow0 + 2 * D + 16 * i) =
+        u32x4{kw1[4 * i], kw1[4 * i + 1], kw1[4 * i + 2], kw1[4 * i + 3]};
+  }
+  const int vc = chunk_vcol(pp);
+#pragma unroll
+  for (int d = 0; d < DPL; ++d)
+    *reinterpret_cast<uint32_t *>(blk + L::kVPart + (c * DPL + d) * 32 + vc * 2) = vw[d];
+  if (h == 0 && lane == 0)
+    reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + lc] = pg >= 0 ? 1 : 0;
+}
+
+// 16-byte buffer -> LDS copy: lane i's bytes (buffer offset voff + soff)
+// land at lds_base + 16 i. Kept out of the kernel template: the host pass of
+// a template that names the builtin directly drops the kernel's launch stub.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, void *lds_base, uint32_t voff,
+                                                  uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_base, 16, (int)voff,
+                                           (int)soff, 0, 0);
+}
+
+// Attention over staged chunks: 4 waves x 32 queries, 64-key tiles filled by
+// global_load_lds into unpadded LDS rows whose 16-byte chunks are
+// XOR-swizzled (K: chunk ^ (row & 15) for 256-byte rows, chunk ^ ((row >> 1)
+// & 7) for 128-byte rows; V^T: chunk ^ ((row >> 1) & 7)), which keeps the
+// MFMA operand reads free of bank conflicts.
+template <int D>
+__global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillParams p, const uint8_t *__restrict__ ws,
+                                                                int32_t MC, int32_t units) {
+  constexpr int NW = 4, TK = 64, NCK = 4;
+  constexpr int KRB = 2 * D;      // K row bytes
+  constexpr int KC = KRB / 16;    // 16-byte chunks per K row
+  constexpr int VRB = TK * 2;     // V^T row bytes
+  constexpr int KBUF = TK * KRB, VBUF = D * VRB;
+  constexpr int NCH = D / 16, NDB = D / 32;
+  using L = StageLayout<D>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k[2 * KBUF];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_v[2 * VBUF];
+  __shared__ int32_t s_pg[2][NCK];
+
+  auto kswz = [](int R) { return KC == 16 ? (R & 15) : ((R >> 1) & 7); };
+
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int32_t nqt = (p.Lq + 32 * NW - 1) / (32 * NW);
+  int32_t wg = blockIdx.x;
+  const int32_t n8 = (int32_t)(gridDim.x & ~7u);
+  if (wg < n8) wg = (wg & 7) * (n8 >> 3) + (wg >> 3);
+  const int32_t qt = nqt - 1 - wg % nqt;
+  const int32_t h = (wg / nqt) % p.H, b = wg / (nqt * p.H);
+  const int32_t ctx = p.ctx[b];
+  const int32_t kv_lim = min(ctx, p.M * p.bs);
+  const int32_t q0 = qt * 32 * NW;
+  const int32_t qw0 = q0 + 32 * wave;
+  const bool causal = p.causal != 0;
+  const float cs = p.qk_scale_log2;
+  const int32_t qi = qw0 + (lane & 31);
+  const bool q_ok = qi < p.Lq;
+  const int32_t qpos = ctx - p.Lq + qi;
+
+  half8_t qf[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    half8_t v = {};
+    if (q_ok) {
+      const half8_t n = __builtin_bit_cast(
+          half8_t, *reinterpret_cast<const uint4 *>(p.q + (((int64_t)b * p.Lq + qi) * p.H + h) * D + 16 * c + 8 * hl));
+      v[0] = n[0]; v[1] = n[4]; v[2] = n[1]; v[3] = n[5];
+      v[4] = n[2]; v[5] = n[6]; v[6] = n[3]; v[7] = n[7];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] * cs);
+    }
+    qf[c] = v;
+  }
+  float16_t o[NDB];
+#pragma unroll
+  for (int i = 0; i < NDB; ++i) o[i] = (float16_t){};
+  float m = -INFINITY, lsum = 0.0f;
+  float16_t mtile = (float16_t){};
+
+  const int32_t qlast = min(q0 + 32 * NW, p.Lq) - 1;
+  const int32_t pos_lo = ctx - p.Lq + q0, pos_hi = ctx - p.Lq + qlast;
+  const int32_t hi = max(0, causal ? min(kv_lim, pos_hi + 1) : kv_lim);
+  const int32_t win_lo = max(0, causal ? pos_lo - p.W + 1 : ctx - p.W);
+  const int32_t sink_end = min(p.sinks, hi);
+  const int32_t sink_tiles = (sink_end + TK - 1) / TK;
+  const int32_t t_first = max(win_lo / TK, sink_tiles);
+  const int32_t t_last = (hi + TK - 1) / TK;
+  const int32_t n_tiles = sink_tiles + max(0, t_last - t_first);
+  auto tile_base = [&](int32_t it) { return (it < sink_tiles ? it : t_first + (it - sink_tiles)) * TK; };
+  // Keys this lane's query sees: [vis_lo, vis_hi] plus the sinks below
+  // vis_hi; vis_hi = -1 for a padding query.
+  const int32_t vis_hi = !q_ok ? -1 : (causal ? min(qpos, kv_lim - 1) : kv_lim - 1);
+  const int32_t vis_lo = causal ? qpos - p.W + 1 : ctx - p.W;
+  const int32_t wq_last = min(qw0 + 31, p.Lq - 1);
+  const int32_t wpos_lo = ctx - p.Lq + qw0, wpos_hi = ctx - p.Lq + wq_last;
+
+  const int32_t *valid = reinterpret_cast<const int32_t *>(ws + (int64_t)units * L::kBlock);
+  // Chunk lc of (b, h) sits at buffer offset lc * HB from this (b, h)'s
+  // first block. Each thread fills KBUF/4096 K and VBUF/4096 V slots of 16
+  // bytes per tile (slot i of a buffer at byte 16 i); its offset inside the
+  // tile does not depend on the tile, so it is computed once, and the tile's
+  // chunk offset goes in the scalar offset.
+  const uint32_t HB = (uint32_t)p.H * (uint32_t)L::kBlock;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(ws + ((int64_t)b * MC * p.H + h) * L::kBlock), (short)0, (int)((MC - 1) * HB + L::kBlock), 0x00020000);
+  uint32_t kvoff, vvoff;
+  {
+    const int r = (tid / KC) & 15, j = (tid % KC) ^ kswz(tid / KC);
+    kvoff = (uint32_t)(r * KRB + 16 * j);
+    const int jv = (tid & 7) ^ ((tid >> 4) & 7);
+    vvoff = (uint32_t)(jv >> 1) * HB + (uint32_t)((tid >> 3) * 32 + 16 * (jv & 1));
+  }
+  int32_t pg_pend = 0;
+  auto load_tile = [&](int32_t it, int buf) __attribute__((always_inline)) {
+    const int32_t lc0 = tile_base(it) / 16;
+    const uint32_t cb = (uint32_t)lc0 * HB;
+#pragma unroll
+    for (int cl = 0; cl < KBUF / 4096; ++cl) {
+      const uint32_t k = (uint32_t)(cl * 256 + wave * 64) / (16 * KC);  // chunk of this wave's rows
+      buffer_load_lds16(rs, lds_k + buf * KBUF + (cl * 256 + wave * 64) * 16, kvoff, cb + k * HB);
+    }
+#pragma unroll
+    for (int cl = 0; cl < VBUF / 4096; ++cl)
+      buffer_load_lds16(rs, lds_v + buf * VBUF + (cl * 256 + wave * 64) * 16, vvoff,
+                        cb + (uint32_t)(L::kVPart + cl * 1024));
+    if (tid < NCK) {
+      const int32_t key = tile_base(it) + 16 * tid;
+      pg_pend = key < kv_lim ? valid[(int64_t)b * MC + lc0 + tid] : 0;
+    }
+  };
+  auto publish = [&](int buf) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0);
+    if (tid < NCK) s_pg[buf][tid] = pg_pend ? 1 : -1;
+    __syncthreads();
+  };
+
+  int32_t ka[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) ka[c] = (lane & 31) * KRB + 16 * ((2 * c + hl) ^ kswz(lane & 31));
+  int32_t va[NCK];
+#pragma unroll
+  for (int kc = 0; kc < NCK; ++kc) va[kc] = (lane & 31) * VRB + 16 * ((2 * kc + hl) ^ (((lane & 31) >> 1) & 7));
+
+  if (n_tiles > 0) {
+    load_tile(0, 0);
+    publish(0);
+  }
+  const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
+  for (int32_t it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    const int32_t tb = tile_base(it);
+    const uint8_t *kt = lds_k + buf * KBUF;
+    const uint8_t *vt = lds_v + buf * VBUF;
+    if (it + 1 < n_tiles) load_tile(it + 1, buf ^ 1);
+    const bool is_sink_tile = tb < sink_end;
+    bool any_vis = qw0 < p.Lq;
+    if (causal) any_vis = any_vis && tb <= wpos_hi && (is_sink_tile || tb + TK - 1 >= wpos_lo - p.W + 1);
+    int32_t pgs[NCK], pg_all = 0;
+#pragma unroll
+    for (int k = 0; k < NCK; ++k) {
+      pgs[k] = s_pg[buf][k];
+      pg_all |= pgs[k];
+    }
+    const bool full = pg_all >= 0 && tb + TK <= kv_lim &&
+                      (causal ? (tb + TK - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
+                      wq_last == qw0 + 31;
+    if (any_vis) {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        half8_t a[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) a[c] = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]);
+        float16_t s = mtile;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], s, 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NCH, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NCH, 0);
+        if (!full) {
+          // Slot r of this lane holds key tb + 2 hl + c_r; compare c_r with
+          // the lane's visible range shifted by that base (branch-free).
+          const int32_t kb = tb + 2 * hl;
+          const int32_t rl = vis_lo - kb, rs = p.sinks - kb;
+          int32_t rh[2];
+#pragma unroll
+          for (int g = 0; g < 2; ++g) rh[g] = pgs[2 * blk + g] >= 0 ? vis_hi - kb : -1;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int32_t c = 32 * blk + 16 * (r >> 3) + 4 * ((r >> 2) & 1) + ((r >> 1) & 1) + 8 * (r & 1);
+            const bool ok = (c <= rh[r >> 3]) & ((c >= rl) | (c < rs));
+            s[r] = ok ? s[r] : -INFINITY;
+          }
+        }
+        float tmax = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
+        tmax = half_max(tmax);
+        const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
+        if (__any(raise)) {
+          const float base = (m == -INFINITY) ? 0.0f : m;
+          const float mn = fmaxf(m, base + tmax);
+          const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
+          const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
+          lsum *= alpha;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[r] -= delta;
+          m = mn;
+          const float nb = (mn == -INFINITY) ? 0.0f : -mn;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mtile[r] = nb;
+        }
+        half8_t pb[2];
+#pragma unroll
+        for (int g2 = 0; g2 < 2; ++g2) {
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e]), (half_t)fast_exp2(s[8 * g2 + e + 1])};
+            lsum = __builtin_amdgcn_fdot2(pp2, ones, lsum, false);
+            pb[g2][e] = pp2.x;
+            pb[g2][e + 1] = pp2.y;
+          }
+        }
+        half8_t av[NDB][2];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int g2 = 0; g2 < 2; ++g2)
+            av[db][g2] = *reinterpret_cast<const half8_t *>(vt + 32 * db * VRB + va[2 * blk + g2]);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int g2 = 0; g2 < 2; ++g2)
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[db][g2], pb[g2], o[db], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NDB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * NDB, 0);
+      }
+    }
+    if (it + 1 < n_tiles) publish(buf ^ 1);
+    else __syncthreads();
+  }
+
+  const float l = half_sum(lsum);
+  if (!q_ok) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  half_t *orow = p.out + (((int64_t)b * p.Lq + qi) * p.H + h) * D;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * db + 8 * g + 4 * hl;
+      const half2_t x = {(half_t)(o[db][4 * g] * inv), (half_t)(o[db][4 * g + 1] * inv)};
+      const half2_t y = {(half_t)(o[db][4 * g + 2] * inv), (half_t)(o[db][4 * g + 3] * inv)};
+      *reinterpret_cast<uint2 *>(orow + d0) = make_uint2(as_u32(x), as_u32(y));
+    }
+  }
+}
+
 bool prefill_supported(const memopt_attn_desc &d) {
   auto al16 = [](const void *x) { return ((uintptr_t)x & 15) == 0; };
   if (d.q_len < 16 || (d.head_dim != 64 && d.head_dim != 128)) return false;
@@ -566,6 +948,21 @@ bool prefill_supported(const memopt_attn_desc &d) {
   // contiguous [num_blocks, block_size, H, D] pools (element strides)
   const int64_t D = d.head_dim, H = d.num_heads;
   return d.kv_head_stride == D && d.kv_token_stride == H * D && d.kv_page_stride == d.block_size * H * D;
+}
+
+// 16-token chunks staged per sequence: the block table's span rounded up to
+// whole 64-key tiles, so a tile never reads past its sequence's chunks.
+static int64_t staged_chunks(const memopt_attn_desc &d) {
+  return ((int64_t)d.max_blocks_per_seq * d.block_size / 16 + 3) / 4 * 4;
+}
+
+int64_t prefill_workspace_bytes(const memopt_attn_desc &d) {
+  if (std::getenv("MEMOPT_PREFILL_STAGED") && std::atoi(std::getenv("MEMOPT_PREFILL_STAGED")) == 0) return 0;
+  const int64_t mc = staged_chunks(d);
+  const int64_t units = (int64_t)d.batch * mc * d.num_heads;
+  // one sequence's chunks must stay inside a 31-bit buffer range
+  if (units <= 0 || units >= (1LL << 31) || mc * d.num_heads * 64LL * d.head_dim >= (1LL << 31)) return 0;
+  return units * (64LL * d.head_dim) + (int64_t)d.batch * mc * 4;
 }
 
 int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hipStream_t stream) {
@@ -585,6 +982,27 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
   p.sinks = d.num_sink_tokens < 0 ? 0 : d.num_sink_tokens;
   p.causal = d.causal;
   p.qk_scale_log2 = qk_scale_log2;
+  const int64_t need = prefill_workspace_bytes(d);
+  if (need > 0 && d.workspace && d.workspace_bytes >= need) {
+    // staged path: chunks in LDS operand layout, then the direct-load kernel
+    const int32_t mc = (int32_t)staged_chunks(d);
+    const int32_t units = d.batch * mc * d.num_heads;
+    const int64_t n_wg = (int64_t)((d.q_len + 127) / 128) * d.num_heads * d.batch;
+    MEMOPT_REQUIRE(n_wg < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "paged_attention: too many query tiles");
+    uint8_t *ws = (uint8_t *)d.workspace;
+    const dim3 sgrid((unsigned)((units + 3) / 4)), grid((unsigned)n_wg);
+    const bool int4 = d.kv_format == MEMOPT_KV_INT4;
+    if (d.head_dim == 128) {
+      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<128, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
+      else hipLaunchKernelGGL((prefill_stage_kernel<128, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
+      hipLaunchKernelGGL(prefill_direct_kernel<128>, grid, dim3(256), 0, stream, p, ws, mc, units);
+    } else {
+      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<64, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
+      else hipLaunchKernelGGL((prefill_stage_kernel<64, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
+      hipLaunchKernelGGL(prefill_direct_kernel<64>, grid, dim3(256), 0, stream, p, ws, mc, units);
+    }
+    return check_launch("paged_attention(prefill, staged)");
+  }
   int nw = 4, tk = 64;
   if (const char *e = std::getenv("MEMOPT_PREFILL_WAVES")) nw = std::atoi(e) == 8 ? 8 : 4;
   if (const char *e = std::getenv("MEMOPT_PREFILL_TILE")) tk = std::atoi(e) == 32 ? 32 : 64;

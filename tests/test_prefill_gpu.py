@@ -80,6 +80,38 @@ def test_prefill_out_of_pool_pages_are_skipped():
     assert_close(got, want)
 
 
+@pytest.mark.parametrize("int4", [False, True], ids=["fp16", "int4"])
+@pytest.mark.parametrize("Lq", [1, 40])
+def test_nan_past_context_is_ignored(int4, Lq):
+    """Tokens of a linked page at or past the context length never reach the
+    output, whatever their bits: the last page's tail holds NaN keys and
+    values (fp16 pool) or NaN scales (INT4 pages). Decode (q_len 1) and
+    prefill both follow the reference, which reads keys < context_len only
+    (src/csrc/attention.cu:173)."""
+    B, H, D, bs, ctx = 1, 2, 64, 16, 37
+    nb = 6
+    q, kp, vp, bt, cl = _case_inputs(24, B, H, D, bs, nb, [ctx], Lq)
+    want = O.paged_attention(q, kp, vp, bt, cl, 64, 64, causal=True)
+    tail = int(bt[0, 2])
+    if int4:
+        pages = O.to_int4_pages(kp, vp)
+        want = O.paged_attention_int4(q, pages, bt, cl, 64, 64, causal=True)
+        G = D // 64
+        sc = pages[tail].reshape(H, -1)[:, 16 * D:].copy().view(np.float16).reshape(H, 2, G, 16)
+        for t in range(ctx - 32, 16):
+            sc[:, :, :, 2 * (t % 8) + t // 8] = np.float16(np.nan)
+        pages[tail].reshape(H, -1)[:, 16 * D:] = sc.reshape(H, -1).view(np.uint8)
+        pg = to_dev(pages)
+        got = memopt_C.dynamic_sparse_attention(to_dev(q), pg, pg, to_dev(bt), to_dev(cl), 64, 64, causal=True)
+    else:
+        kp[tail, ctx - 32:] = np.float16(np.nan)
+        vp[tail, ctx - 32:] = np.float16(np.nan)
+        got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt), to_dev(cl), 64, 64,
+                                                causal=True)
+    assert not torch.isnan(got).any()
+    assert_close(got, want)
+
+
 def test_reference_math_equivalence_multi_query():
     """tests/test_attention.py:112-192 restated on this path: full window,
     non-causal, torch.rand inputs, == SDPA within atol = rtol = 1e-3, and
