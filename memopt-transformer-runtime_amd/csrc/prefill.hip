@@ -689,13 +689,24 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams 
     reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + lc] = pg >= 0 ? 1 : 0;
 }
 
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+
 // 16-byte buffer -> LDS copy: lane i's bytes (buffer offset voff + soff)
-// land at lds_base + 16 i. Kept out of the kernel template: the host pass of
-// a template that names the builtin directly drops the kernel's launch stub.
-__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, void *lds_base, uint32_t voff,
+// land at LDS byte address lds_base + 16 i. Written as inline assembly so the
+// compiler does not track it: its wait-count pass cannot tell the two LDS
+// buffers apart and would otherwise wait for the next tile's prefetch before
+// every operand read of the current one. Callers wait for completion
+// themselves (s_waitcnt vmcnt(0) before the barrier that publishes a tile).
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, const void *lds_base, uint32_t voff,
                                                   uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_base, 16, (int)voff,
-                                           (int)soff, 0, 0);
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)lds_base);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0v), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
 }
 
 // Attention over staged chunks: 4 waves x 32 queries, 64-key tiles filled by
@@ -713,9 +724,12 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
   constexpr int KBUF = TK * KRB, VBUF = D * VRB;
   constexpr int NCH = D / 16, NDB = D / 32;
   using L = StageLayout<D>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k[2 * KBUF];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_v[2 * VBUF];
-  __shared__ int32_t s_pg[2][NCK];
+  // Two buffers per operand as separate LDS objects, selected by a
+  // compile-time index: the compiler then sees that a tile's loads into one
+  // buffer never alias the operand reads of the other, and does not wait on
+  // the prefetch before those reads.
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k0[KBUF], lds_k1[KBUF];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_v0[VBUF], lds_v1[VBUF];
 
   auto kswz = [](int R) { return KC == 16 ? (R & 15) : ((R >> 1) & 7); };
 
@@ -774,7 +788,11 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
   const int32_t wq_last = min(qw0 + 31, p.Lq - 1);
   const int32_t wpos_lo = ctx - p.Lq + qw0, wpos_hi = ctx - p.Lq + wq_last;
 
-  const int32_t *valid = reinterpret_cast<const int32_t *>(ws + (int64_t)units * L::kBlock);
+  // Linked flags of a tile's 4 chunks (lane l holds chunk l % 4); the stage
+  // pass clears them for chunks at or past the context length. Loaded with
+  // the tile's data and read (readlane) only after the tile is published.
+  const int32_t *vrow = reinterpret_cast<const int32_t *>(ws + (int64_t)units * L::kBlock) + (int64_t)b * MC;
+  int32_t fl_next = 0;
   // Chunk lc of (b, h) sits at buffer offset lc * HB from this (b, h)'s
   // first block. Each thread fills KBUF/4096 K and VBUF/4096 V slots of 16
   // bytes per tile (slot i of a buffer at byte 16 i); its offset inside the
@@ -790,27 +808,27 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
     const int jv = (tid & 7) ^ ((tid >> 4) & 7);
     vvoff = (uint32_t)(jv >> 1) * HB + (uint32_t)((tid >> 3) * 32 + 16 * (jv & 1));
   }
-  int32_t pg_pend = 0;
-  auto load_tile = [&](int32_t it, int buf) __attribute__((always_inline)) {
+  auto load_tile = [&](int32_t it, auto bufc) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+    uint8_t *const lk = buf ? lds_k1 : lds_k0;
+    uint8_t *const lv = buf ? lds_v1 : lds_v0;
     const int32_t lc0 = tile_base(it) / 16;
     const uint32_t cb = (uint32_t)lc0 * HB;
+    fl_next = vrow[lc0 + (lane & 3)];
 #pragma unroll
     for (int cl = 0; cl < KBUF / 4096; ++cl) {
       const uint32_t k = (uint32_t)(cl * 256 + wave * 64) / (16 * KC);  // chunk of this wave's rows
-      buffer_load_lds16(rs, lds_k + buf * KBUF + (cl * 256 + wave * 64) * 16, kvoff, cb + k * HB);
+      buffer_load_lds16(rs, lk + (cl * 256 + wave * 64) * 16, kvoff, cb + k * HB);
     }
 #pragma unroll
     for (int cl = 0; cl < VBUF / 4096; ++cl)
-      buffer_load_lds16(rs, lds_v + buf * VBUF + (cl * 256 + wave * 64) * 16, vvoff,
+      buffer_load_lds16(rs, lv + (cl * 256 + wave * 64) * 16, vvoff,
                         cb + (uint32_t)(L::kVPart + cl * 1024));
-    if (tid < NCK) {
-      const int32_t key = tile_base(it) + 16 * tid;
-      pg_pend = key < kv_lim ? valid[(int64_t)b * MC + lc0 + tid] : 0;
-    }
   };
-  auto publish = [&](int buf) __attribute__((always_inline)) {
+  // Completes the tile loads in flight (vmcnt also covers the untracked LDS
+  // copies) and makes them visible to the workgroup.
+  auto publish = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0);
-    if (tid < NCK) s_pg[buf][tid] = pg_pend ? 1 : -1;
     __syncthreads();
   };
 
@@ -822,39 +840,53 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
   for (int kc = 0; kc < NCK; ++kc) va[kc] = (lane & 31) * VRB + 16 * ((2 * kc + hl) ^ (((lane & 31) >> 1) & 7));
 
   if (n_tiles > 0) {
-    load_tile(0, 0);
-    publish(0);
+    load_tile(0, IntC<0>{});
+    publish();
   }
   const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
-  for (int32_t it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1;
+  auto tile = [&](int32_t it, auto bufc) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
     const int32_t tb = tile_base(it);
-    const uint8_t *kt = lds_k + buf * KBUF;
-    const uint8_t *vt = lds_v + buf * VBUF;
-    if (it + 1 < n_tiles) load_tile(it + 1, buf ^ 1);
+    const uint8_t *const kt = buf ? lds_k1 : lds_k0;
+    const uint8_t *const vt = buf ? lds_v1 : lds_v0;
+    const int32_t fl = fl_next;
+    if (it + 1 < n_tiles) load_tile(it + 1, IntC<buf ^ 1>{});
     const bool is_sink_tile = tb < sink_end;
     bool any_vis = qw0 < p.Lq;
     if (causal) any_vis = any_vis && tb <= wpos_hi && (is_sink_tile || tb + TK - 1 >= wpos_lo - p.W + 1);
-    int32_t pgs[NCK], pg_all = 0;
+    int32_t pgs[NCK];
 #pragma unroll
-    for (int k = 0; k < NCK; ++k) {
-      pgs[k] = s_pg[buf][k];
-      pg_all |= pgs[k];
-    }
+    for (int k = 0; k < NCK; ++k) pgs[k] = __builtin_amdgcn_readlane(fl, k) ? 1 : -1;
+    const int32_t pg_all = pgs[0] | pgs[1] | pgs[2] | pgs[3];
     const bool full = pg_all >= 0 && tb + TK <= kv_lim &&
                       (causal ? (tb + TK - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
                       wq_last == qw0 + 31;
     if (any_vis) {
+      // Both 32-key blocks' S^T chains are issued first: the second chain
+      // runs on the matrix core while the first block's softmax runs on the
+      // VALU, and block 0's PV chain overlaps block 1's softmax.
+      float16_t sb[2];
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
         half8_t a[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) a[c] = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]);
-        float16_t s = mtile;
+        sb[blk] = mtile;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], s, 0, 0, 0);
+        for (int c = 0; c < NCH; ++c) sb[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], sb[blk], 0, 0, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, NCH, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, NCH, 0);
+      }
+      const float m_qk = m;  // both chains started from -m_qk (0 while m is -inf)
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        float16_t s = sb[blk];
+        if (blk == 1 && __any(m != m_qk)) {
+          // block 0 raised the running max after block 1's chain started
+          const float shift = (m == m_qk) ? 0.0f : m - (m_qk == -INFINITY ? 0.0f : m_qk);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[r] -= shift;
+        }
         if (!full) {
           // Slot r of this lane holds key tb + 2 hl + c_r; compare c_r with
           // the lane's visible range shifted by that base (branch-free).
@@ -918,8 +950,11 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
         __builtin_amdgcn_sched_group_barrier(0x008, 2 * NDB, 0);
       }
     }
-    if (it + 1 < n_tiles) publish(buf ^ 1);
-    else __syncthreads();
+    publish();
+  };
+  for (int32_t it = 0; it < n_tiles; it += 2) {
+    tile(it, IntC<0>{});
+    if (it + 1 < n_tiles) tile(it + 1, IntC<1>{});
   }
 
   const float l = half_sum(lsum);
