@@ -862,36 +862,18 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
                       (causal ? (tb + TK - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
                       wq_last == qw0 + 31;
     if (any_vis) {
-      // Both 32-key blocks' S^T chains are issued first: the second chain
-      // runs on the matrix core while the first block's softmax runs on the
-      // VALU, and block 0's PV chain overlaps block 1's softmax.
+      // The mask enters as the chains' initial accumulator: -inf for a
+      // hidden (key, query) slot, -m (the running max) otherwise. Slot r of
+      // this lane holds key tb + 2 hl + c_r.
       float16_t sb[2];
+      if (full) {
+        sb[0] = mtile;
+        sb[1] = mtile;
+      } else {
+        const int32_t kb = tb + 2 * hl;
+        const int32_t rl = vis_lo - kb, rs = p.sinks - kb;
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        half8_t a[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) a[c] = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]);
-        sb[blk] = mtile;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) sb[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], sb[blk], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, NCH, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, NCH, 0);
-      }
-      const float m_qk = m;  // both chains started from -m_qk (0 while m is -inf)
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        float16_t s = sb[blk];
-        if (blk == 1 && __any(m != m_qk)) {
-          // block 0 raised the running max after block 1's chain started
-          const float shift = (m == m_qk) ? 0.0f : m - (m_qk == -INFINITY ? 0.0f : m_qk);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[r] -= shift;
-        }
-        if (!full) {
-          // Slot r of this lane holds key tb + 2 hl + c_r; compare c_r with
-          // the lane's visible range shifted by that base (branch-free).
-          const int32_t kb = tb + 2 * hl;
-          const int32_t rl = vis_lo - kb, rs = p.sinks - kb;
+        for (int blk = 0; blk < 2; ++blk) {
           int32_t rh[2];
 #pragma unroll
           for (int g = 0; g < 2; ++g) rh[g] = pgs[2 * blk + g] >= 0 ? vis_hi - kb : -1;
@@ -899,37 +881,64 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
           for (int r = 0; r < 16; ++r) {
             const int32_t c = 32 * blk + 16 * (r >> 3) + 4 * ((r >> 2) & 1) + ((r >> 1) & 1) + 8 * (r & 1);
             const bool ok = (c <= rh[r >> 3]) & ((c >= rl) | (c < rs));
-            s[r] = ok ? s[r] : -INFINITY;
+            sb[blk][r] = ok ? mtile[r] : -INFINITY;
           }
         }
-        float tmax = s[0];
+      }
 #pragma unroll
-        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
-        tmax = half_max(tmax);
-        const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
-        if (__any(raise)) {
-          const float base = (m == -INFINITY) ? 0.0f : m;
-          const float mn = fmaxf(m, base + tmax);
-          const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
-          const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
-          lsum *= alpha;
+      for (int blk = 0; blk < 2; ++blk) {
+        half8_t a[NCH];
 #pragma unroll
-          for (int db = 0; db < NDB; ++db)
+        for (int c = 0; c < NCH; ++c) a[c] = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        for (int c = 0; c < NCH; ++c) sb[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], sb[blk], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NCH, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NCH, 0);
+      }
+      if (!full) {
+        // A hidden slot whose key holds inf or NaN sums to NaN; max(NaN,
+        // -inf) is -inf, so such keys stay hidden as the reference's skip does.
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[r] -= delta;
-          m = mn;
-          const float nb = (mn == -INFINITY) ? 0.0f : -mn;
+        for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mtile[r] = nb;
+          for (int r = 0; r < 16; ++r) sb[blk][r] = fmaxf(sb[blk][r], -INFINITY);
+      }
+      // One running-max check for the whole 64-key tile.
+      float tmax = sb[0][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, sb[0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sb[1][r]);
+      tmax = half_max(tmax);
+      const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
+      if (__any(raise)) {
+        const float base = (m == -INFINITY) ? 0.0f : m;
+        const float mn = fmaxf(m, base + tmax);
+        const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
+        const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
+        lsum *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sb[0][r] -= delta;
+          sb[1][r] -= delta;
         }
+        m = mn;
+        const float nb = (mn == -INFINITY) ? 0.0f : -mn;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mtile[r] = nb;
+      }
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
         half8_t pb[2];
 #pragma unroll
         for (int g2 = 0; g2 < 2; ++g2) {
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
-            const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e]), (half_t)fast_exp2(s[8 * g2 + e + 1])};
+            const half2_t pp2 = {(half_t)fast_exp2(sb[blk][8 * g2 + e]), (half_t)fast_exp2(sb[blk][8 * g2 + e + 1])};
             lsum = __builtin_amdgcn_fdot2(pp2, ones, lsum, false);
             pb[g2][e] = pp2.x;
             pb[g2][e + 1] = pp2.y;

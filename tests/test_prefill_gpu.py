@@ -112,6 +112,28 @@ def test_nan_past_context_is_ignored(int4, Lq):
     assert_close(got, want)
 
 
+def test_non_finite_key_outside_window_is_ignored():
+    """A NaN key inside the context reaches only the queries whose window
+    holds it; the reference never reads keys outside a query's window
+    (src/csrc/attention.cu:173-190), so every other row stays finite and
+    matches the oracle."""
+    B, H, D, bs, ctx, Lq, W, sinks = 1, 2, 64, 16, 300, 300, 64, 4
+    nb = 22
+    q, kp, vp, bt, cl = _case_inputs(25, B, H, D, bs, nb, [ctx], Lq)
+    bad_tok = 100
+    # expected rows from the finite cache: rows that cannot see the key do not
+    # depend on its value (the oracle's additive mask cannot hide a NaN)
+    want = O.paged_attention(q, kp, vp, bt, cl, 512, W, num_sink_tokens=sinks, causal=True)
+    kp[bt[0, bad_tok // bs], bad_tok % bs, 1] = np.float16(np.nan)   # head 1 only
+    got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt), to_dev(cl), 512, W,
+                                            num_sink_tokens=sinks, causal=True).cpu().numpy()
+    sees = (np.arange(Lq) >= bad_tok) & (np.arange(Lq) < bad_tok + W)
+    keep = ~sees
+    assert not np.isnan(got[0, keep]).any()
+    assert_close(torch.from_numpy(got[0, keep]), want[0, keep])
+    assert_close(torch.from_numpy(got[0, :, 0]), want[0, :, 0])   # head 0 holds no NaN
+
+
 def test_reference_math_equivalence_multi_query():
     """tests/test_attention.py:112-192 restated on this path: full window,
     non-causal, torch.rand inputs, == SDPA within atol = rtol = 1e-3, and
