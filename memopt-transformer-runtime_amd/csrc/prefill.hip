@@ -571,16 +571,18 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
 // the next column (vt_col of K-tile row 2p).
 __device__ __forceinline__ int chunk_vcol(int p) { return 8 * ((p >> 1) & 1) + 4 * (p >> 2) + 2 * (p & 1); }
 
-// Workspace block of one (sequence, 16-token chunk, head): 2*16*D fp16 =
-// K part [16 rows][D] then V^T part [D rows][16 columns]; followed, after all
-// blocks, by one int32 per (sequence, chunk): 1 if its page is linked.
+// Workspace block of one (sequence, head, 16-token chunk): 2*16*D fp16 =
+// K part [16 rows][D] then V^T part [D rows][16 columns]. Blocks are ordered
+// [sequence][head][chunk], so the chunks of one (sequence, head) are one
+// contiguous run. After all blocks comes one int32 per (sequence, chunk): 1
+// if its page is linked.
 template <int D>
 struct StageLayout {
   static constexpr int64_t kBlock = 2 * 16 * D * 2;  // bytes
   static constexpr int64_t kVPart = 16 * D * 2;      // byte offset of V^T in a block
 };
 
-// One wave per (sequence b, chunk lc, head h); lane l = 8p + c owns tokens
+// One wave per (sequence b, head h, chunk lc); lane l = 8p + c owns tokens
 // (p, p + 8) x dims [c*D/8, (c+1)*D/8), as in the INT4 page format.
 template <int D, bool INT4>
 __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams p, uint8_t *__restrict__ ws,
@@ -590,7 +592,7 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams 
   const int lane = threadIdx.x & 63;
   const int32_t unit = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (unit >= units) return;  // wave-uniform
-  const int32_t h = unit % p.H, bl = unit / p.H, lc = bl % MC, b = bl / MC;
+  const int32_t lc = unit % MC, bh = unit / MC, h = bh % p.H, b = bh / p.H;
   const int pp = lane >> 3, c = lane & 7;
   const int32_t kv_lim = min(p.ctx[b], p.M * p.bs);
   const int32_t key0 = lc * 16;
@@ -694,41 +696,66 @@ struct IntC {
   static constexpr int value = N;
 };
 
-// 16-byte buffer -> LDS copy: lane i's bytes (buffer offset voff + soff)
-// land at LDS byte address lds_base + 16 i. Written as inline assembly so the
-// compiler does not track it: its wait-count pass cannot tell the two LDS
-// buffers apart and would otherwise wait for the next tile's prefetch before
-// every operand read of the current one. Callers wait for completion
-// themselves (s_waitcnt vmcnt(0) before the barrier that publishes a tile).
-__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, const void *lds_base, uint32_t voff,
-                                                  uint32_t soff) {
-  const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)lds_base);
+// Scheduling group: `n` instructions of class `mask` (0x002 VALU, 0x008
+// MFMA, 0x100 LDS read, 0x400 transcendental) in this position of the order.
+#define PIPE_SGB(mask, n, id) __builtin_amdgcn_sched_group_barrier(mask, n, id)
+
+// LDS-DMA copy (buffer_load ... lds): lane i's 16 bytes at buffer offset
+// voff + soff land at LDS byte m0v + 16 i. Written as inline assembly so the
+// compiler does not track it: its wait-count pass cannot tell the LDS
+// buffers apart and would wait for the next tiles' copies before every
+// operand read of the current one. Callers wait for completion themselves
+// (s_waitcnt vmcnt before the barrier that publishes a tile).
+__device__ __forceinline__ void buffer_load_lds16_m0(__amdgpu_buffer_rsrc_t r, uint32_t m0v, uint32_t voff,
+                                                     uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
                : "s"(m0v), "v"(voff), "s"(r), "s"(soff)
                : "memory", "m0");
 }
 
-// Attention over staged chunks: 4 waves x 32 queries, 64-key tiles filled by
-// global_load_lds into unpadded LDS rows whose 16-byte chunks are
-// XOR-swizzled (K: chunk ^ (row & 15) for 256-byte rows, chunk ^ ((row >> 1)
-// & 7) for 128-byte rows; V^T: chunk ^ ((row >> 1) & 7)), which keeps the
-// MFMA operand reads free of bank conflicts.
+__device__ __forceinline__ uint32_t lds_u32(const void *p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p);
+}
+
+// Attention over staged chunks, software-pipelined inside each wave.
+//  * A workgroup of 4 waves owns 128 queries of one (batch, head); wave w
+//    owns 32 of them, one query per lane column (lanes l and l+32 share
+//    query l % 32). Q is held in registers, pre-scaled by log2(e)/sqrt(D).
+//  * Keys advance in 64-key tiles (four staged 16-token chunks). Tiles are
+//    copied from the workspace into LDS with buffer-to-LDS DMA: unpadded
+//    rows whose 16-byte chunks are XOR-swizzled (K: chunk ^ (row & 15) for
+//    256-byte rows, chunk ^ ((row >> 1) & 7) for 128-byte rows; V^T: chunk ^
+//    ((row >> 1) & 7)), which keeps the MFMA operand reads conflict-free.
+//  * S^T = K Q^T and O^T += V^T P^T run on v_mfma_f32_32x32x16_f16. The S^T
+//    accumulator layout is the PV B-operand layout (the staged V^T columns
+//    are in that key order), so probabilities go from exp2 straight into
+//    the PV MFMAs. The running max enters the S chains as their initial
+//    accumulator (-m), so the MFMA returns score - m.
+//  * Iteration i holds S(i) (computed by iteration i - 1) and interleaves
+//      QK(i+1) block 0 MFMAs  with the running max of S(i),
+//      QK(i+1) block 1 MFMAs  with exp2 / packing of S(i) block 0,
+//      PV(i) block 0 MFMAs    with exp2 / packing of S(i) block 1,
+//      PV(i) block 1 MFMAs,
+//    so the matrix pipe has independent work while the softmax runs.
+//  * K tiles are copied three tiles ahead (three buffers), V tiles one tile
+//    ahead (two buffers); iteration i reads K(i+1) and V(i) and refills the
+//    buffers of K(i) and V(i-1), both last read in iteration i-1.
+//  * Workgroup IDs are remapped so that each XCD owns whole heads (a head's
+//    window stays in one L2), longest causal query tiles first.
 template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillParams p, const uint8_t *__restrict__ ws,
-                                                                int32_t MC, int32_t units) {
-  constexpr int NW = 4, TK = 64, NCK = 4;
-  constexpr int KRB = 2 * D;      // K row bytes
-  constexpr int KC = KRB / 16;    // 16-byte chunks per K row
-  constexpr int VRB = TK * 2;     // V^T row bytes
+__global__ __launch_bounds__(256, 2) void prefill_pipe_kernel(const PrefillParams p, const uint8_t *__restrict__ ws,
+                                                              int32_t MC, int32_t units) {
+  constexpr int NW = 4, TK = 64;
+  constexpr int KRB = 2 * D, KC = KRB / 16, VRB = TK * 2;
   constexpr int KBUF = TK * KRB, VBUF = D * VRB;
   constexpr int NCH = D / 16, NDB = D / 32;
+  constexpr int NKL = KBUF / 4096, NVL = VBUF / 4096;
   using L = StageLayout<D>;
-  // Two buffers per operand as separate LDS objects, selected by a
-  // compile-time index: the compiler then sees that a tile's loads into one
-  // buffer never alias the operand reads of the other, and does not wait on
-  // the prefetch before those reads.
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k0[KBUF], lds_k1[KBUF];
+  constexpr uint32_t CS = (uint32_t)L::kBlock;  // bytes per staged chunk
+  // Three K buffers and two V buffers: 160 KiB for the two workgroups of a CU at D = 128.
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k0[KBUF], lds_k1[KBUF], lds_k2[KBUF];
   __shared__ __attribute__((aligned(16))) uint8_t lds_v0[VBUF], lds_v1[VBUF];
 
   auto kswz = [](int R) { return KC == 16 ? (R & 15) : ((R >> 1) & 7); };
@@ -781,190 +808,272 @@ __global__ __launch_bounds__(256, 2) void prefill_direct_kernel(const PrefillPar
   const int32_t t_last = (hi + TK - 1) / TK;
   const int32_t n_tiles = sink_tiles + max(0, t_last - t_first);
   auto tile_base = [&](int32_t it) { return (it < sink_tiles ? it : t_first + (it - sink_tiles)) * TK; };
-  // Keys this lane's query sees: [vis_lo, vis_hi] plus the sinks below
-  // vis_hi; vis_hi = -1 for a padding query.
   const int32_t vis_hi = !q_ok ? -1 : (causal ? min(qpos, kv_lim - 1) : kv_lim - 1);
   const int32_t vis_lo = causal ? qpos - p.W + 1 : ctx - p.W;
   const int32_t wq_last = min(qw0 + 31, p.Lq - 1);
   const int32_t wpos_lo = ctx - p.Lq + qw0, wpos_hi = ctx - p.Lq + wq_last;
+  // Every (key, query) slot of the tile is visible: no mask needed.
+  auto tile_full = [&](int32_t tb, int4 fl) {
+    return (fl.x & fl.y & fl.z & fl.w) != 0 && tb + TK <= kv_lim &&
+           (causal ? (tb + TK - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
+           wq_last == qw0 + 31;
+  };
 
-  // Linked flags of a tile's 4 chunks (lane l holds chunk l % 4); the stage
-  // pass clears them for chunks at or past the context length. Loaded with
-  // the tile's data and read (readlane) only after the tile is published.
   const int32_t *vrow = reinterpret_cast<const int32_t *>(ws + (int64_t)units * L::kBlock) + (int64_t)b * MC;
-  int32_t fl_next = 0;
-  // Chunk lc of (b, h) sits at buffer offset lc * HB from this (b, h)'s
-  // first block. Each thread fills KBUF/4096 K and VBUF/4096 V slots of 16
-  // bytes per tile (slot i of a buffer at byte 16 i); its offset inside the
-  // tile does not depend on the tile, so it is computed once, and the tile's
-  // chunk offset goes in the scalar offset.
-  const uint32_t HB = (uint32_t)p.H * (uint32_t)L::kBlock;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(ws + ((int64_t)b * MC * p.H + h) * L::kBlock), (short)0, (int)((MC - 1) * HB + L::kBlock), 0x00020000);
+      (void *)(ws + ((int64_t)b * p.H + h) * MC * L::kBlock), (short)0, (int)(MC * CS), 0x00020000);
   uint32_t kvoff, vvoff;
   {
     const int r = (tid / KC) & 15, j = (tid % KC) ^ kswz(tid / KC);
     kvoff = (uint32_t)(r * KRB + 16 * j);
     const int jv = (tid & 7) ^ ((tid >> 4) & 7);
-    vvoff = (uint32_t)(jv >> 1) * HB + (uint32_t)((tid >> 3) * 32 + 16 * (jv & 1));
+    vvoff = (uint32_t)(jv >> 1) * CS + (uint32_t)((tid >> 3) * 32 + 16 * (jv & 1));
   }
-  auto load_tile = [&](int32_t it, auto bufc) __attribute__((always_inline)) {
+  const uint32_t wofs = (uint32_t)wave * 64 * 16;
+  const uint32_t mk0 = lds_u32(lds_k0) + wofs, mk1 = lds_u32(lds_k1) + wofs, mk2 = lds_u32(lds_k2) + wofs;
+  const uint32_t mv0 = lds_u32(lds_v0) + wofs, mv1 = lds_u32(lds_v1) + wofs;
+  // Copies cl in [c0, c1) of a tile's K (V) part; a tile is split over the
+  // segments of an iteration so the copies are not issued in one burst.
+  auto load_k = [&](int32_t it, auto bufc, int c0, int c1) __attribute__((always_inline)) {
     constexpr int buf = decltype(bufc)::value;
-    uint8_t *const lk = buf ? lds_k1 : lds_k0;
-    uint8_t *const lv = buf ? lds_v1 : lds_v0;
-    const int32_t lc0 = tile_base(it) / 16;
-    const uint32_t cb = (uint32_t)lc0 * HB;
-    fl_next = vrow[lc0 + (lane & 3)];
+    const uint32_t cb = (uint32_t)(tile_base(it) / 16) * CS;
 #pragma unroll
-    for (int cl = 0; cl < KBUF / 4096; ++cl) {
-      const uint32_t k = (uint32_t)(cl * 256 + wave * 64) / (16 * KC);  // chunk of this wave's rows
-      buffer_load_lds16(rs, lk + (cl * 256 + wave * 64) * 16, kvoff, cb + k * HB);
+    for (int cl = c0; cl < c1; ++cl) {
+      const uint32_t k = (uint32_t)(cl * 256 + wave * 64) / (16 * KC);
+      buffer_load_lds16_m0(rs, (buf == 2 ? mk2 : buf ? mk1 : mk0) + cl * 4096, kvoff, cb + k * CS);
     }
-#pragma unroll
-    for (int cl = 0; cl < VBUF / 4096; ++cl)
-      buffer_load_lds16(rs, lv + (cl * 256 + wave * 64) * 16, vvoff,
-                        cb + (uint32_t)(L::kVPart + cl * 1024));
   };
-  // Completes the tile loads in flight (vmcnt also covers the untracked LDS
-  // copies) and makes them visible to the workgroup.
-  auto publish = [&]() __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(0);
+  auto load_v = [&](int32_t it, auto bufc, int c0, int c1) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value;
+    const uint32_t cb = (uint32_t)(tile_base(it) / 16) * CS + (uint32_t)L::kVPart;
+#pragma unroll
+    for (int cl = c0; cl < c1; ++cl) buffer_load_lds16_m0(rs, (buf ? mv1 : mv0) + cl * 4096, vvoff, cb + cl * 1024);
+  };
+  // End of a tile: wait for this thread's tile copies except the newest
+  // `keep` (the K prefetch, which has another tile of time), and for its LDS
+  // reads; fetch the linked flags of the next tile's four chunks with one
+  // scalar load inside the same wait (the value is complete when the asm
+  // returns); then the barrier publishes the copies of all threads.
+  auto publish = [&](int32_t next_it, auto keepc) __attribute__((always_inline)) {
+    constexpr int keep = decltype(keepc)::value;
+    const int32_t *fp = vrow + (next_it < n_tiles ? tile_base(next_it) / 16 : 0);
+    int4 f;
+    if constexpr (keep == 0)
+      asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt vmcnt(0) lgkmcnt(0)" : "=s"(f) : "s"(fp) : "memory");
+    else
+      asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt vmcnt(%2) lgkmcnt(0)"
+                   : "=s"(f) : "s"(fp), "n"(keep) : "memory");
     __syncthreads();
+    return f;
   };
 
   int32_t ka[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) ka[c] = (lane & 31) * KRB + 16 * ((2 * c + hl) ^ kswz(lane & 31));
-  int32_t va[NCK];
+  int32_t va[4];
 #pragma unroll
-  for (int kc = 0; kc < NCK; ++kc) va[kc] = (lane & 31) * VRB + 16 * ((2 * kc + hl) ^ (((lane & 31) >> 1) & 7));
+  for (int kc = 0; kc < 4; ++kc) va[kc] = (lane & 31) * VRB + 16 * ((2 * kc + hl) ^ (((lane & 31) >> 1) & 7));
 
-  if (n_tiles > 0) {
-    load_tile(0, IntC<0>{});
-    publish();
-  }
-  const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
-  auto tile = [&](int32_t it, auto bufc) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    const int32_t tb = tile_base(it);
-    const uint8_t *const kt = buf ? lds_k1 : lds_k0;
-    const uint8_t *const vt = buf ? lds_v1 : lds_v0;
-    const int32_t fl = fl_next;
-    if (it + 1 < n_tiles) load_tile(it + 1, IntC<buf ^ 1>{});
-    const bool is_sink_tile = tb < sink_end;
-    bool any_vis = qw0 < p.Lq;
-    if (causal) any_vis = any_vis && tb <= wpos_hi && (is_sink_tile || tb + TK - 1 >= wpos_lo - p.W + 1);
-    int32_t pgs[NCK];
+  // Hidden (key, query) slots of S(i) become -inf. Slot r of block blk of
+  // this lane holds key tb + 32 blk + 16(r/8) + 4((r/4)%2) + (r/2)%2 + 8(r%2) + 2 hl.
+  auto apply_mask = [&](float16_t (&s)[2], int32_t tb, int4 fl) __attribute__((always_inline)) {
+    const int32_t kb = tb + 2 * hl;
+    const int32_t rl = vis_lo - kb, rsk = p.sinks - kb;
 #pragma unroll
-    for (int k = 0; k < NCK; ++k) pgs[k] = __builtin_amdgcn_readlane(fl, k) ? 1 : -1;
-    const int32_t pg_all = pgs[0] | pgs[1] | pgs[2] | pgs[3];
-    const bool full = pg_all >= 0 && tb + TK <= kv_lim &&
-                      (causal ? (tb + TK - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
-                      wq_last == qw0 + 31;
-    if (any_vis) {
-      // The mask enters as the chains' initial accumulator: -inf for a
-      // hidden (key, query) slot, -m (the running max) otherwise. Slot r of
-      // this lane holds key tb + 2 hl + c_r.
-      float16_t sb[2];
-      if (full) {
-        sb[0] = mtile;
-        sb[1] = mtile;
-      } else {
-        const int32_t kb = tb + 2 * hl;
-        const int32_t rl = vis_lo - kb, rs = p.sinks - kb;
+    for (int blk = 0; blk < 2; ++blk) {
+      int32_t rh[2];
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-          int32_t rh[2];
-#pragma unroll
-          for (int g = 0; g < 2; ++g) rh[g] = pgs[2 * blk + g] >= 0 ? vis_hi - kb : -1;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int32_t c = 32 * blk + 16 * (r >> 3) + 4 * ((r >> 2) & 1) + ((r >> 1) & 1) + 8 * (r & 1);
-            const bool ok = (c <= rh[r >> 3]) & ((c >= rl) | (c < rs));
-            sb[blk][r] = ok ? mtile[r] : -INFINITY;
-          }
-        }
+      for (int g = 0; g < 2; ++g) {
+        const int32_t f = (2 * blk + g) == 0 ? fl.x : (2 * blk + g) == 1 ? fl.y : (2 * blk + g) == 2 ? fl.z : fl.w;
+        rh[g] = f ? vis_hi - kb : -1;
       }
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        half8_t a[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) a[c] = *reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]);
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) sb[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c], qf[c], sb[blk], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, NCH, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, NCH, 0);
-      }
-      if (!full) {
-        // A hidden slot whose key holds inf or NaN sums to NaN; max(NaN,
-        // -inf) is -inf, so such keys stay hidden as the reference's skip does.
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sb[blk][r] = fmaxf(sb[blk][r], -INFINITY);
-      }
-      // One running-max check for the whole 64-key tile.
-      float tmax = sb[0][0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, sb[0][r]);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sb[1][r]);
-      tmax = half_max(tmax);
-      const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
-      if (__any(raise)) {
-        const float base = (m == -INFINITY) ? 0.0f : m;
-        const float mn = fmaxf(m, base + tmax);
-        const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
-        const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
-        lsum *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sb[0][r] -= delta;
-          sb[1][r] -= delta;
-        }
-        m = mn;
-        const float nb = (mn == -INFINITY) ? 0.0f : -mn;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mtile[r] = nb;
-      }
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        half8_t pb[2];
-#pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const half2_t pp2 = {(half_t)fast_exp2(sb[blk][8 * g2 + e]), (half_t)fast_exp2(sb[blk][8 * g2 + e + 1])};
-            lsum = __builtin_amdgcn_fdot2(pp2, ones, lsum, false);
-            pb[g2][e] = pp2.x;
-            pb[g2][e + 1] = pp2.y;
-          }
-        }
-        half8_t av[NDB][2];
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int g2 = 0; g2 < 2; ++g2)
-            av[db][g2] = *reinterpret_cast<const half8_t *>(vt + 32 * db * VRB + va[2 * blk + g2]);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int g2 = 0; g2 < 2; ++g2)
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[db][g2], pb[g2], o[db], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NDB, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 2 * NDB, 0);
+      for (int r = 0; r < 16; ++r) {
+        const int32_t c = 32 * blk + 16 * (r >> 3) + 4 * ((r >> 2) & 1) + ((r >> 1) & 1) + 8 * (r & 1);
+        const bool ok = (c <= rh[r >> 3]) & ((c >= rl) | (c < rsk));
+        s[blk][r] = ok ? s[blk][r] : -INFINITY;
       }
     }
-    publish();
   };
-  for (int32_t it = 0; it < n_tiles; it += 2) {
-    tile(it, IntC<0>{});
-    if (it + 1 < n_tiles) tile(it + 1, IntC<1>{});
+  auto row_max = [&](const float16_t (&s)[2]) __attribute__((always_inline)) {
+    float t = s[0][0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) t = fmaxf(t, s[0][r]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t = fmaxf(t, s[1][r]);
+    return half_max(t);
+  };
+  // Lazy running max: rescale only when a score exceeds m by more than 2^8
+  // (log2 units); the first visible key always raises. S values held in
+  // `s` and in the nblk_next blocks of `nx` (scores of the next tile already
+  // computed against the old m) are moved to the new m.
+  auto raise_max = [&](float tmax, float16_t (&s)[2], float16_t (&nx)[2], int nblk_next) __attribute__((always_inline)) {
+    const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
+    if (__any(raise)) {
+      const float base = (m == -INFINITY) ? 0.0f : m;
+      const float mn = fmaxf(m, base + tmax);
+      const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
+      const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[0][r] -= delta;
+        s[1][r] -= delta;
+      }
+      if (nblk_next > 0)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nx[0][r] -= delta;
+      if (nblk_next > 1)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) nx[1][r] -= delta;
+      m = mn;
+      const float nb = (mn == -INFINITY) ? 0.0f : -mn;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mtile[r] = nb;
+    }
+  };
+  const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
+  // exp2 of one S block, packed to fp16 in PV B-operand order; adds the
+  // probabilities to the running sum.
+  auto probs = [&](const float16_t &s, half8_t (&pb)[2], float &ls) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e]), (half_t)fast_exp2(s[8 * g2 + e + 1])};
+        ls = __builtin_amdgcn_fdot2(pp2, ones, ls, false);
+        pb[g2][e] = pp2.x;
+        pb[g2][e + 1] = pp2.y;
+      }
+    }
+  };
+  auto qk_block = [&](const uint8_t *kt, int blk, float16_t &acc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]),
+                                                   qf[c], c == 0 ? mtile : acc, 0, 0, 0);
+  };
+  auto pv_block = [&](const uint8_t *vt, int blk, const half8_t (&pb)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            *reinterpret_cast<const half8_t *>(vt + 32 * db * VRB + va[2 * blk + g2]), pb[g2], o[db], 0, 0, 0);
+  };
+
+  float16_t sx[2], sy[2];
+  int4 fl_cur = {};
+  if (n_tiles > 0) {
+    // K(0), V(0), K(1), K(2) in that order; K(2) may stay in flight.
+    load_k(0, IntC<0>{}, 0, NKL);
+    load_v(0, IntC<0>{}, 0, NVL);
+    if (n_tiles > 1) load_k(1, IntC<1>{}, 0, NKL);
+    if (n_tiles > 2) {
+      load_k(2, IntC<2>{}, 0, NKL);
+      fl_cur = publish(0, IntC<NKL>{});
+    } else {
+      fl_cur = publish(0, IntC<0>{});
+    }
+    qk_block(lds_k0, 0, sx[0]);
+    qk_block(lds_k0, 1, sx[1]);
+    __syncthreads();  // K(0)'s buffer is refilled by the first iteration
   }
+
+  // Iteration `it` with S(it) in `sc` and S(it + 1) computed into `sn`.
+  // K(it+1) is read from buffer (it+1) % 3 and K(it+3) loaded into buffer
+  // it % 3 (last read for QK(it) in iteration it - 1); V(it) is read from
+  // buffer it % 2 and V(it+1) loaded into buffer (it+1) % 2.
+  auto iter = [&](int32_t it, float16_t (&sc)[2], float16_t (&sn)[2], auto k3c, auto v2c)
+                  __attribute__((always_inline)) {
+    constexpr int K3 = decltype(k3c)::value, V2 = decltype(v2c)::value;
+    constexpr int KR = (K3 + 1) % 3;
+    const uint8_t *const kt = KR == 0 ? lds_k0 : KR == 1 ? lds_k1 : lds_k2;
+    const uint8_t *const vt = V2 ? lds_v1 : lds_v0;
+    const int32_t tb = tile_base(it);
+    const bool v_ahead = it + 1 < n_tiles, k_ahead = it + 3 < n_tiles;
+    if (v_ahead) load_v(it + 1, IntC<V2 ^ 1>{}, 0, NVL / 2);
+    // Tiles that are not fully visible go through the mask, which also
+    // covers tiles this wave sees nothing of (all slots -inf: P = 0, O and
+    // the row sum unchanged). S(i+1) of the last iteration is computed from
+    // stale LDS and never read.
+    if (!tile_full(tb, fl_cur)) apply_mask(sc, tb, fl_cur);
+    {
+      // Operand fragments stream 4 ahead of the MFMA that uses them (the
+      // scheduling groups below keep at most 4 in flight).
+      // Seg 1: QK(i+1) block 0 | running max of S(i)
+      qk_block(kt, 0, sn[0]);
+      const float tmax = row_max(sc);
+      PIPE_SGB(0x100, 4, 0);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        PIPE_SGB(0x008, 1, 0);
+        if (c + 4 < NCH) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x002, 2, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      raise_max(tmax, sc, sn, 1);
+      if (v_ahead) load_v(it + 1, IntC<V2 ^ 1>{}, NVL / 2, NVL);
+      // Seg 2: QK(i+1) block 1 | probabilities of S(i) block 0
+      half8_t pa[2], pb[2];
+      qk_block(kt, 1, sn[1]);
+      probs(sc[0], pa, lsum);
+      PIPE_SGB(0x100, 4, 0);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        PIPE_SGB(0x008, 1, 0);
+        if (c + 4 < NCH) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x400, 16 / NCH, 0);
+        PIPE_SGB(0x002, 16 / NCH, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // K copies go last: the end-of-tile wait leaves the newest NKL in flight.
+      if (k_ahead) load_k(it + 3, IntC<K3>{}, 0, NKL / 2);
+      // Seg 3: PV(i) block 0 | probabilities of S(i) block 1
+      pv_block(vt, 0, pa);
+      probs(sc[1], pb, lsum);
+      PIPE_SGB(0x100, 4, 0);
+#pragma unroll
+      for (int c = 0; c < 2 * NDB; ++c) {
+        PIPE_SGB(0x008, 1, 0);
+        if (c + 4 < 2 * NDB) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x400, 16 / (2 * NDB), 0);
+        PIPE_SGB(0x002, 16 / (2 * NDB), 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (k_ahead) load_k(it + 3, IntC<K3>{}, NKL / 2, NKL);
+      // Seg 4: PV(i) block 1
+      pv_block(vt, 1, pb);
+      PIPE_SGB(0x100, 4, 0);
+#pragma unroll
+      for (int c = 0; c < 2 * NDB; ++c) {
+        PIPE_SGB(0x008, 1, 0);
+        if (c + 4 < 2 * NDB) PIPE_SGB(0x100, 1, 0);
+      }
+    }
+    if (k_ahead) fl_cur = publish(it + 1, IntC<NKL>{});
+    else fl_cur = publish(it + 1, IntC<0>{});
+  };
+  // Unrolled by six: buffer indices (mod 3 for K, mod 2 for V and the
+  // score registers) stay compile-time constants.
+  for (int32_t it = 0; it < n_tiles; it += 6) {
+    iter(it, sx, sy, IntC<0>{}, IntC<0>{});
+    if (it + 1 >= n_tiles) break;
+    iter(it + 1, sy, sx, IntC<1>{}, IntC<1>{});
+    if (it + 2 >= n_tiles) break;
+    iter(it + 2, sx, sy, IntC<2>{}, IntC<0>{});
+    if (it + 3 >= n_tiles) break;
+    iter(it + 3, sy, sx, IntC<0>{}, IntC<1>{});
+    if (it + 4 >= n_tiles) break;
+    iter(it + 4, sx, sy, IntC<1>{}, IntC<0>{});
+    if (it + 5 >= n_tiles) break;
+    iter(it + 5, sy, sx, IntC<2>{}, IntC<1>{});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
 
   const float l = half_sum(lsum);
   if (!q_ok) return;
@@ -1039,11 +1148,11 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
     if (d.head_dim == 128) {
       if (int4) hipLaunchKernelGGL((prefill_stage_kernel<128, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
       else hipLaunchKernelGGL((prefill_stage_kernel<128, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      hipLaunchKernelGGL(prefill_direct_kernel<128>, grid, dim3(256), 0, stream, p, ws, mc, units);
+      hipLaunchKernelGGL(prefill_pipe_kernel<128>, grid, dim3(256), 0, stream, p, ws, mc, units);
     } else {
       if (int4) hipLaunchKernelGGL((prefill_stage_kernel<64, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
       else hipLaunchKernelGGL((prefill_stage_kernel<64, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      hipLaunchKernelGGL(prefill_direct_kernel<64>, grid, dim3(256), 0, stream, p, ws, mc, units);
+      hipLaunchKernelGGL(prefill_pipe_kernel<64>, grid, dim3(256), 0, stream, p, ws, mc, units);
     }
     return check_launch("paged_attention(prefill, staged)");
   }
