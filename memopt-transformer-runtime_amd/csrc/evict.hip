@@ -11,12 +11,17 @@
 //     counts one token per 32-token run, so no block is ever freed);
 //   * no seq_len cap (the reference rejects seq_len > 4096).
 // evict_cache: src/csrc/kv_cache.cu:379-483 (per (block, head) selection).
+#include <string>
+
 #include "common.hpp"
 #include "page_format.hpp"
 
 namespace memopt {
 
-static constexpr int kEvictThreads = 256;
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t u = __builtin_bit_cast(uint32_t, f);
@@ -65,65 +70,214 @@ __device__ void zero_row(const RowZero &z, int64_t page, int32_t pos, int32_t he
   }
 }
 
-// One workgroup per (seq, head). blockIdx.x = seq, blockIdx.y = head.
-__global__ __launch_bounds__(kEvictThreads) void evict_tokens_kernel(
+// Zeroes the evicted tokens of one (page, head) block of the INT4 page pool,
+// one wave per block: lane l = 8p + c owns tokens p and p + 8 and dims
+// [c D/8, (c+1) D/8) of the block, the slot layout of page_format.hpp.
+// Write-only stores of exactly the bytes of evicted tokens: K codes (D/16
+// contiguous bytes per token), V codes (2-byte units interleaved with the
+// other token) and the fp16 scales (adjacent per token pair).
+__device__ __forceinline__ void zero_int4_block(uint8_t *blk, int32_t D, int lane, bool e0, bool e1) {
+  if (!(e0 || e1)) return;
+  const Int4Page f(D);
+  const int32_t bpl = f.BPL, p = lane >> 3, c = lane & 7;
+  uint8_t *ks = blk + f.kcodes + lane * bpl, *vs = blk + f.vcodes + lane * bpl;
+  if (bpl == 16) {
+    const uint2 k8 = {0x88888888u, 0x88888888u};
+    if (e0) *reinterpret_cast<uint2 *>(ks) = k8;
+    if (e1) *reinterpret_cast<uint2 *>(ks + 8) = k8;
+  } else {
+    for (int i = 0; i < bpl / 2; ++i) {
+      if (e0) ks[i] = 0x88;
+      if (e1) ks[bpl / 2 + i] = 0x88;
+    }
+  }
+  if (e0 && e1) {
+    for (int u = 0; u < bpl / 4; ++u) reinterpret_cast<uint32_t *>(vs)[u] = 0x88888888u;
+  } else {
+    const int half = e0 ? 0 : 1;
+    for (int u = 0; u < bpl / 4; ++u) reinterpret_cast<uint16_t *>(vs + 4 * u)[half] = 0x8888u;
+  }
+  // the first lane of each 64-dim scale group writes the group's scales
+  const int32_t dpl = D / 8, g = (c * dpl) / 64;
+  if ((c * dpl) % 64 == 0) {
+    half_t *ksc = reinterpret_cast<half_t *>(blk + f.kscales), *vsc = reinterpret_cast<half_t *>(blk + f.vscales);
+    const int32_t i0 = g * 16 + 2 * p;
+    if (e0) { ksc[i0] = (half_t)1.0f; vsc[i0] = (half_t)1.0f; }
+    if (e1) { ksc[i0 + 1] = (half_t)1.0f; vsc[i0 + 1] = (half_t)1.0f; }
+  }
+}
+
+// Longest score row handled (the evicted-token bitmask lives in LDS).
+static constexpr int32_t kEvictMaxLen = 1 << 19;
+
+// One workgroup of NT threads per (seq, head): blockIdx.x = seq, blockIdx.y = head.
+// Thread tid owns tokens t = tid + i NT; with R > 0 their keys stay in
+// registers (rows up to R NT tokens are read once), with R == 0 the row is
+// streamed from memory in batches of 8 loads per pass.
+//  A. tau = key of the keep-th largest sink-boosted score, by a 4-pass 8-bit
+//     radix select (MSB first): per-wave LDS histograms of the digit among
+//     keys matching the prefix so far, then a parallel suffix sum over the
+//     256 bins picks the digit.
+//  B. evicted-token bitmask in LDS (key < tau, sinks excluded), then zero the
+//     evicted (token, head) rows.
+//  C. block votes: a full logical block whose every token is evicted votes
+//     is_block_free[phys] += 1; the vote that reaches H unlinks it. A head
+//     votes only after its own zeroing, so the H-th vote (the unlink) comes
+//     after every head has read the block-table entry.
+template <int NT, int R>
+__global__ __launch_bounds__(NT) void evict_tokens_kernel(
     const float *__restrict__ scores, int32_t *__restrict__ block_tables, int32_t *__restrict__ is_block_free,
     int32_t H, int32_t L, int32_t M, int64_t total_pool_blocks, int32_t keep, int32_t sinks, RowZero z) {
-  const int32_t n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  constexpr int NW = NT / 64;
+  const int32_t n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float *row = scores + ((int64_t)n * H + h) * L;
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[NW][256];
+  __shared__ uint32_t suf[257];
   __shared__ uint32_t s_prefix, s_k;
+  extern __shared__ uint32_t evbits[];  // (L + 63) / 64 * 2 words
 
-  // ---- Phase A: exact keep-th largest key (radix select, MSB first) ----
-  uint32_t prefix = 0, pmask = 0;
-  uint32_t k = (uint32_t)keep;  // rank (1-based) inside the current prefix class
+  const uint32_t sink_key = order_key(1e38f);
+  // All loads of a batch are issued first (index clamped into the row),
+  // then turned into keys: a load placed under the sink test would be waited
+  // on before the next one is issued.
+  auto keys_of = [&](int32_t t0, auto nc, uint32_t *kout) __attribute__((always_inline)) {
+    constexpr int N = decltype(nc)::value;
+    float v[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = row[min(t0 + j * NT, L - 1)];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const uint32_t kv = order_key(v[j]);
+      kout[j] = t0 + j * NT < sinks ? sink_key : kv;
+    }
+  };
+  uint32_t kreg[R > 0 ? R : 1];
+  if constexpr (R > 0) keys_of(tid, IntC<R>{}, kreg);
+  // Calls f(t, key) for every token of this thread.
+  auto for_keys = [&](auto f) __attribute__((always_inline)) {
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int32_t t = tid + i * NT;
+        if (t < L) f(t, kreg[i]);
+      }
+    } else {
+      for (int32_t base = 0; base < L; base += 8 * NT) {
+        uint32_t kb[8];
+        keys_of(base + tid, IntC<8>{}, kb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int32_t t = base + tid + j * NT;
+          if (t < L) f(t, kb[j]);
+        }
+      }
+    }
+  };
+
+  // ---- A: radix select ----
+  uint32_t prefix = 0, pmask = 0, k = (uint32_t)keep;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < 256; i += kEvictThreads) hist[i] = 0;
+    for (int i = tid; i < NW * 256; i += NT) (&hist[0][0])[i] = 0;
+    if (tid == 0) suf[256] = 0;
     __syncthreads();
-    for (int t = tid; t < L; t += kEvictThreads) {
-      const uint32_t key = (t < sinks) ? order_key(1e38f) : order_key(row[t]);
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 0xFF], 1u);
+    for_keys([&](int32_t, uint32_t key) {
+      if ((key & pmask) == prefix) atomicAdd(&hist[wave][(key >> shift) & 0xFF], 1u);
+    });
+    __syncthreads();
+    if (tid < 256) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) c += hist[w][tid];
+      suf[tid] = c;
     }
     __syncthreads();
-    if (tid == 0) {
-      uint32_t acc = 0;
-      int b = 255;
-      for (; b > 0; --b) {
-        if (acc + hist[b] >= k) break;
-        acc += hist[b];
-      }
-      s_prefix = prefix | ((uint32_t)b << shift);
-      s_k = k - acc;
+    for (int off = 1; off < 256; off <<= 1) {  // suf[i] := sum of bins >= i
+      const uint32_t v = (tid < 256 && tid + off < 256) ? suf[tid + off] : 0u;
+      __syncthreads();
+      if (tid < 256) suf[tid] += v;
+      __syncthreads();
+    }
+    if (tid < 256 && suf[tid] >= k && suf[tid + 1] < k) {
+      s_prefix = prefix | ((uint32_t)tid << shift);
+      s_k = k - suf[tid + 1];
     }
     __syncthreads();
     prefix = s_prefix;
     k = s_k;
     pmask |= 0xFFu << shift;
-    __syncthreads();
   }
-  const uint32_t tau = prefix;  // key of the keep-th largest boosted score
+  const uint32_t tau = prefix;
 
-  // ---- Phase B: zero evicted (token, head) rows ----
+  // ---- B: evicted bitmask (the 64 lanes of a wave hold 64 consecutive tokens) ----
+  const int32_t nwords = (L + 63) / 64 * 2;
+  for (int i = tid; i < nwords; i += NT) evbits[i] = 0;
+  __syncthreads();
+  for_keys([&](int32_t t, uint32_t key) {
+    const uint64_t m = __ballot(t >= sinks && key < tau);
+    if (lane == 0 && m) {
+      evbits[t / 32] = (uint32_t)m;
+      evbits[t / 32 + 1] = (uint32_t)(m >> 32);
+    }
+  });
+  __syncthreads();
+  auto ev = [&](int32_t t) { return (evbits[t >> 5] >> (t & 31)) & 1u; };
+
   const int32_t *bt = block_tables + (int64_t)n * M;
-  for (int t = tid; t < L; t += kEvictThreads) {
-    if (t < sinks) continue;
-    if (order_key(row[t]) >= tau) continue;
-    const int32_t lb = t / z.bs;
-    if (lb >= M) continue;
-    const int32_t phys = bt[lb];
-    if (phys < 0 || phys >= total_pool_blocks) continue;
-    zero_row(z, phys, t - lb * z.bs, h);
+  if (z.kv_format == MEMOPT_KV_INT4) {
+    const Int4Page f(z.D);
+    const int32_t nlb = min((L + 15) / 16, M);
+    const int32_t p = lane >> 3;
+    for (int32_t lb0 = wave * 64; lb0 < nlb; lb0 += NW * 64) {
+      const int32_t phys_l = lb0 + lane < nlb ? bt[lb0 + lane] : -1;
+      const int32_t cnt = min(64, nlb - lb0);
+      for (int i = 0; i < cnt; ++i) {
+        const int32_t lb = lb0 + i;
+        const uint32_t m16 = (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu;  // tokens 16 lb .. 16 lb + 15
+        const int32_t phys = __builtin_amdgcn_readlane(phys_l, i);
+        if (m16 == 0 || phys < 0 || phys >= total_pool_blocks) continue;  // wave-uniform
+        zero_int4_block((uint8_t *)z.k + ((int64_t)phys * z.H + h) * f.block, z.D, lane, (m16 >> p) & 1,
+                        (m16 >> (p + 8)) & 1);
+      }
+    }
+  } else {
+    for (int32_t t0 = wave * 64; t0 < L; t0 += NW * 64) {
+      const int32_t t = t0 + lane, lb = t / z.bs;
+      bool e = t < L && ev(t) && lb < M;
+      int32_t phys = -1;
+      if (e) {
+        phys = bt[lb];
+        e = phys >= 0 && phys < total_pool_blocks;
+      }
+      uint64_t mask = __ballot(e);
+      while (mask) {  // the wave zeroes each evicted row, 16 bytes per lane
+        const int j = __builtin_ctzll(mask);
+        mask &= mask - 1;
+        const int32_t tj = t0 + j, pj = __shfl(phys, j, 64), lbj = tj / z.bs;
+        const int64_t off = (((int64_t)pj * z.bs + (tj - lbj * z.bs)) * z.H + h) * (int64_t)z.D;
+        half_t *kr = (half_t *)z.k + off, *vr = (half_t *)z.v + off;
+        if ((z.D & 7) == 0) {
+          const uint4 zero = {0u, 0u, 0u, 0u};
+          for (int d = 8 * lane; d < z.D; d += 512) {
+            *reinterpret_cast<uint4 *>(kr + d) = zero;
+            *reinterpret_cast<uint4 *>(vr + d) = zero;
+          }
+        } else {
+          for (int d = lane; d < z.D; d += 64) {
+            kr[d] = (half_t)0.0f;
+            vr[d] = (half_t)0.0f;
+          }
+        }
+      }
+    }
   }
   __syncthreads();
 
-  // ---- Phase C: block votes (full blocks whose every position is evicted) ----
-  const int32_t nlb = min(L / z.bs, M);
-  for (int lb = tid; lb < nlb; lb += kEvictThreads) {
+  // ---- C: block votes ----
+  const int32_t nlb_full = min(L / z.bs, M);
+  for (int32_t lb = tid; lb < nlb_full; lb += NT) {
     bool all = true;
-    for (int j = 0; j < z.bs && all; ++j) {
-      const int t = lb * z.bs + j;
-      all = (t >= sinks) && (order_key(row[t]) < tau);
-    }
+    for (int j = 0; j < z.bs && all; ++j) all = ev(lb * z.bs + j);
     if (!all) continue;
     const int32_t phys = bt[lb];
     if (phys < 0 || phys >= total_pool_blocks) continue;
@@ -170,9 +324,24 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
   keep = keep < 1 ? 1 : (keep > seq_len ? seq_len : keep);
   RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key, p.value, p.key_scales, p.value_scales};
   const int32_t sinks = num_sink_tokens < 0 ? 0 : (num_sink_tokens > seq_len ? seq_len : num_sink_tokens);
-  hipLaunchKernelGGL(evict_tokens_kernel, dim3(num_seqs, num_heads), dim3(kEvictThreads), 0,
-                     (hipStream_t)stream, attention_scores, block_tables, is_block_free, num_heads, seq_len,
-                     max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
+  MEMOPT_REQUIRE(p.kv_format != MEMOPT_KV_INT4 || p.block_size == 16, MEMOPT_ERR_UNSUPPORTED,
+                 "evict_tokens: INT4 page pools use 16-token pages");
+  MEMOPT_REQUIRE(seq_len <= kEvictMaxLen, MEMOPT_ERR_UNSUPPORTED,
+                 "evict_tokens: seq_len > " + std::to_string(kEvictMaxLen) + " not supported");
+  const size_t lds = (size_t)((seq_len + 63) / 64 * 2) * sizeof(uint32_t);
+  const dim3 grid(num_seqs, num_heads);
+  hipStream_t st = (hipStream_t)stream;
+  // Rows up to 8192 (32768) tokens keep their keys in registers with 256
+  // (1024) threads; longer rows stream with 1024 threads.
+  if (seq_len <= 256 * 32)
+    hipLaunchKernelGGL((evict_tokens_kernel<256, 32>), grid, dim3(256), lds, st, attention_scores, block_tables,
+                       is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
+  else if (seq_len <= 1024 * 32)
+    hipLaunchKernelGGL((evict_tokens_kernel<1024, 32>), grid, dim3(1024), lds, st, attention_scores, block_tables,
+                       is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
+  else
+    hipLaunchKernelGGL((evict_tokens_kernel<1024, 0>), grid, dim3(1024), lds, st, attention_scores, block_tables,
+                       is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
   return check_launch("evict_tokens");
 }
 
