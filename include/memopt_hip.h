@@ -83,6 +83,15 @@ int memopt_pool_info(int64_t *num_blocks, int32_t *block_size, int32_t *num_head
 /* Drops the pool (storage pointers are forgotten; the caller frees them). */
 int memopt_reset_pool(void);
 
+/* Swaps the live pool's storage and format (fp16 <-> INT4 pages) for the same
+ * geometry, keeping the free list, so block tables stay valid across the
+ * switch. No counterpart in the reference: it serves the policy forward
+ * wrapper that applies MemoryScheduler.use_int4 (src/memopt/scheduler.py:15-18
+ * documents the switch; no reference code performs it). The caller fills the
+ * new storage (memopt_write_cache into INT4 pages, memopt_int4_pages_to_fp16
+ * into fp16 pools) on the stream before using the pool. */
+int memopt_pool_set_storage(int32_t kv_format, void *key_pool, void *value_pool);
+
 /* Replaces allocate_block() — src/csrc/kv_cache.cu:163-172. *block_idx = -1
  * when exhausted (not an error). */
 int memopt_allocate_block(int64_t *block_idx);
@@ -147,6 +156,14 @@ int memopt_quantize_kv_cache_int4(const void *cache, int64_t numel, int64_t last
 int memopt_dequantize_kv_cache_int4(const uint8_t *packed, int64_t packed_numel,
                                     const float *scales, int64_t num_scales,
                                     int32_t group_size, void *out, void *stream);
+
+/* Dequantizes an INT4 page pool [num_blocks, H, B] into fp16 pools
+ * key_out/value_out [num_blocks, 16, H, D]: value = fp16(RN(float(code-8) *
+ * page scale)), the dequantize_kv_cache_int4 arithmetic of
+ * src/csrc/quantization.cu:232-270 applied to this build's page layout
+ * (fp16 page scales). head_dim 64 or 128. */
+int memopt_int4_pages_to_fp16(const uint8_t *pages, int64_t num_blocks, int32_t num_heads,
+                              int32_t head_dim, void *key_out, void *value_out, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Paged attention                                                          */

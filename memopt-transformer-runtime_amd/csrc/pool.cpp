@@ -94,6 +94,27 @@ int memopt_init_pool(int64_t num_blocks, int32_t block_size, int32_t num_heads,
   return MEMOPT_OK;
 }
 
+int memopt_pool_set_storage(int32_t kv_format, void *key_pool, void *value_pool) {
+  std::lock_guard<std::mutex> lk(g_pool.mu);
+  PoolView &v = g_pool.view;
+  MEMOPT_REQUIRE(v.initialized, MEMOPT_ERR_STATE, "pool_set_storage: pool not initialized");
+  MEMOPT_REQUIRE(kv_format == MEMOPT_KV_FP16 || kv_format == MEMOPT_KV_INT4, MEMOPT_ERR_INVALID,
+                 "pool_set_storage: unknown kv_format");
+  if (kv_format == MEMOPT_KV_INT4) {
+    MEMOPT_REQUIRE(v.head_dim % 64 == 0 && v.block_size == 16, MEMOPT_ERR_INVALID,
+                   "pool_set_storage: INT4 pools need 16-token pages and head_dim % 64 == 0");
+    MEMOPT_REQUIRE(key_pool, MEMOPT_ERR_INVALID, "pool_set_storage: null page buffer");
+    value_pool = nullptr;
+  } else {
+    MEMOPT_REQUIRE(key_pool && value_pool, MEMOPT_ERR_INVALID, "pool_set_storage: null pool storage");
+  }
+  v.kv_format = kv_format;
+  v.key = key_pool;
+  v.value = value_pool;
+  v.key_scales = v.value_scales = nullptr;
+  return MEMOPT_OK;
+}
+
 int memopt_pool_info(int64_t *num_blocks, int32_t *block_size, int32_t *num_heads,
                      int32_t *head_dim, int32_t *kv_format) {
   std::lock_guard<std::mutex> lk(g_pool.mu);

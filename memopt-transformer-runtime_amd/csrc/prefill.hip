@@ -594,8 +594,18 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams 
   if (unit >= units) return;  // wave-uniform
   const int32_t lc = unit % MC, bh = unit / MC, h = bh % p.H, b = bh / p.H;
   const int pp = lane >> 3, c = lane & 7;
-  const int32_t kv_lim = min(p.ctx[b], p.M * p.bs);
+  const int32_t ctx = p.ctx[b];
+  const int32_t kv_lim = min(ctx, p.M * p.bs);
   const int32_t key0 = lc * 16;
+  {
+    // Only the 64-key tiles some query tile of this sequence visits are
+    // staged: the sink tiles and [window start of the first query, kv_lim).
+    // The attention kernel reads neither data nor flags of other chunks.
+    const int32_t win_lo = max(0, p.causal ? ctx - p.Lq - p.W + 1 : ctx - p.W);
+    const int32_t sink_chunks = 4 * ((min(p.sinks, kv_lim) + 63) / 64);
+    const int32_t lo = 4 * (win_lo / 64), hi = 4 * ((kv_lim + 63) / 64);
+    if (lc >= sink_chunks && (lc < lo || lc >= hi)) return;  // wave-uniform
+  }
   int32_t pg = -1;
   if (key0 < kv_lim) {
     const int32_t e = p.bt[(int64_t)b * p.M + key0 / p.bs];

@@ -263,6 +263,53 @@ __global__ __launch_bounds__(kThreads) void write_int4_pages_kernel(
   }
 }
 
+// INT4 page pool -> fp16 pools [nb, 16, H, D] (K and V): one wave per
+// (page, head), lane l = 8p + c decodes tokens p and p + 8 over dims
+// [c D/8, (c+1) D/8) (page_format.hpp). value = fp16(RN(float(code - 8) *
+// scale)) with the page's fp16 scale, the values the attention kernels use.
+template <int D>
+__global__ __launch_bounds__(256) void int4_pages_to_fp16_kernel(const uint8_t *__restrict__ pages, int64_t units,
+                                                                 int32_t H, half_t *__restrict__ kout,
+                                                                 half_t *__restrict__ vout) {
+  constexpr int DPL = D / 8;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= units) return;
+  const Int4Page f(D);
+  const int lane = threadIdx.x & 63, p = lane >> 3, c = lane & 7, g = (c * DPL) / 64;
+  const int64_t page = unit / H;
+  const int32_t h = (int32_t)(unit % H);
+  const uint8_t *blk = pages + unit * f.block;
+  const half_t *ksc = reinterpret_cast<const half_t *>(blk + f.kscales);
+  const half_t *vsc = reinterpret_cast<const half_t *>(blk + f.vscales);
+  const uint8_t *kb = blk + f.kcodes + lane * DPL, *vb = blk + f.vcodes + lane * DPL;
+#pragma unroll
+  for (int tok = 0; tok < 2; ++tok) {
+    const float sk = (float)ksc[g * 16 + 2 * p + tok], sv = (float)vsc[g * 16 + 2 * p + tok];
+    half_t ko[DPL], vo[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) {
+      const uint32_t byte = kb[tok * (DPL / 2) + i];
+      ko[2 * i] = (half_t)((float)((int)(byte & 15u) - 8) * sk);
+      ko[2 * i + 1] = (half_t)((float)((int)(byte >> 4) - 8) * sk);
+    }
+#pragma unroll
+    for (int u = 0; u < DPL / 4; ++u) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const uint32_t byte = vb[4 * u + 2 * tok + b];
+        vo[4 * u + 2 * b] = (half_t)((float)((int)(byte & 15u) - 8) * sv);
+        vo[4 * u + 2 * b + 1] = (half_t)((float)((int)(byte >> 4) - 8) * sv);
+      }
+    }
+    const int64_t row = ((page * 16 + p + 8 * tok) * H + h) * (int64_t)D + c * DPL;
+#pragma unroll
+    for (int i = 0; i < DPL / 8; ++i) {
+      *reinterpret_cast<uint4 *>(kout + row + 8 * i) = *reinterpret_cast<const uint4 *>(ko + 8 * i);
+      *reinterpret_cast<uint4 *>(vout + row + 8 * i) = *reinterpret_cast<const uint4 *>(vo + 8 * i);
+    }
+  }
+}
+
 }  // namespace memopt
 
 using namespace memopt;
@@ -367,6 +414,24 @@ int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
                          num_heads, head_dim, n_slots);
   }
   return check_launch("write_cache");
+}
+
+int memopt_int4_pages_to_fp16(const uint8_t *pages, int64_t num_blocks, int32_t num_heads, int32_t head_dim,
+                              void *key_out, void *value_out, void *stream) {
+  MEMOPT_REQUIRE(num_blocks >= 0 && num_heads > 0, MEMOPT_ERR_INVALID, "int4_pages_to_fp16: bad sizes");
+  MEMOPT_REQUIRE(head_dim == 64 || head_dim == 128, MEMOPT_ERR_UNSUPPORTED,
+                 "int4_pages_to_fp16: head_dim must be 64 or 128");
+  if (num_blocks == 0) return MEMOPT_OK;
+  MEMOPT_REQUIRE(pages && key_out && value_out, MEMOPT_ERR_INVALID, "int4_pages_to_fp16: null pointer");
+  const int64_t units = num_blocks * num_heads;
+  const dim3 grid((unsigned)((units + 3) / 4));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(int4_pages_to_fp16_kernel<128>, grid, dim3(256), 0, (hipStream_t)stream, pages, units,
+                       num_heads, (half_t *)key_out, (half_t *)value_out);
+  else
+    hipLaunchKernelGGL(int4_pages_to_fp16_kernel<64>, grid, dim3(256), 0, (hipStream_t)stream, pages, units,
+                       num_heads, (half_t *)key_out, (half_t *)value_out);
+  return check_launch("int4_pages_to_fp16");
 }
 
 }  // extern "C"

@@ -87,6 +87,8 @@ _lib.memopt_get_hello.restype = ctypes.c_char_p
 _c_init_pool = _sig("memopt_init_pool", [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp])
 _c_pool_info = _sig("memopt_pool_info", [ctypes.POINTER(_i64)] + [ctypes.POINTER(_i32)] * 4)
 _c_reset_pool = _sig("memopt_reset_pool", [])
+_c_set_storage = _sig("memopt_pool_set_storage", [_i32, _vp, _vp])
+_c_pages_to_fp16 = _sig("memopt_int4_pages_to_fp16", [_vp, _i64, _i32, _i32, _vp, _vp, _vp])
 _c_alloc = _sig("memopt_allocate_block", [ctypes.POINTER(_i64)])
 _c_free = _sig("memopt_free_block", [_i64])
 _c_free_count = _sig("memopt_free_blocks_count", [ctypes.POINTER(_i64)])
@@ -182,6 +184,13 @@ def init_pool(num_blocks: int, block_size: int, num_heads: int, head_dim: int,
         _pool.update(fmt=fmt, nb=num_blocks, bs=block_size, h=num_heads, d=head_dim)
 
 
+def reset_pool() -> None:
+    """Drop the pool (storage and free list); the next ``init_pool`` starts fresh."""
+    with _pool_lock:
+        _pool.clear()
+        _c_reset_pool()
+
+
 def int4_layout(head_dim: int) -> dict:
     """Byte offsets of the regions of one (page, head) block of the INT4 page
     pool (include/memopt_hip.h MEMOPT_KV_INT4)."""
@@ -238,6 +247,11 @@ def get_int4_pages() -> torch.Tensor:
     return p["pages"]
 
 
+def pool_kv_format() -> str:
+    """Storage format of the live pool: ``"fp16"`` or ``"int4"``."""
+    return "int4" if _pool_or_raise("pool_kv_format")["fmt"] == KV_INT4 else "fp16"
+
+
 def get_key_pool() -> torch.Tensor:
     return _pool_or_raise("get_key_pool")["k"]
 
@@ -251,6 +265,69 @@ def get_pool_scales() -> Tuple[torch.Tensor, torch.Tensor]:
     p = _pool_or_raise("get_pool_scales")
     _require(p["fmt"] == KV_INT4, "get_pool_scales: pool is not an INT4 pool")
     return p["ks"], p["vs"]
+
+
+def dequantize_int4_pages(pages: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Dequantize an INT4 page buffer ``[nb, H, block]`` (default: the live pool)
+    into fresh fp16 ``(K, V)`` pools ``[nb, 16, H, D]``.
+
+    Each value is ``fp16(float(code - 8) * page_scale)``, the arithmetic of
+    the reference dequantize kernel (src/csrc/quantization.cu:232-270) on this
+    build's page layout; the attention kernels read the same values.
+    """
+    p = _pool_or_raise("dequantize_int4_pages")
+    if pages is None:
+        _require(p["fmt"] == KV_INT4, "dequantize_int4_pages: pool is not an INT4 pool")
+        pages, D = p["pages"], p["d"]
+    else:
+        _require(pages.dim() == 3 and pages.dtype == torch.uint8, "dequantize_int4_pages: pages must be u8 [nb, H, B]")
+        D = next((d for d in (64, 128) if int4_layout(d)["block"] == pages.shape[2]), None)
+        _require(D is not None, "dequantize_int4_pages: block size matches no supported head_dim (64, 128)")
+        _cuda(pages, "pages", "dequantize_int4_pages")
+    pages = pages.contiguous()
+    nb, H = pages.shape[0], pages.shape[1]
+    k = torch.empty((nb, 16, H, D), dtype=torch.float16, device=pages.device)
+    v = torch.empty_like(k)
+    with torch.cuda.device(pages.device):
+        _check(_c_pages_to_fp16(pages.data_ptr(), nb, H, D, k.data_ptr(), v.data_ptr(), _stream(pages)))
+    return k, v
+
+
+def convert_pool(kv_format: str) -> None:
+    """Switch the live pool between ``"fp16"`` and ``"int4"`` storage in place.
+
+    The free list and every block table stay valid: fp16 pages are quantized
+    into INT4 pages (what ``write_cache`` into an INT4 pool would store for
+    the same rows), INT4 pages are dequantized into fp16 pools. This is the
+    switch MemoryScheduler.use_int4 asks for (src/memopt/scheduler.py:15-18);
+    the reference has no code that performs it.
+    """
+    fmt = _FORMATS.get(kv_format)
+    _require(fmt is not None, f"convert_pool: kv_format must be one of {sorted(_FORMATS)}")
+    with _pool_lock:
+        p = _pool_or_raise("convert_pool")
+        if p["fmt"] == fmt:
+            return
+        nb, bs, H, D = p["nb"], p["bs"], p["h"], p["d"]
+        dev = p["k"].device
+        if fmt == KV_INT4:
+            _require(bs == 16 and D % 64 == 0, "convert_pool: INT4 pools need 16-token pages and head_dim % 64 == 0")
+            lay = int4_layout(D)
+            pages = torch.empty((nb, H, lay["block"]), dtype=torch.uint8, device=dev)
+            old_k, old_v = p["k"], p["v"]
+            _check(_c_set_storage(KV_INT4, pages.data_ptr(), None))
+            slots = torch.arange(nb * bs, dtype=torch.int32, device=dev)
+            with torch.cuda.device(dev):
+                _check(_c_write(old_k.data_ptr(), old_v.data_ptr(), nb * bs, H, D, slots.data_ptr(),
+                                _stream(old_k)))
+            _pool.update(fmt=fmt, pages=pages, k=pages[:, :, lay["kcodes"]:lay["vcodes"]],
+                         v=pages[:, :, lay["vcodes"]:lay["kscales"]],
+                         ks=pages[:, :, lay["kscales"]:lay["vscales"]].view(torch.float16),
+                         vs=pages[:, :, lay["vscales"]:].view(torch.float16))
+        else:
+            k, v = dequantize_int4_pages()
+            _check(_c_set_storage(KV_FP16, k.data_ptr(), v.data_ptr()))
+            _pool.update(fmt=fmt, pages=None, k=k, v=v, ks=None, vs=None)
 
 
 # ---------------------------------------------------------------------------
