@@ -188,7 +188,7 @@ def bench_prefill(torch, memopt_C, cfg, steps=10, warmup=3):
     tflops = flops / (launch_ms * 1e-3) / 1e12
     return {"workload": "BASELINE configs[3]: B 1, seq 16384, 32 heads, head_dim 128, INT4 16-token pages, "
                         "causal window 4096 + 4 sinks, all 16384 queries",
-            "kernel": "prefill_stage_kernel<128, true> + prefill_direct_kernel<128>", "kernel_ms": round(launch_ms, 4),
+            "kernel": "prefill_stage_kernel<128, true> + prefill_pipe_kernel<128>", "kernel_ms": round(launch_ms, 4),
             "flops": flops, "TFLOP/s": round(tflops, 1), "peak_TFLOP/s": MFMA_F16_PEAK_TFLOPS,
             "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "write_cache_ms": round(write_ms, 4)}

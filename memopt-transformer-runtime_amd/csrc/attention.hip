@@ -120,9 +120,6 @@ __global__ __launch_bounds__(64) void generic_attention_kernel(const GenericPara
 
 static bool aligned_to(const void *p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
 
-static int32_t effective_window(int32_t window, int32_t max_seq_len) {
-  return (window <= 0 || window > max_seq_len) ? max_seq_len : window;
-}
 
 // Upper bound of pages one sequence visits (sizes the split count).
 static int32_t max_pages_visited(const memopt_attn_desc &d) {

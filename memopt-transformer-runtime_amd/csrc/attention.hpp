@@ -28,6 +28,12 @@ __host__ __device__ inline KeyRange key_range(int32_t ctx, int32_t pos, int32_t 
   return r;
 }
 
+// Window of the reference signature: W <= 0 or W > max_seq_len means
+// max_seq_len (src/csrc/attention.cu:453-455).
+inline int32_t effective_window(int32_t window, int32_t max_seq_len) {
+  return (window <= 0 || window > max_seq_len) ? max_seq_len : window;
+}
+
 struct DecodeParams {
   const half_t *q;
   half_t *out;

@@ -27,8 +27,6 @@
 //  * tiles wholly inside every query's visible range skip the mask; the
 //    running max is raised lazily (rescale only when exceeded by > 8 in log2
 //    units).
-#include <cstdlib>
-
 #include "attention.hpp"
 #include "page_format.hpp"
 
@@ -571,11 +569,36 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
 // the next column (vt_col of K-tile row 2p).
 __device__ __forceinline__ int chunk_vcol(int p) { return 8 * ((p >> 1) & 1) + 4 * (p >> 2) + 2 * (p & 1); }
 
-// Workspace block of one (sequence, head, 16-token chunk): 2*16*D fp16 =
+// Workspace block of one (sequence, head, staged chunk): 2*16*D fp16 =
 // K part [16 rows][D] then V^T part [D rows][16 columns]. Blocks are ordered
-// [sequence][head][chunk], so the chunks of one (sequence, head) are one
-// contiguous run. After all blocks comes one int32 per (sequence, chunk): 1
+// [sequence][head][slot], so the chunks of one (sequence, head) are one
+// contiguous run. After all blocks comes one int32 per (sequence, slot): 1
 // if its page is linked.
+//
+// Only the chunks some query tile of a sequence visits are staged: the sink
+// tiles [0, sc) and the window tiles [lo, hi) (64-key aligned). Chunk lc sits
+// in slot lc < sc ? lc : lc - off, off = max(0, lo - sc), so a sequence uses
+// hi - off slots: about (q_len + W) / 16 for causal calls, however long the
+// context is.
+struct StageMap {
+  int32_t sc, off, hi;  // sink chunks, slot offset of the window chunks, end chunk
+  __host__ __device__ int32_t slot(int32_t lc) const { return lc < sc ? lc : lc - off; }
+};
+
+__host__ __device__ inline StageMap stage_map(int32_t ctx, int32_t max_tokens, int32_t Lq, int32_t W, int32_t sinks,
+                                              bool causal) {
+  const int32_t kv_lim = ctx < max_tokens ? ctx : max_tokens;
+  int32_t win_lo = causal ? ctx - Lq - W + 1 : ctx - W;
+  win_lo = win_lo > 0 ? win_lo : 0;
+  const int32_t s = sinks < kv_lim ? sinks : kv_lim;
+  StageMap m;
+  m.sc = 4 * (((s > 0 ? s : 0) + 63) / 64);
+  m.hi = kv_lim > 0 ? 4 * ((kv_lim + 63) / 64) : 0;
+  const int32_t lo = 4 * (win_lo / 64);
+  m.off = lo > m.sc ? lo - m.sc : 0;
+  return m;
+}
+
 template <int D>
 struct StageLayout {
   static constexpr int64_t kBlock = 2 * 16 * D * 2;  // bytes
@@ -592,20 +615,14 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams 
   const int lane = threadIdx.x & 63;
   const int32_t unit = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (unit >= units) return;  // wave-uniform
-  const int32_t lc = unit % MC, bh = unit / MC, h = bh % p.H, b = bh / p.H;
+  const int32_t slot = unit % MC, bh = unit / MC, h = bh % p.H, b = bh / p.H;
   const int pp = lane >> 3, c = lane & 7;
   const int32_t ctx = p.ctx[b];
   const int32_t kv_lim = min(ctx, p.M * p.bs);
+  const StageMap sm = stage_map(ctx, p.M * p.bs, p.Lq, p.W, p.sinks, p.causal != 0);
+  if (slot >= sm.hi - sm.off) return;  // wave-uniform: no chunk maps here
+  const int32_t lc = slot < sm.sc ? slot : slot + sm.off;
   const int32_t key0 = lc * 16;
-  {
-    // Only the 64-key tiles some query tile of this sequence visits are
-    // staged: the sink tiles and [window start of the first query, kv_lim).
-    // The attention kernel reads neither data nor flags of other chunks.
-    const int32_t win_lo = max(0, p.causal ? ctx - p.Lq - p.W + 1 : ctx - p.W);
-    const int32_t sink_chunks = 4 * ((min(p.sinks, kv_lim) + 63) / 64);
-    const int32_t lo = 4 * (win_lo / 64), hi = 4 * ((kv_lim + 63) / 64);
-    if (lc >= sink_chunks && (lc < lo || lc >= hi)) return;  // wave-uniform
-  }
   int32_t pg = -1;
   if (key0 < kv_lim) {
     const int32_t e = p.bt[(int64_t)b * p.M + key0 / p.bs];
@@ -698,7 +715,7 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams 
   for (int d = 0; d < DPL; ++d)
     *reinterpret_cast<uint32_t *>(blk + L::kVPart + (c * DPL + d) * 32 + vc * 2) = vw[d];
   if (h == 0 && lane == 0)
-    reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + lc] = pg >= 0 ? 1 : 0;
+    reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + slot] = pg >= 0 ? 1 : 0;
 }
 
 template <int N>
@@ -830,6 +847,8 @@ __global__ __launch_bounds__(256, 2) void prefill_pipe_kernel(const PrefillParam
   };
 
   const int32_t *vrow = reinterpret_cast<const int32_t *>(ws + (int64_t)units * L::kBlock) + (int64_t)b * MC;
+  const StageMap sm = stage_map(ctx, p.M * p.bs, p.Lq, p.W, p.sinks, causal);
+  auto tile_slot = [&](int32_t it) { return (uint32_t)sm.slot(tile_base(it) / 16); };
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(ws + ((int64_t)b * p.H + h) * MC * L::kBlock), (short)0, (int)(MC * CS), 0x00020000);
   uint32_t kvoff, vvoff;
@@ -846,7 +865,7 @@ __global__ __launch_bounds__(256, 2) void prefill_pipe_kernel(const PrefillParam
   // segments of an iteration so the copies are not issued in one burst.
   auto load_k = [&](int32_t it, auto bufc, int c0, int c1) __attribute__((always_inline)) {
     constexpr int buf = decltype(bufc)::value;
-    const uint32_t cb = (uint32_t)(tile_base(it) / 16) * CS;
+    const uint32_t cb = tile_slot(it) * CS;
 #pragma unroll
     for (int cl = c0; cl < c1; ++cl) {
       const uint32_t k = (uint32_t)(cl * 256 + wave * 64) / (16 * KC);
@@ -855,7 +874,7 @@ __global__ __launch_bounds__(256, 2) void prefill_pipe_kernel(const PrefillParam
   };
   auto load_v = [&](int32_t it, auto bufc, int c0, int c1) __attribute__((always_inline)) {
     constexpr int buf = decltype(bufc)::value;
-    const uint32_t cb = (uint32_t)(tile_base(it) / 16) * CS + (uint32_t)L::kVPart;
+    const uint32_t cb = tile_slot(it) * CS + (uint32_t)L::kVPart;
 #pragma unroll
     for (int cl = c0; cl < c1; ++cl) buffer_load_lds16_m0(rs, (buf ? mv1 : mv0) + cl * 4096, vvoff, cb + cl * 1024);
   };
@@ -866,7 +885,7 @@ __global__ __launch_bounds__(256, 2) void prefill_pipe_kernel(const PrefillParam
   // returns); then the barrier publishes the copies of all threads.
   auto publish = [&](int32_t next_it, auto keepc) __attribute__((always_inline)) {
     constexpr int keep = decltype(keepc)::value;
-    const int32_t *fp = vrow + (next_it < n_tiles ? tile_base(next_it) / 16 : 0);
+    const int32_t *fp = vrow + (next_it < n_tiles ? tile_slot(next_it) : 0);
     int4 f;
     if constexpr (keep == 0)
       asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt vmcnt(0) lgkmcnt(0)" : "=s"(f) : "s"(fp) : "memory");
@@ -1113,14 +1132,20 @@ bool prefill_supported(const memopt_attn_desc &d) {
   return d.kv_head_stride == D && d.kv_token_stride == H * D && d.kv_page_stride == d.block_size * H * D;
 }
 
-// 16-token chunks staged per sequence: the block table's span rounded up to
-// whole 64-key tiles, so a tile never reads past its sequence's chunks.
+// Staged slots per sequence: the sink tiles plus the window tiles a call can
+// visit (stage_map), bounded without reading context_lens: keys
+// [ctx - q_len - W + 1, ctx) for causal calls ([ctx - W, ctx) otherwise),
+// plus one tile of alignment; never more than the block table's span.
 static int64_t staged_chunks(const memopt_attn_desc &d) {
-  return ((int64_t)d.max_blocks_per_seq * d.block_size / 16 + 3) / 4 * 4;
+  const int64_t full = ((int64_t)d.max_blocks_per_seq * d.block_size / 16 + 3) / 4 * 4;
+  const int64_t W = effective_window(d.window_size, d.max_seq_len);
+  const int64_t span = d.causal ? (int64_t)d.q_len + W - 1 : W;
+  const int64_t sinks = d.num_sink_tokens > 0 ? d.num_sink_tokens : 0;
+  const int64_t bound = 4 * ((span + 63) / 64 + 1) + 4 * ((sinks + 63) / 64);
+  return bound < full ? bound : full;
 }
 
 int64_t prefill_workspace_bytes(const memopt_attn_desc &d) {
-  if (std::getenv("MEMOPT_PREFILL_STAGED") && std::atoi(std::getenv("MEMOPT_PREFILL_STAGED")) == 0) return 0;
   const int64_t mc = staged_chunks(d);
   const int64_t units = (int64_t)d.batch * mc * d.num_heads;
   // one sequence's chunks must stay inside a 31-bit buffer range
@@ -1166,29 +1191,19 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
     }
     return check_launch("paged_attention(prefill, staged)");
   }
-  int nw = 4, tk = 64;
-  if (const char *e = std::getenv("MEMOPT_PREFILL_WAVES")) nw = std::atoi(e) == 8 ? 8 : 4;
-  if (const char *e = std::getenv("MEMOPT_PREFILL_TILE")) tk = std::atoi(e) == 32 ? 32 : 64;
-  if (tk == 32) nw = 4;
-  const int64_t n_wg = (int64_t)((d.q_len + 32 * nw - 1) / (32 * nw)) * d.num_heads * d.batch;
+  // In-kernel staging (no workspace, or a workspace range beyond 31 bits):
+  // 4 waves x 32 queries, 64-key tiles dequantized into LDS by the workgroup.
+  const int64_t n_wg = (int64_t)((d.q_len + 127) / 128) * d.num_heads * d.batch;
   MEMOPT_REQUIRE(n_wg < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "paged_attention: too many query tiles");
   const dim3 grid((unsigned)n_wg);
   const bool int4 = d.kv_format == MEMOPT_KV_INT4;
-#define MEMOPT_PREFILL_LAUNCH(D_, NW_, TK_)                                                                       \
-  do {                                                                                                          \
-    if (int4) hipLaunchKernelGGL((prefill_kernel<D_, true, NW_, 1, TK_>), grid, dim3(NW_ * 64), 0, stream, p);  \
-    else hipLaunchKernelGGL((prefill_kernel<D_, false, NW_, 1, TK_>), grid, dim3(NW_ * 64), 0, stream, p);      \
-  } while (0)
   if (d.head_dim == 128) {
-    if (tk == 32) MEMOPT_PREFILL_LAUNCH(128, 4, 32);
-    else if (nw == 8) MEMOPT_PREFILL_LAUNCH(128, 8, 64);
-    else MEMOPT_PREFILL_LAUNCH(128, 4, 64);
+    if (int4) hipLaunchKernelGGL((prefill_kernel<128, true, 4, 1, 64>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<128, false, 4, 1, 64>), grid, dim3(256), 0, stream, p);
   } else {
-    if (tk == 32) MEMOPT_PREFILL_LAUNCH(64, 4, 32);
-    else if (nw == 8) MEMOPT_PREFILL_LAUNCH(64, 8, 64);
-    else MEMOPT_PREFILL_LAUNCH(64, 4, 64);
+    if (int4) hipLaunchKernelGGL((prefill_kernel<64, true, 4, 1, 64>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((prefill_kernel<64, false, 4, 1, 64>), grid, dim3(256), 0, stream, p);
   }
-#undef MEMOPT_PREFILL_LAUNCH
   return check_launch("paged_attention(prefill)");
 }
 

@@ -658,6 +658,11 @@ class PreparedAttention:
                 num_sink_tokens, causal, key_scales, value_scales, kv_layout, out)
         self._dp = ctypes.byref(self._d) if self._d is not None else None
 
+    @property
+    def workspace_bytes(self) -> int:
+        """Device workspace held for the call (split-K partials or staged K/V)."""
+        return 0 if self._ws is None else self._ws.numel() * self._ws.element_size()
+
     def __call__(self, stream: Optional[int] = None) -> torch.Tensor:
         if self._dp is not None:
             s = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream

@@ -243,3 +243,31 @@ def test_cache_exhaustion_and_free():
     assert cache.length(7) == 60 and memopt_C.free_blocks_count() == 0
     cache.free_sequence(7)
     assert memopt_C.free_blocks_count() == 4
+
+
+def test_chunk_call_workspace_is_bounded_by_the_window():
+    """A chunk call over the end of a long context stages only the sink tiles
+    and the tiles its queries' windows reach, so its workspace does not grow
+    with the context (the property AutoChunk's budget relies on)."""
+    R = _runtime()
+    H, D, S, Lq, W, sinks = 8, 128, 16384, 256, 1024, 4
+    cache = R.PagedKVCache(S // 16 + 4, H, D, kv_format="int4")
+    cache.add_sequence(0)
+    k = torch.randn(S, H, D, device=dev(), dtype=torch.float16)
+    cache.append([0], k[None], k[None])
+    bt, ctx, _ = R.attention_inputs(cache, [0])
+    kp, vp = cache.key_value_pools()
+    q = torch.randn(1, Lq, H, D, device=dev(), dtype=torch.float16)
+    win = memopt_C.PreparedAttention(q, kp, vp, bt, ctx, S, W, num_sink_tokens=sinks, causal=True)
+    full = memopt_C.PreparedAttention(q, kp, vp, bt, ctx, S, -1, num_sink_tokens=sinks, causal=True)
+    slots = 4 * ((Lq + W - 1 + 63) // 64 + 1) + 4  # window tiles + alignment + one sink tile
+    assert win.workspace_bytes == slots * H * 64 * D + slots * 4
+    assert full.workspace_bytes == (S // 16) * H * 64 * D + (S // 16) * 4
+    chunk_bytes = R.chunk_call_bytes(Lq, S, H, D, W)
+    assert win.workspace_bytes <= chunk_bytes
+    # and the call is right: same rows as the whole-window reference on the dequantized pool
+    out = win()
+    kd, vd = O.from_int4_pages(memopt_C.get_int4_pages().cpu().numpy(), D)
+    want = O.paged_attention(q.cpu().numpy(), kd, vd, bt.cpu().numpy(), ctx.cpu().numpy(), S, W, sinks,
+                             causal=True)
+    assert_close(out, want, what="chunk call at the end of a long context")
