@@ -771,14 +771,15 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p) {
 //    buffers of K(i) and V(i-1), both last read in iteration i-1.
 //  * Workgroup IDs are remapped so that each XCD owns whole heads (a head's
 //    window stays in one L2), longest causal query tiles first.
-template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_pipe_kernel(const PrefillParams p, const uint8_t *__restrict__ ws,
-                                                              int32_t MC, int32_t units) {
-  constexpr int NW = 4, TK = 64;
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(const PrefillParams p,
+                                                                                const uint8_t *__restrict__ ws,
+                                                                                int32_t MC, int32_t units) {
+  constexpr int TK = 64, NT = NW * 64;
   constexpr int KRB = 2 * D, KC = KRB / 16, VRB = TK * 2;
   constexpr int KBUF = TK * KRB, VBUF = D * VRB;
   constexpr int NCH = D / 16, NDB = D / 32;
-  constexpr int NKL = KBUF / 4096, NVL = VBUF / 4096;
+  constexpr int NKL = KBUF / (NT * 16), NVL = VBUF / (NT * 16);  // 16-byte copies per thread per tile
   using L = StageLayout<D>;
   constexpr uint32_t CS = (uint32_t)L::kBlock;  // bytes per staged chunk
   // Three K buffers and two V buffers: 160 KiB for the two workgroups of a CU at D = 128.
@@ -868,15 +869,16 @@ __global__ __launch_bounds__(256, 2) void prefill_pipe_kernel(const PrefillParam
     const uint32_t cb = tile_slot(it) * CS;
 #pragma unroll
     for (int cl = c0; cl < c1; ++cl) {
-      const uint32_t k = (uint32_t)(cl * 256 + wave * 64) / (16 * KC);
-      buffer_load_lds16_m0(rs, (buf == 2 ? mk2 : buf ? mk1 : mk0) + cl * 4096, kvoff, cb + k * CS);
+      const uint32_t k = (uint32_t)(cl * NT + wave * 64) / (16 * KC);
+      buffer_load_lds16_m0(rs, (buf == 2 ? mk2 : buf ? mk1 : mk0) + cl * NT * 16, kvoff, cb + k * CS);
     }
   };
   auto load_v = [&](int32_t it, auto bufc, int c0, int c1) __attribute__((always_inline)) {
     constexpr int buf = decltype(bufc)::value;
     const uint32_t cb = tile_slot(it) * CS + (uint32_t)L::kVPart;
 #pragma unroll
-    for (int cl = c0; cl < c1; ++cl) buffer_load_lds16_m0(rs, (buf ? mv1 : mv0) + cl * 4096, vvoff, cb + cl * 1024);
+    for (int cl = c0; cl < c1; ++cl)
+      buffer_load_lds16_m0(rs, (buf ? mv1 : mv0) + cl * NT * 16, vvoff, cb + cl * NT * 4);
   };
   // End of a tile: wait for this thread's tile copies except the newest
   // `keep` (the K prefetch, which has another tile of time), and for its LDS
@@ -1175,7 +1177,8 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
     // staged path: chunks in LDS operand layout, then the direct-load kernel
     const int32_t mc = (int32_t)staged_chunks(d);
     const int32_t units = d.batch * mc * d.num_heads;
-    const int64_t n_wg = (int64_t)((d.q_len + 127) / 128) * d.num_heads * d.batch;
+    constexpr int NW = 4;  // waves (32 queries each) per workgroup
+    const int64_t n_wg = (int64_t)((d.q_len + 32 * NW - 1) / (32 * NW)) * d.num_heads * d.batch;
     MEMOPT_REQUIRE(n_wg < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "paged_attention: too many query tiles");
     uint8_t *ws = (uint8_t *)d.workspace;
     const dim3 sgrid((unsigned)((units + 3) / 4)), grid((unsigned)n_wg);
@@ -1183,11 +1186,11 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
     if (d.head_dim == 128) {
       if (int4) hipLaunchKernelGGL((prefill_stage_kernel<128, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
       else hipLaunchKernelGGL((prefill_stage_kernel<128, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      hipLaunchKernelGGL(prefill_pipe_kernel<128>, grid, dim3(256), 0, stream, p, ws, mc, units);
+      hipLaunchKernelGGL((prefill_pipe_kernel<128, NW>), grid, dim3(NW * 64), 0, stream, p, ws, mc, units);
     } else {
       if (int4) hipLaunchKernelGGL((prefill_stage_kernel<64, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
       else hipLaunchKernelGGL((prefill_stage_kernel<64, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      hipLaunchKernelGGL(prefill_pipe_kernel<64>, grid, dim3(256), 0, stream, p, ws, mc, units);
+      hipLaunchKernelGGL((prefill_pipe_kernel<64, NW>), grid, dim3(NW * 64), 0, stream, p, ws, mc, units);
     }
     return check_launch("paged_attention(prefill, staged)");
   }
