@@ -118,42 +118,76 @@ __device__ __forceinline__ float wave_max(float v) {
 // away from zero; NaN quotients give code 8, like the float->int conversion
 // of the reference (v_cvt_i32_f32(NaN) = 0).
 
-// Scale of a 64-element group whose absmax is spread over LANES consecutive
-// lanes (4 or 8, aligned): DPP max inside the lane group, then absmax / 7.
+// RN(a / 7) for a >= 0 without an IEEE division (Markstein with the
+// constant c7 = RN(1/7)): q0 = RN(a * c7) is within an ulp of a / 7,
+// r = a - 7 * q0 is exact in one fma, and RN(q0 + r * c7) = RN(a / 7).
+// Checked against the IEEE quotient for every finite fp16 absmax; a = inf
+// keeps the IEEE result inf (the fma would give inf - inf).
+__device__ __forceinline__ float div7(float a) {
+  constexpr float c7 = 0.142857149f;  // 0x3E124925
+  const float q0 = a * c7;
+  const float r = fmaf(-q0, 7.0f, a);
+  const float q = fmaf(r, c7, q0);
+  return a == __builtin_inff() ? a : q;
+}
+
+// Group scale from the group's absmax: absmax / 7, or 1 for an all-zero group.
+__device__ __forceinline__ float scale_of(float absmax) { return absmax > 0.0f ? div7(absmax) : 1.0f; }
+
+// Absmax of a 64-element group spread over LANES consecutive lanes (4 or 8,
+// aligned): DPP max inside the lane group.
 template <int LANES>
-__device__ __forceinline__ float group_scale(float a) {
+__device__ __forceinline__ float group_absmax(float a) {
   a = fmaxf(a, xor1(a));
   a = fmaxf(a, xor2(a));
   if (LANES == 8) a = fmaxf(a, half_mirror(a));
-  return (a > 0.0f) ? (a / 7.0f) : 1.0f;
+  return a;
 }
 
-// Codes of N elements with one scale, packed 8 per word (element i of word
-// k in bits 4i..4i+3, i.e. byte j = code[2j] | code[2j+1] << 4).
-// RN(v / scale) without a full IEEE division per element (Markstein): with
-// y = RN(1 / scale) from one IEEE division and q0 = RN(v * y) within an ulp
-// of v / scale, r = v - q0 * scale is exact in one fma and
-// RN(q0 + r * y) = RN(v / scale). No overflow or underflow is possible here
-// (|v| <= 65504, scale in [absmax / 7, 9358]); NaN/inf inputs still end in a
-// NaN quotient and code 8.
+template <int LANES>
+__device__ __forceinline__ float group_scale(float a) {
+  return scale_of(group_absmax<LANES>(a));
+}
+
+// Codes of N elements with one scale (y = RN(1 / scale)), packed 8 per word
+// (element i of word k in bits 4i..4i+3, i.e. byte j = code[2j] | code[2j+1] << 4).
+//  - Quotient: RN(v / scale) without a full IEEE division per element
+//    (Markstein): q0 = RN(v * y) is within an ulp of v / scale,
+//    r = v - q0 * scale is exact in one fma and RN(q0 + r * y) = RN(v / scale).
+//    No overflow or underflow is possible (|v| <= 65504, scale in
+//    [absmax / 7, 9358]); NaN/inf inputs end in a NaN quotient.
+//  - Rounding: roundf(q) (half away from zero) = trunc(q + copysign(h, q))
+//    with h = 0.5 - 2^-25, the float just below one half: the sum rounds up
+//    to the next integer exactly when |q| reaches a half (checked for every
+//    float with |q| < 16). The float->int conversion truncates and turns NaN
+//    into 0 (code 8).
+//  - Clamp: |q| <= 7 (1 + 2^-22) for every finite v in the group, since
+//    |v| <= absmax and scale = RN(absmax / 7); the rounded value lies in
+//    [-7, 7] and clamp(iq + 8, 0, 15) = iq + 8.
+//  - Packing: sum over i of (iq_i + 8) << 4i = 0x88888888 + sum of iq_i << 4i
+//    (mod 2^32), one shift-add per element.
 template <int N>
-__device__ __forceinline__ void int4_pack(const float *v, float scale, uint32_t *w) {
-  const float y = 1.0f / scale;
+__device__ __forceinline__ void int4_pack(const float *v, float scale, float y, uint32_t *w) {
+  constexpr float h = 0.49999997f;  // 0x3EFFFFFF
 #pragma unroll
   for (int k = 0; k < N / 8; ++k) {
-    uint32_t acc = 0;
+    uint32_t acc = 0x88888888u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float x = v[8 * k + i];
       const float q0 = __fmul_rn(x, y);
       const float r = fmaf(-q0, scale, x);
       const float q = fmaf(r, y, q0);
-      int iq = (int)roundf(q) + 8;
-      iq = iq < 0 ? 0 : (iq > 15 ? 15 : iq);
-      acc |= (uint32_t)iq << (4 * i);
+      const int iq = (int)(q + __builtin_copysignf(h, q));
+      acc += (uint32_t)iq << (4 * i);
     }
     w[k] = acc;
   }
+}
+
+template <int N>
+__device__ __forceinline__ void int4_pack(const float *v, float scale, uint32_t *w) {
+  int4_pack<N>(v, scale, 1.0f / scale, w);
 }
 
 // Quantizes 8 consecutive elements (one 16-byte lane chunk of a 64-element

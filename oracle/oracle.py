@@ -144,6 +144,10 @@ def _clib():
         lib.oracle_dequantize_int4.restype = None
         lib.oracle_markstein_mismatches.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64]
         lib.oracle_markstein_mismatches.restype = ctypes.c_int64
+        lib.oracle_div7_mismatches.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+        lib.oracle_div7_mismatches.restype = ctypes.c_int64
+        lib.oracle_round_shortcut_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]
+        lib.oracle_round_shortcut_mismatches.restype = ctypes.c_int64
         _CLIB = lib
     return _CLIB
 
@@ -175,6 +179,21 @@ def markstein_mismatches(values: np.ndarray, scales: np.ndarray) -> int:
     v = np.ascontiguousarray(values, dtype=np.float32)
     sc = np.ascontiguousarray(scales, dtype=np.float32)
     return int(_clib().oracle_markstein_mismatches(v.ctypes.data, v.size, sc.ctypes.data, sc.size))
+
+
+def div7_mismatches(absmax: np.ndarray) -> int:
+    """Checker of the device's group-scale shortcut (oracle/quant_ref.c):
+    number of positive a whose constant-reciprocal Markstein quotient differs
+    from the IEEE quotient a / 7."""
+    a = np.ascontiguousarray(absmax, dtype=np.float32)
+    return int(_clib().oracle_div7_mismatches(a.ctypes.data, a.size))
+
+
+def round_shortcut_mismatches(lo_bits: int, hi_bits: int, h: float = 0.49999997) -> int:
+    """Checker of the device's rounding shortcut (oracle/quant_ref.c): number
+    of floats +-q, bit patterns of |q| in [lo_bits, hi_bits), for which
+    (int)(q + copysign(h, q)) differs from roundf(q)."""
+    return int(_clib().oracle_round_shortcut_mismatches(lo_bits, hi_bits, h))
 
 
 # ---------------------------------------------------------------------------

@@ -12,6 +12,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <string.h>
 
 #define GROUP 64
 
@@ -68,6 +69,47 @@ int64_t oracle_markstein_mismatches(const float *v, int64_t nv, const float *s, 
       const float q = fmaf(r, y, q0);
       const float want = x / sc;
       if (q != want) ++bad;
+    }
+  }
+  return bad;
+}
+
+/*
+ * Checker for the device's group-scale shortcut (not part of the reference):
+ * for each a[i] (positive), compares the Markstein quotient with the
+ * constant c7 = RN(1/7)
+ *   q0 = RN(a*c7); r = fma(-q0, 7, a); q = fma(r, c7, q0)
+ * with the IEEE quotient RN(a/7). Returns the number of mismatches.
+ */
+int64_t oracle_div7_mismatches(const float *a, int64_t n) {
+  const float c7 = 1.0f / 7.0f;
+  int64_t bad = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const float x = a[i];
+    const float q0 = x * c7;
+    const float r = fmaf(-q0, 7.0f, x);
+    const float q = fmaf(r, c7, q0);
+    if (q != x / 7.0f) ++bad;
+  }
+  return bad;
+}
+
+/*
+ * Checker for the device's rounding shortcut (not part of the reference):
+ * for every float whose bit pattern lies in [lo, hi) and for its negation,
+ * compares (int)(q + copysign(h, q)) with (int)roundf(q) (round half away
+ * from zero); the device uses h = 0.5 - 2^-25. Patterns must encode finite
+ * |q| < 2^30. Returns the number of mismatches.
+ */
+int64_t oracle_round_shortcut_mismatches(uint32_t lo, uint32_t hi, float h) {
+  int64_t bad = 0;
+  for (uint32_t b = lo; b < hi; ++b) {
+    float q;
+    memcpy(&q, &b, 4);
+    for (int sgn = 0; sgn < 2; ++sgn, q = -q) {
+      const int fast = (int)(q + copysignf(h, q));
+      const int want = (int)roundf(q);
+      if (fast != want) ++bad;
     }
   }
   return bad;

@@ -423,3 +423,27 @@ def test_division_shortcut_matches_ieee_on_fp16_domain():
     a = v[v > 0][::8]
     s = (a / np.float32(7.0)).astype(np.float32)
     assert O.markstein_mismatches(v, s) == 0
+
+
+def test_group_scale_shortcut_matches_ieee_on_fp16_domain():
+    """The device computes scale = RN(absmax / 7) as q0 = RN(a * RN(1/7)),
+    r = fma(-q0, 7, a), q = fma(r, RN(1/7), q0). For every positive finite
+    fp16 absmax this equals the IEEE quotient; a perturbed constant does not."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    a = h[np.isfinite(h)].astype(np.float32)
+    a = a[a > 0]
+    assert a.size == 31743
+    assert O.div7_mismatches(a) == 0
+
+
+def test_rounding_shortcut_matches_roundf():
+    """The device rounds half away from zero as (int)(q + copysign(h, q)) with
+    h = 0.5 - 2^-25. Checked for every float with 2^-3 <= |q| < 16 (both
+    signs; the sweep over all |q| < 16 also gives 0, ~8 s) and a sparse sweep
+    below; h = 0.5 itself fails (0.49999997 + 0.5 rounds to 1)."""
+    lo, hi = int(np.float32(0.125).view(np.uint32)), int(np.float32(16.0).view(np.uint32))
+    assert O.round_shortcut_mismatches(lo, hi) == 0
+    for b in range(0, lo, 4099):  # sparse sweep of |q| < 1/8 (every code 8)
+        assert O.round_shortcut_mismatches(b, b + 1) == 0
+    assert O.round_shortcut_mismatches(lo, hi, h=0.5) > 0
+    assert O.round_shortcut_mismatches(lo, hi, h=0.4999999) > 0
