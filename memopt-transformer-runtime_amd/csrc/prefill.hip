@@ -1061,6 +1061,10 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
         PIPE_SGB(0x400, 16 / NCH, 0);
         PIPE_SGB(0x002, 16 / NCH, 0);
       }
+      // The probabilities must be complete here: without this use the
+      // compiler sinks their exp2s past the conditional copies below into
+      // segment 3, ahead of the PV MFMAs that need them.
+      asm volatile("" ::"v"(pa[0]), "v"(pa[1]));
       __builtin_amdgcn_sched_barrier(0);
       // K copies go last: the end-of-tile wait leaves the newest NKL in flight.
       if (k_ahead) load_k(it + 3, IntC<K3>{}, 0, NKL / 2);
@@ -1075,6 +1079,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
         PIPE_SGB(0x400, 16 / (2 * NDB), 0);
         PIPE_SGB(0x002, 16 / (2 * NDB), 0);
       }
+      asm volatile("" ::"v"(pb[0]), "v"(pb[1]));
       __builtin_amdgcn_sched_barrier(0);
       if (k_ahead) load_k(it + 3, IntC<K3>{}, NKL / 2, NKL);
       // Seg 4: PV(i) block 1
