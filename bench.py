@@ -276,7 +276,7 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
         calls.append(memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, window, num_sink_tokens=cfg["sinks"]))
         del scores
     nbytes //= copies  # bytes per step (copies are equal up to unlinked pages)
-    ms, _ = time_steps(torch, calls, steps, warmup)
+    ms, _ = time_steps(torch, calls, steps, warmup, pre_sleep_cycles=20_000_000)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"kernel": "decode_int4_pages_kernel<128, 4, 2>", "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
             "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
@@ -319,7 +319,7 @@ def main():
     for i in range(1000):
         calls[i % len(calls)]()
     torch.cuda.synchronize()
-    region_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup)
+    region_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup, pre_sleep_cycles=20_000_000)
     nbytes = effective_kv_bytes(cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"])
     value = nbytes / (region_ms * 1e-3) / 1e9
     achieved = value  # one decode launch per step
