@@ -21,7 +21,10 @@ def _pool_state(fmt):
 @pytest.mark.parametrize("fmt", ["fp16", "int4"])
 @pytest.mark.parametrize("N,H,L,bs,r,sinks", [
     (2, 4, 100, 16, 0.5, 4), (3, 2, 64, 16, 0.75, 0), (1, 8, 4096, 16, 0.75, 4),
-    (2, 2, 8192, 16, 0.3, 4), (2, 3, 50, 8, 0.1, 2), (1, 2, 40, 16, 1.0, 4)])
+    (2, 2, 8192, 16, 0.3, 4), (2, 3, 50, 8, 0.1, 2), (1, 2, 40, 16, 1.0, 4),
+    # 1024-thread kernels: keys in registers (L <= 32768), then streamed rows
+    # read as float4 (L % 4 == 0) and token by token (L % 4 != 0)
+    (1, 2, 20000, 16, 0.75, 4), (1, 2, 40000, 16, 0.6, 4), (1, 1, 40001, 16, 0.5, 3)])
 def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
     if fmt == "int4" and bs != 16:
         pytest.skip("the INT4 page pool uses 16-token pages")
