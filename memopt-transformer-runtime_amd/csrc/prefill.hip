@@ -710,10 +710,22 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams 
     *reinterpret_cast<u32x4 *>(krow0 + 2 * D + 16 * i) =
         u32x4{kw1[4 * i], kw1[4 * i + 1], kw1[4 * i + 2], kw1[4 * i + 3]};
   }
+  // V^T goes through LDS: the 4-byte pieces of a lane (two tokens of one
+  // dim) land in the block's layout there, and the wave then writes the
+  // block as contiguous 16-byte stores; written directly, the scattered
+  // 4-byte stores cost twice the K stores for the same bytes.
   const int vc = chunk_vcol(pp);
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[4][32 * D];
+  uint8_t *vl = vt_lds[threadIdx.x >> 6];
 #pragma unroll
-  for (int d = 0; d < DPL; ++d)
-    *reinterpret_cast<uint32_t *>(blk + L::kVPart + (c * DPL + d) * 32 + vc * 2) = vw[d];
+  for (int d = 0; d < DPL; ++d) *reinterpret_cast<uint32_t *>(vl + (c * DPL + d) * 32 + vc * 2) = vw[d];
+  // One wave's LDS accesses complete in order; the clobber keeps the compiler
+  // from moving the reads above the writes.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int k = 0; k < 32 * D / 1024; ++k)
+    *reinterpret_cast<u32x4 *>(blk + L::kVPart + k * 1024 + lane * 16) =
+        *reinterpret_cast<const u32x4 *>(vl + k * 1024 + lane * 16);
   if (h == 0 && lane == 0)
     reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + slot] = pg >= 0 ? 1 : 0;
 }
