@@ -296,8 +296,8 @@ def main():
                     help="only run 5 plain 512 MiB device-to-device copies (scales rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU only (the path is single-GPU; multi-GPU sharding is "
-              "design-only, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the kernels run on one GPU's share of the "
+              "work; sharding across GPUs is not built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
