@@ -25,8 +25,9 @@
 //    group in nibble-unpack order (0,4,1,5,2,6,3,7); Q is loaded once in the
 //    same dim order, so neither staging path repacks;
 //  * tiles wholly inside every query's visible range skip the mask; the
-//    running max is raised lazily (rescale only when exceeded by > 8 in log2
-//    units).
+//    running max is raised lazily (rescale only when a probability would
+//    exceed 2^8); scores stay unscaled fp32 q . k and exp2 takes
+//    log2(e) / sqrt(D) (score - m), so no scaled copy of Q is rounded.
 #include "attention.hpp"
 #include "page_format.hpp"
 
@@ -180,19 +181,17 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
         } else {
           v = n;
         }
-        // scores come out of the MFMA in log2 units: Q is pre-scaled by
-        // log2(e) / sqrt(D) (an extra fp16 rounding of q, ~2^-12 relative)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] * cs);
       }
       qf[qb][c] = v;
     }
   }
 
   float16_t o[QB][NDB];
-  // m: running max of the scores (log2 units), -inf until the first visible
+  // m: running max of the raw scores q . k, -inf until the first visible
   // key. The S accumulators start from `mtile` = -m (0 while m is -inf), so
-  // the MFMA returns score - m directly.
+  // the MFMA returns score - m directly; exp2 takes cs (score - m) with cs =
+  // log2(e) / sqrt(D) applied in fp32 (Q is not pre-scaled: a scaled fp16 Q
+  // would carry a 2^-11 relative rounding into every score).
   float m[QB], lsum[QB];
   float16_t mtile[QB];
 #pragma unroll
@@ -445,11 +444,11 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
         tmax = half_max(tmax);
         // lazy rescale: p stays <= 2^8 between raises; the first visible key
         // always raises
-        const bool raise = (m[qb] == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
+        const bool raise = (m[qb] == -INFINITY) ? (tmax != -INFINITY) : (tmax * cs > 8.0f);
         if (__any(raise)) {
           const float base = (m[qb] == -INFINITY) ? 0.0f : m[qb];
           const float mn = fmaxf(m[qb], base + tmax);
-          const float alpha = (mn == m[qb]) ? 1.0f : fast_exp2(m[qb] - mn);
+          const float alpha = (mn == m[qb]) ? 1.0f : fast_exp2((m[qb] - mn) * cs);
           const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
           lsum[qb] *= alpha;
 #pragma unroll
@@ -467,7 +466,7 @@ __global__ __launch_bounds__(NW * 64, (QB == 1 && NW == 4) ? (TK == 32 ? 3 : 2) 
         for (int g2 = 0; g2 < 2; ++g2) {
 #pragma unroll
           for (int e = 0; e < 8; e += 2) {
-            const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e]), (half_t)fast_exp2(s[8 * g2 + e + 1])};
+            const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e] * cs), (half_t)fast_exp2(s[8 * g2 + e + 1] * cs)};
             lsum[qb] = __builtin_amdgcn_fdot2(pp2, ones, lsum[qb], false);
             pb[qb][g2][e] = pp2.x;
             pb[qb][g2][e + 1] = pp2.y;
@@ -761,7 +760,7 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p) {
 // Attention over staged chunks, software-pipelined inside each wave.
 //  * A workgroup of 4 waves owns 128 queries of one (batch, head); wave w
 //    owns 32 of them, one query per lane column (lanes l and l+32 share
-//    query l % 32). Q is held in registers, pre-scaled by log2(e)/sqrt(D).
+//    query l % 32). Q is held in registers as given (unscaled fp16).
 //  * Keys advance in 64-key tiles (four staged 16-token chunks). Tiles are
 //    copied from the workspace into LDS with buffer-to-LDS DMA: unpadded
 //    rows whose 16-byte chunks are XOR-swizzled (K: chunk ^ (row & 15) for
@@ -827,8 +826,6 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
           half8_t, *reinterpret_cast<const uint4 *>(p.q + (((int64_t)b * p.Lq + qi) * p.H + h) * D + 16 * c + 8 * hl));
       v[0] = n[0]; v[1] = n[4]; v[2] = n[1]; v[3] = n[5];
       v[4] = n[2]; v[5] = n[6]; v[6] = n[3]; v[7] = n[7];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] * cs);
     }
     qf[c] = v;
   }
@@ -946,16 +943,17 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     for (int r = 0; r < 16; ++r) t = fmaxf(t, s[1][r]);
     return half_max(t);
   };
-  // Lazy running max: rescale only when a score exceeds m by more than 2^8
-  // (log2 units); the first visible key always raises. S values held in
+  // Lazy running max (raw score units): rescale only when cs (score - m)
+  // exceeds 8, i.e. a probability would exceed 2^8; the first visible key
+  // always raises. S values held in
   // `s` and in the nblk_next blocks of `nx` (scores of the next tile already
   // computed against the old m) are moved to the new m.
   auto raise_max = [&](float tmax, float16_t (&s)[2], float16_t (&nx)[2], int nblk_next) __attribute__((always_inline)) {
-    const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax > 8.0f);
+    const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax * cs > 8.0f);
     if (__any(raise)) {
       const float base = (m == -INFINITY) ? 0.0f : m;
       const float mn = fmaxf(m, base + tmax);
-      const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
+      const float alpha = (mn == m) ? 1.0f : fast_exp2((m - mn) * cs);
       const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
       lsum *= alpha;
 #pragma unroll
@@ -987,7 +985,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     for (int g2 = 0; g2 < 2; ++g2) {
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e]), (half_t)fast_exp2(s[8 * g2 + e + 1])};
+        const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e] * cs), (half_t)fast_exp2(s[8 * g2 + e + 1] * cs)};
         ls = __builtin_amdgcn_fdot2(pp2, ones, ls, false);
         pb[g2][e] = pp2.x;
         pb[g2][e + 1] = pp2.y;
@@ -1070,8 +1068,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       for (int c = 0; c < NCH; ++c) {
         PIPE_SGB(0x008, 1, 0);
         if (c + 4 < NCH) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x002, 32 / NCH, 0);  // per exp2: a scale multiply, half a pack, half a row-sum dot
         PIPE_SGB(0x400, 16 / NCH, 0);
-        PIPE_SGB(0x002, 16 / NCH, 0);
       }
       // The probabilities must be complete here: without this use the
       // compiler sinks their exp2s past the conditional copies below into
@@ -1088,8 +1086,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       for (int c = 0; c < 2 * NDB; ++c) {
         PIPE_SGB(0x008, 1, 0);
         if (c + 4 < 2 * NDB) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x002, 32 / (2 * NDB), 0);
         PIPE_SGB(0x400, 16 / (2 * NDB), 0);
-        PIPE_SGB(0x002, 16 / (2 * NDB), 0);
       }
       asm volatile("" ::"v"(pb[0]), "v"(pb[1]));
       __builtin_amdgcn_sched_barrier(0);

@@ -1,0 +1,114 @@
+"""Seeded sweeps of random shapes through the fused INT4 write, decode and
+prefill paths against the CPU oracle. Each case draws its sizes from a fixed
+seed (batch, heads, head_dim, ragged contexts, window, sinks, unlinked pages,
+slot patterns), so the sweep is deterministic and covers combinations the
+hand-written cases do not."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import assert_close, memopt_C, same_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _kv(rng, shape):
+    k = (rng.standard_normal(shape) * np.where(rng.random(shape) < 0.01, 8, 1)).astype(np.float16)
+    v = rng.standard_normal(shape).astype(np.float16)
+    return k, v
+
+
+def _decode_case(seed):
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 5))
+    H = int(rng.integers(1, 5))
+    D = int(rng.choice([64, 128]))
+    ctx = rng.integers(1, 3000, size=B)
+    W = int(rng.choice([int(rng.integers(1, 3000)), 1 << 20]))
+    sinks = int(rng.integers(0, 24))
+    return B, H, D, [int(c) for c in ctx], W, sinks, int(rng.integers(0, 4))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_decode_sweep(seed):
+    B, H, D, ctx, W, sinks, unlink = _decode_case(seed)
+    rng = np.random.default_rng(seed)
+    bs = 16
+    M = (max(ctx) + bs - 1) // bs
+    nb = B * M + 3
+    kp, vp = _kv(rng, (nb, bs, H, D))
+    q = rng.standard_normal((B, 1, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    for _ in range(unlink):
+        bt[int(rng.integers(0, B)), int(rng.integers(0, M))] = -1
+    cl = np.array(ctx, np.int32)
+    pages = O.to_int4_pages(kp, vp)
+    want = O.paged_attention_int4(q, pages, bt, cl, 1 << 20, W, num_sink_tokens=sinks)
+    pg = to_dev(pages)
+    got = memopt_C.dynamic_sparse_attention(to_dev(q), pg, pg, to_dev(bt), to_dev(cl), 1 << 20, W,
+                                            num_sink_tokens=sinks)
+    assert_close(got, want, what=f"decode seed {seed}: B{B} H{H} D{D} ctx{ctx} W{W} sinks{sinks}")
+
+
+def _prefill_case(seed):
+    rng = np.random.default_rng(2000 + seed)
+    B = int(rng.integers(1, 3))
+    H = int(rng.integers(1, 4))
+    D = int(rng.choice([64, 128]))
+    ctx = [int(c) for c in rng.integers(16, 1200, size=B)]
+    Lq = int(rng.integers(16, min(ctx) + 1))
+    causal = bool(rng.integers(0, 2))
+    W = int(rng.choice([int(rng.integers(1, 1200)), 1 << 20]))
+    sinks = int(rng.integers(0, 20))
+    return B, H, D, ctx, Lq, causal, W, sinks, bool(rng.integers(0, 2))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_prefill_sweep(seed):
+    B, H, D, ctx, Lq, causal, W, sinks, unlink = _prefill_case(seed)
+    rng = np.random.default_rng(seed + 50)
+    bs = 16
+    M = (max(ctx) + bs - 1) // bs
+    nb = B * M + 3
+    kp, vp = _kv(rng, (nb, bs, H, D))
+    q = rng.standard_normal((B, Lq, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    if unlink:
+        bt[0, int(rng.integers(0, M))] = -1
+    cl = np.array(ctx, np.int32)
+    pages = O.to_int4_pages(kp, vp)
+    want = O.paged_attention_int4(q, pages, bt, cl, 1 << 20, W, num_sink_tokens=sinks, causal=causal)
+    pg = to_dev(pages)
+    got = memopt_C.dynamic_sparse_attention(to_dev(q), pg, pg, to_dev(bt), to_dev(cl), 1 << 20, W,
+                                            num_sink_tokens=sinks, causal=causal)
+    assert_close(got, want, what=f"prefill seed {seed}: B{B} H{H} D{D} ctx{ctx} Lq{Lq} causal{causal} W{W} "
+                                 f"sinks{sinks}")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_write_int4_sweep(seed):
+    """Random token counts and slot patterns: whole aligned pages (the page
+    path), shifted runs and scattered slots (the chunk path), mixed in one call."""
+    rng = np.random.default_rng(3000 + seed)
+    D = int(rng.choice([64, 128]))
+    H = int(rng.integers(1, 5))
+    nb, bs = int(rng.integers(4, 20)), 16
+    T = int(rng.integers(1, nb * bs + 1))
+    pattern = seed % 3
+    if pattern == 0:  # contiguous from an aligned page
+        start = 16 * int(rng.integers(0, max(1, nb - (T + 15) // 16 + 1)))
+        slots = (start + np.arange(T)) % (nb * bs)
+    elif pattern == 1:  # contiguous from an unaligned slot
+        start = int(rng.integers(0, nb * bs))
+        slots = (start + np.arange(T)) % (nb * bs)
+    else:
+        slots = rng.permutation(nb * bs)[:T]
+    slots = slots.astype(np.int32)
+    memopt_C.reset_pool()  # identical parameters would otherwise keep an earlier test's pages
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    k, v = _kv(rng, (T, H, D))
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)), to_dev(slots))
+    wk, wv = np.zeros((nb, bs, H, D), np.float16), np.zeros((nb, bs, H, D), np.float16)
+    O.write_cache(wk, k, slots)
+    O.write_cache(wv, v, slots)
+    same_bits(memopt_C.get_int4_pages(), O.to_int4_pages(wk, wv))
