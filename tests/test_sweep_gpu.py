@@ -29,7 +29,7 @@ def _decode_case(seed):
     return B, H, D, [int(c) for c in ctx], W, sinks, int(rng.integers(0, 4))
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(40))
 def test_decode_sweep(seed):
     B, H, D, ctx, W, sinks, unlink = _decode_case(seed)
     rng = np.random.default_rng(seed)
@@ -63,7 +63,7 @@ def _prefill_case(seed):
     return B, H, D, ctx, Lq, causal, W, sinks, bool(rng.integers(0, 2))
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(32))
 def test_prefill_sweep(seed):
     B, H, D, ctx, Lq, causal, W, sinks, unlink = _prefill_case(seed)
     rng = np.random.default_rng(seed + 50)
@@ -85,7 +85,7 @@ def test_prefill_sweep(seed):
                                  f"sinks{sinks}")
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(18))
 def test_write_int4_sweep(seed):
     """Random token counts and slot patterns: whole aligned pages (the page
     path), shifted runs and scattered slots (the chunk path), mixed in one call."""
@@ -112,3 +112,91 @@ def test_write_int4_sweep(seed):
     O.write_cache(wk, k, slots)
     O.write_cache(wv, v, slots)
     same_bits(memopt_C.get_int4_pages(), O.to_int4_pages(wk, wv))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_decode_token_major_sweep(seed):
+    """The same random decode shapes through the token-major INT4 layout (the
+    reference's byte order and fp32 surface scales)."""
+    B, H, D, ctx, W, sinks, unlink = _decode_case(100 + seed)
+    rng = np.random.default_rng(seed + 7)
+    bs = 16
+    M = (max(ctx) + bs - 1) // bs
+    nb = B * M + 3
+    kp, vp = _kv(rng, (nb, bs, H, D))
+    q = rng.standard_normal((B, 1, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    for _ in range(unlink):
+        bt[int(rng.integers(0, B)), int(rng.integers(0, M))] = -1
+    cl = np.array(ctx, np.int32)
+    kc, ks = O.quantize_int4(kp)
+    vc, vs = O.quantize_int4(vp)
+    want = O.paged_attention(q, O.dequantize_int4(kc, ks), O.dequantize_int4(vc, vs), bt, cl, 1 << 20, W,
+                             num_sink_tokens=sinks)
+    got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kc), to_dev(vc), to_dev(bt), to_dev(cl), 1 << 20, W,
+                                            num_sink_tokens=sinks, key_scales=to_dev(ks), value_scales=to_dev(vs),
+                                            kv_layout="token_major")
+    assert_close(got, want, what=f"token-major decode seed {seed}: B{B} H{H} D{D} ctx{ctx} W{W} sinks{sinks}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_prefill_fp16_pool_sweep(seed):
+    """Random prefill shapes over fp16 pools (16- and 32-token pages)."""
+    B, H, D, ctx, Lq, causal, W, sinks, unlink = _prefill_case(100 + seed)
+    rng = np.random.default_rng(seed + 90)
+    bs = 16 if seed % 2 == 0 else 32
+    M = (max(ctx) + bs - 1) // bs
+    nb = B * M + 3
+    kp, vp = _kv(rng, (nb, bs, H, D))
+    q = rng.standard_normal((B, Lq, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    if unlink:
+        bt[0, int(rng.integers(0, M))] = -1
+    cl = np.array(ctx, np.int32)
+    want = O.paged_attention(q, kp, vp, bt, cl, 1 << 20, W, num_sink_tokens=sinks, causal=causal)
+    got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt), to_dev(cl), 1 << 20, W,
+                                            num_sink_tokens=sinks, causal=causal)
+    assert_close(got, want, what=f"fp16 prefill seed {seed}: B{B} H{H} D{D} bs{bs} ctx{ctx} Lq{Lq} causal{causal} "
+                                 f"W{W} sinks{sinks}")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_evict_tokens_sweep(seed):
+    """Random (seq, head, length, retain ratio, sinks) through evict_tokens on
+    both pool formats against the oracle's exact top-k eviction."""
+    rng = np.random.default_rng(4000 + seed)
+    fmt = "int4" if seed % 2 else "fp16"
+    N, H = int(rng.integers(1, 4)), int(rng.integers(1, 5))
+    L = int(rng.integers(1, 6000))
+    r = float(rng.choice([0.1, 0.3, 0.5, 0.75, 0.9, 1.0]))
+    sinks = int(rng.integers(0, 40))
+    bs, D = 16, 64
+    M = (L + bs - 1) // bs
+    nb = N * M + 2
+    memopt_C.reset_pool()
+    memopt_C.init_pool(nb, bs, H, D, kv_format=fmt)
+    k, v = _kv(rng, (nb * bs, H, D))
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)),
+                         to_dev(np.arange(nb * bs, dtype=np.int32)))
+    scores = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    if L > 32:
+        scores[0, :, 16:32] = 1e-6  # a logical block evicted in every head
+    bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
+    ibf = np.zeros(nb, np.int32)
+    if fmt == "fp16":
+        kk, vv = memopt_C.get_pool_tensors()
+        before = {"format": fmt, "k": kk.cpu().numpy(), "v": vv.cpu().numpy()}
+    else:
+        pages = memopt_C.get_int4_pages()
+        before = {"format": fmt, "pages": pages.cpu().numpy(), "D": D}
+    bt_d, ibf_d = to_dev(bt), to_dev(ibf)
+    memopt_C.evict_tokens(to_dev(scores), bt_d, ibf_d, r, sinks)
+    O.evict_tokens_intended(scores, bt, ibf, r, sinks, before, bs)
+    if fmt == "fp16":
+        kk, vv = memopt_C.get_pool_tensors()
+        same_bits(kk, before["k"])
+        same_bits(vv, before["v"])
+    else:
+        same_bits(memopt_C.get_int4_pages(), before["pages"])
+    same_bits(bt_d, bt)
+    same_bits(ibf_d, ibf)
