@@ -1047,6 +1047,10 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       // Operand fragments stream 4 ahead of the MFMA that uses them (the
       // scheduling groups below keep at most 4 in flight).
       // Seg 1: QK(i+1) block 0 | running max of S(i)
+      // The four segments run at raised wave priority and the end-of-tile
+      // wait at the normal one, so of the two waves sharing a SIMD the one
+      // with MFMAs to issue wins the arbitration (measured ~0.7 % faster).
+      __builtin_amdgcn_s_setprio(1);
       qk_block(kt, 0, sn[0]);
       const float tmax = row_max(sc);
       PIPE_SGB(0x100, 4, 0);
@@ -1100,6 +1104,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
         PIPE_SGB(0x008, 1, 0);
         if (c + 4 < 2 * NDB) PIPE_SGB(0x100, 1, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
     }
     if (k_ahead) fl_cur = publish(it + 1, IntC<NKL>{});
     else fl_cur = publish(it + 1, IntC<0>{});
