@@ -14,7 +14,8 @@ step never re-reads what the previous step left in the 256 MB last-level
 cache. The JSON line also carries the roofline of the decode kernel (timed
 with HIP events on the stream it runs on), a CPU baseline (the reference's
 torch CPU path, restated in oracle/, on a bounded sample), and secondary
-figures (KV-quant write path GB/s).
+figures (prefill MFMA use, sparse and long-context decode with evict_tokens,
+the KV-quant write path, and config 2's decode shape over an fp16 page pool).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 200] [--no-cpu]
 """
@@ -134,6 +135,34 @@ def cpu_baseline_decode(torch, O, memopt_C, tables, q, cl, cfg, budget_s=15.0):
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{nseq} of {cfg['batch']} sequences of config 2 (dequantize + gather + fp32 SDPA, torch CPU), "
                       f"median of {len(times)} after 1 warm-up"}
+
+
+def bench_fp16_decode(torch, memopt_C, cfg, steps=20):
+    """Config 2's decode shape over an fp16 page pool (the reference's default
+    cache format, 16-token pages), HBM GB/s on the K/V bytes streamed."""
+    B, H, D, ctx, bs = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
+    nbps = ctx // bs
+    nb = 2 * B * nbps  # two page sets, alternated, so repeats are not served by the last-level cache
+    memopt_C.reset_pool()
+    memopt_C.init_pool(nb, bs, H, D)
+    dev = torch.device("cuda", 0)
+    kc, vc = memopt_C.get_pool_tensors()
+    g = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    for t in (kc, vc):
+        for i in range(0, nb, 1024):
+            t[i:i + 1024].copy_(torch.randn(t[i:i + 1024].shape, device=dev, generator=g))
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(cfg["seed"])).to(torch.int32)
+    tables = [perm[c * B * nbps:(c + 1) * B * nbps].reshape(B, nbps).to(dev) for c in range(2)]
+    q = torch.randn(B, 1, H, D, device=dev, generator=g).half()
+    cl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    calls = [memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, ctx) for bt in tables]
+    ms, _ = time_steps(torch, calls, steps, 5, pre_sleep_cycles=20_000_000)
+    nbytes = 2 * B * ctx * H * D * 2
+    return {"workload": "config 2 decode shape over an fp16 page pool: batch 16, 32 heads, head_dim 128, "
+                        "context 4096, 16-token pages, random-permutation block tables",
+            "kernel": "decode_fp16_kernel<128, 4, 2>", "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def bench_kv_quant(torch, memopt_C, cfg, steps=20):
@@ -358,6 +387,7 @@ def main():
             workload="BASELINE configs[4]: B 4, ctx 131072, 32768 pages, evict_tokens r 0.75 + 4 sinks, full window",
             **bench_sparse_decode(torch, memopt_C, CFG5, CFG5["ctx"], fifo_trace=True))
         sec["kv_quant"] = bench_kv_quant(torch, memopt_C, cfg)
+        sec["fp16_pool_decode"] = bench_fp16_decode(torch, memopt_C, cfg)
         line["secondary"] = sec
     print(json.dumps(line), flush=True)
 

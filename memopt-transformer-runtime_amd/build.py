@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "memopt_C", "libmemopt_hip.so")
-SOURCES = ["pool.cpp", "quant.hip", "evict.hip", "attention.hip", "decode_int4.hip", "prefill.hip"]
+SOURCES = ["pool.cpp", "quant.hip", "evict.hip", "attention.hip", "decode_int4.hip", "decode_fp16.hip", "prefill.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("MEMOPT_ARCH", "gfx950")

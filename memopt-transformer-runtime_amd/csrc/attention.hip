@@ -7,6 +7,9 @@
 // Dispatch:
 //   * INT4 cache, q_len == 1, 16-token pages, D in {64, 128}, aligned
 //     strides -> decode_int4 (split-K, HBM-streaming; decode_int4.hip);
+//   * fp16 cache, q_len == 1, pages of 16 * 2^k tokens, D in {64, 128},
+//     16-byte aligned rows -> decode_fp16 (split-K, HBM-streaming;
+//     decode_fp16.hip);
 //   * fp16 or INT4 cache, q_len >= 16, D in {64, 128}, 16-token pages ->
 //     prefill (fp16 MFMA; prefill.hip);
 //   * anything else -> generic_attention_kernel below: one wave per
@@ -146,6 +149,20 @@ static bool use_decode_int4(const memopt_attn_desc &d) {
   return true;
 }
 
+// fp16 pools: 16-token chunks of pages whose token count is 16 times a power
+// of two, 16-byte aligned rows, 32-bit per-lane offsets inside a chunk.
+static bool use_decode_fp16(const memopt_attn_desc &d) {
+  if (d.kv_format != MEMOPT_KV_FP16 || d.q_len != 1 || d.num_kv_blocks <= 0) return false;
+  if (d.head_dim != 64 && d.head_dim != 128) return false;
+  if (d.block_size % 16 != 0) return false;
+  const int32_t cpp = d.block_size / 16;
+  if ((cpp & (cpp - 1)) != 0) return false;
+  if (!aligned_to(d.query, 16) || !aligned_to(d.key_cache, 16) || !aligned_to(d.value_cache, 16)) return false;
+  if ((d.kv_page_stride * 2) % 16 || (d.kv_head_stride * 2) % 16 || (d.kv_token_stride * 2) % 16) return false;
+  if (15 * d.kv_token_stride * 2 + d.head_dim * 2 >= (1LL << 31)) return false;
+  return true;
+}
+
 static int validate(const memopt_attn_desc &d) {
   MEMOPT_REQUIRE(d.batch >= 0 && d.q_len >= 0 && d.num_heads >= 0 && d.head_dim >= 0, MEMOPT_ERR_INVALID,
                  "paged_attention: negative dimension");
@@ -172,7 +189,8 @@ static int validate(const memopt_attn_desc &d) {
 }
 
 static int decode_workspace(const memopt_attn_desc &d, int32_t *splits, int64_t *bytes) {
-  *splits = decode_splits(d.batch, d.num_heads, max_pages_visited(d));
+  // Splits are sized in the kernels' 16-token units.
+  *splits = decode_splits(d.batch, d.num_heads, max_pages_visited(d) * (d.block_size / 16));
   *bytes = (*splits > 1) ? (int64_t)d.batch * d.num_heads * (*splits) * (d.head_dim + 2) * 4 : 0;
   return MEMOPT_OK;
 }
@@ -188,7 +206,7 @@ int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes
   int rc = validate(*desc);
   if (rc != MEMOPT_OK) return rc;
   *bytes = 0;
-  if (use_decode_int4(*desc)) {
+  if (use_decode_int4(*desc) || use_decode_fp16(*desc)) {
     int32_t splits;
     return decode_workspace(*desc, &splits, bytes);
   }
@@ -253,10 +271,43 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
     p.W = W;
     p.sinks = d.num_sink_tokens < 0 ? 0 : d.num_sink_tokens;
     p.splits = splits;
+    p.bs = d.block_size;
     p.qk_scale_log2 = scale * 1.4426950408889634f;
     p.ws_o = (float *)d.workspace;
     p.ws_ml = splits > 1 ? (float *)d.workspace + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
     return launch_decode_int4(p, d.batch, d.head_dim, d.kv_format == MEMOPT_KV_INT4 ? MEMOPT_SCALE_F16 : d.scale_dtype, s);
+  }
+
+  if (use_decode_fp16(d)) {
+    int32_t splits;
+    int64_t need;
+    decode_workspace(d, &splits, &need);
+    MEMOPT_REQUIRE(need == 0 || (d.workspace && d.workspace_bytes >= need), MEMOPT_ERR_INVALID,
+                   "paged_attention: workspace too small (need " + std::to_string(need) + " bytes)");
+    DecodeParams p;
+    p.q = (const half_t *)d.query;
+    p.out = (half_t *)d.out;
+    p.pages = 0;
+    p.kc = (const uint8_t *)d.key_cache;
+    p.vc = (const uint8_t *)d.value_cache;
+    p.ks = p.vs = nullptr;
+    p.kv_ps = d.kv_page_stride * 2;  // bytes
+    p.kv_hs = d.kv_head_stride * 2;
+    p.kv_ts = d.kv_token_stride * 2;
+    p.sc_ps = p.sc_hs = p.sc_ts = 0;
+    p.bt = d.block_tables;
+    p.ctx = d.context_lens;
+    p.nb = d.num_kv_blocks;
+    p.M = d.max_blocks_per_seq;
+    p.H = d.num_heads;
+    p.W = W;
+    p.sinks = d.num_sink_tokens < 0 ? 0 : d.num_sink_tokens;
+    p.splits = splits;
+    p.bs = d.block_size;
+    p.qk_scale_log2 = scale * 1.4426950408889634f;
+    p.ws_o = (float *)d.workspace;
+    p.ws_ml = splits > 1 ? (float *)d.workspace + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
+    return launch_decode_fp16(p, d.batch, d.head_dim, s);
   }
 
   if (prefill_supported(d)) return launch_prefill(d, W, scale * 1.4426950408889634f, s);

@@ -46,6 +46,7 @@ struct DecodeParams {
   int64_t nb;                   // pages in the pool (entries >= nb are skipped)
   int32_t pages;                // 1: this build's INT4 page format (page_format.hpp)
   int32_t M, H, W, sinks, splits;
+  int32_t bs;           // tokens per page (fp16 pools; a multiple of 16)
   float qk_scale_log2;  // (1/sqrt(D)) * log2(e)
   float *ws_o;          // [B, H, splits, D] (splits > 1)
   float *ws_ml;         // [B, H, splits, 2]
@@ -56,6 +57,11 @@ int decode_splits(int32_t batch, int32_t heads, int32_t max_pages_visited);
 // Launches the split-K INT4 decode kernel (+ combine when splits > 1).
 int launch_decode_int4(const DecodeParams &p, int32_t batch, int32_t D, int32_t scale_dtype,
                        hipStream_t stream);
+
+// Launches the split-K fp16-pool decode kernel (+ combine when splits > 1).
+int launch_decode_fp16(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream);
+// Log-sum-exp merge of the split partials in p.ws_o / p.ws_ml into p.out.
+int launch_decode_combine(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream);
 
 // Multi-query (q_len >= 16) MFMA kernel over INT4 page pools or contiguous
 // fp16 pools with 16-multiple pages and D in {64, 128}.

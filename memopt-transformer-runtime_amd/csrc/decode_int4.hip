@@ -591,6 +591,10 @@ int launch_decode_int4(const DecodeParams &p, int32_t batch, int32_t D, int32_t 
     launch_shape<64, float>(p, grid, sh, stream);
   int rc = check_launch("paged_attention(decode_int4)");
   if (rc != MEMOPT_OK || p.splits == 1) return rc;
+  return launch_decode_combine(p, batch, D, stream);
+}
+
+int launch_decode_combine(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream) {
   hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((int64_t)batch * p.H)), dim3(128), 0, stream,
                      p.ws_o, p.ws_ml, p.out, D, p.splits);
   return check_launch("paged_attention(decode_combine)");

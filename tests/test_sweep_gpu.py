@@ -200,3 +200,24 @@ def test_evict_tokens_sweep(seed):
         same_bits(memopt_C.get_int4_pages(), before["pages"])
     same_bits(bt_d, bt)
     same_bits(ibf_d, ibf)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_decode_fp16_pool_sweep(seed):
+    """Random decode shapes over fp16 page pools (16-, 32- and 64-token
+    pages; the reference's default cache format)."""
+    B, H, D, ctx, W, sinks, unlink = _decode_case(200 + seed)
+    rng = np.random.default_rng(seed + 11)
+    bs = (16, 32, 64)[seed % 3]
+    M = (max(ctx) + bs - 1) // bs
+    nb = B * M + 3
+    kp, vp = _kv(rng, (nb, bs, H, D))
+    q = rng.standard_normal((B, 1, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    for _ in range(unlink):
+        bt[int(rng.integers(0, B)), int(rng.integers(0, M))] = -1
+    cl = np.array(ctx, np.int32)
+    want = O.paged_attention(q, kp, vp, bt, cl, 1 << 20, W, num_sink_tokens=sinks)
+    got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt), to_dev(cl), 1 << 20, W,
+                                            num_sink_tokens=sinks)
+    assert_close(got, want, what=f"fp16 decode seed {seed}: B{B} H{H} D{D} bs{bs} ctx{ctx} W{W} sinks{sinks}")
