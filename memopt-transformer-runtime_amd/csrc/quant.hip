@@ -64,29 +64,45 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t *__r
                                                               half_t *__restrict__ out,
                                                               int64_t n_chunks) {
   const int64_t stride = (int64_t)gridDim.x * kThreads;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
-    uint32_t w;
-    if (VEC) {
-      w = reinterpret_cast<const uint32_t *>(packed)[i];
-    } else {
-      w = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) w |= (uint32_t)packed[i * 4 + b] << (8 * b);
-    }
-    const float s = scales[i >> 3];
+  auto expand = [](uint32_t w, float s) {
     half_t h[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) h[e] = (half_t)((float)((int)((w >> (4 * e)) & 0xF) - 8) * s);
-    if (VEC) {
-      uint4 o;
-      o.x = as_u32(half2_t{h[0], h[1]});
-      o.y = as_u32(half2_t{h[2], h[3]});
-      o.z = as_u32(half2_t{h[4], h[5]});
-      o.w = as_u32(half2_t{h[6], h[7]});
-      *reinterpret_cast<uint4 *>(out + i * 8) = o;
-    } else {
+    return make_uint4(as_u32(half2_t{h[0], h[1]}), as_u32(half2_t{h[2], h[3]}), as_u32(half2_t{h[4], h[5]}),
+                      as_u32(half2_t{h[6], h[7]}));
+  };
+  if constexpr (VEC) {
+    // Four chunks per trip, all loads issued before any is used: one 4-byte
+    // load per trip left too few bytes in flight to cover HBM latency.
+    constexpr int R = 4;
+    for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 < n_chunks; i0 += R * stride) {
+      uint32_t w[R];
+      float sc[R];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) out[i * 8 + e] = h[e];
+      for (int r = 0; r < R; ++r) {
+        const int64_t i = min(i0 + r * stride, n_chunks - 1);
+        w[r] = reinterpret_cast<const uint32_t *>(packed)[i];
+        sc[r] = scales[i >> 3];
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t i = i0 + r * stride;
+        if (i < n_chunks) {
+          const uint4 o = expand(w[r], sc[r]);
+          typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+          __builtin_nontemporal_store((u4v){o.x, o.y, o.z, o.w}, reinterpret_cast<u4v *>(out + i * 8));
+        }
+      }
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w |= (uint32_t)packed[i * 4 + b] << (8 * b);
+      const uint4 o = expand(w, scales[i >> 3]);
+      const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[i * 8 + e] = as_half2(ow[e >> 1])[e & 1];
     }
   }
 }
