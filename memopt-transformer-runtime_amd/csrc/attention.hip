@@ -10,7 +10,7 @@
 //   * fp16 cache, q_len == 1, pages of 16 * 2^k tokens, D in {64, 128},
 //     16-byte aligned rows -> decode_fp16 (split-K, HBM-streaming;
 //     decode_fp16.hip);
-//   * fp16 or INT4 cache, q_len >= 16, D in {64, 128}, 16-token pages ->
+//   * fp16 or INT4 cache, q_len >= 2, D in {64, 128}, 16-token pages ->
 //     prefill (fp16 MFMA; prefill.hip);
 //   * anything else -> generic_attention_kernel below: one wave per
 //     (b, query, head), lanes over head dims, keys visited in order with an

@@ -63,7 +63,7 @@ int launch_decode_fp16(const DecodeParams &p, int32_t batch, int32_t D, hipStrea
 // Log-sum-exp merge of the split partials in p.ws_o / p.ws_ml into p.out.
 int launch_decode_combine(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream);
 
-// Multi-query (q_len >= 16) MFMA kernel over INT4 page pools or contiguous
+// Multi-query (q_len >= 2) MFMA kernel over INT4 page pools or contiguous
 // fp16 pools with 16-multiple pages and D in {64, 128}.
 bool prefill_supported(const memopt_attn_desc &d);
 // Workspace of the staged prefill path (0: the path stages in-kernel).

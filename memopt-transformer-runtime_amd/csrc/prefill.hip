@@ -1145,7 +1145,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
 
 bool prefill_supported(const memopt_attn_desc &d) {
   auto al16 = [](const void *x) { return ((uintptr_t)x & 15) == 0; };
-  if (d.q_len < 16 || (d.head_dim != 64 && d.head_dim != 128)) return false;
+  if (d.q_len < 2 || (d.head_dim != 64 && d.head_dim != 128)) return false;
   if (d.num_kv_blocks <= 0) return false;
   if (!al16(d.query) || !al16(d.out) || !al16(d.key_cache)) return false;
   if (d.kv_format == MEMOPT_KV_INT4) return d.block_size == 16;

@@ -1,5 +1,5 @@
 """GPU parity of the multi-query (prefill / chunked-prefill) MFMA attention
-path: q_len >= 16 over fp16 pools and INT4 page pools, causal StreamingLLM
+path: q_len >= 2 over fp16 pools and INT4 page pools, causal StreamingLLM
 masks (window + sinks), non-causal multi-query windows, unlinked pages,
 contexts shorter than the query block, against the CPU oracle; and the
 BASELINE config-4 shape at full size against an fp32 reference on sampled

@@ -221,3 +221,37 @@ def test_decode_fp16_pool_sweep(seed):
     got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt), to_dev(cl), 1 << 20, W,
                                             num_sink_tokens=sinks)
     assert_close(got, want, what=f"fp16 decode seed {seed}: B{B} H{H} D{D} bs{bs} ctx{ctx} W{W} sinks{sinks}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_small_q_len_sweep(seed):
+    """2..15 queries per sequence (speculative or short-chunk steps) on INT4
+    pages and fp16 pools, causal and not."""
+    rng = np.random.default_rng(5000 + seed)
+    B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+    D = int(rng.choice([64, 128]))
+    ctx = [int(c) for c in rng.integers(16, 1500, size=B)]
+    Lq = int(rng.integers(2, 16))
+    causal = bool(seed % 2)
+    W = int(rng.choice([int(rng.integers(1, 1500)), 1 << 20]))
+    sinks = int(rng.integers(0, 20))
+    int4 = seed % 4 >= 2
+    bs = 16
+    M = (max(ctx) + bs - 1) // bs
+    nb = B * M + 3
+    kp, vp = _kv(rng, (nb, bs, H, D))
+    q = rng.standard_normal((B, Lq, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    cl = np.array(ctx, np.int32)
+    if int4:
+        pages = O.to_int4_pages(kp, vp)
+        want = O.paged_attention_int4(q, pages, bt, cl, 1 << 20, W, num_sink_tokens=sinks, causal=causal)
+        pg = to_dev(pages)
+        got = memopt_C.dynamic_sparse_attention(to_dev(q), pg, pg, to_dev(bt), to_dev(cl), 1 << 20, W,
+                                                num_sink_tokens=sinks, causal=causal)
+    else:
+        want = O.paged_attention(q, kp, vp, bt, cl, 1 << 20, W, num_sink_tokens=sinks, causal=causal)
+        got = memopt_C.dynamic_sparse_attention(to_dev(q), to_dev(kp), to_dev(vp), to_dev(bt), to_dev(cl), 1 << 20,
+                                                W, num_sink_tokens=sinks, causal=causal)
+    assert_close(got, want, what=f"small q_len seed {seed}: B{B} H{H} D{D} ctx{ctx} Lq{Lq} causal{causal} W{W} "
+                                 f"sinks{sinks} int4{int4}")
