@@ -128,9 +128,12 @@ int memopt_evict_cache(const float *attention_scores, int64_t num_blocks,
  * Per (seq, head): sinks t < num_sink_tokens always kept; keep =
  * clamp(ceilf(r*L), 1, L); tokens scoring below the exact keep-th largest
  * (sink-boosted) score are evicted; their (token, head) rows are zeroed
- * (INT4: codes 0x88, scale 1.0). A logical block with all block_size
- * positions evicted votes is_block_free[phys] += 1; the vote reaching H
- * unlinks block_tables[seq, lb] = -1. No seq_len cap. */
+ * (INT4: every group scale of the row set to 0, codes kept, so the row
+ * dequantizes to zeros). A logical block with all block_size positions
+ * evicted votes is_block_free[phys] += 1; the vote reaching H unlinks
+ * block_tables[seq, lb] = -1. No seq_len cap. INT4 pools: a physical page
+ * must appear at most once across block_tables (the pool's allocator hands
+ * each page to one sequence); the scale rewrite of a page is not atomic. */
 int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs,
                         int32_t num_heads, int32_t seq_len, int32_t *block_tables,
                         int32_t max_blocks_per_seq, int32_t *is_block_free,

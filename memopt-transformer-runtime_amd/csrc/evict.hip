@@ -33,10 +33,11 @@ struct RowZero {
   void *k, *v, *ks, *vs;
 };
 
-// Zero (page, pos, head) in both K and V. fp16: D halves; INT4 pages: the
-// row's codes set to 8 (value 0) and its D/64 fp16 scales to 1.0, which is exactly
-// what quantizing a zero row produces (scale 1.0 for an all-zero group,
-// src/csrc/quantization.cu:168).
+// Zero (page, pos, head) in both K and V. fp16: D halves. INT4 pages: the
+// row's D/64 fp16 scales in K and V set to 0 and its codes left in place:
+// every element then dequantizes to (code - 8) * 0 = 0 (-0 for codes below
+// 8), so attention sees exactly a zeroed row (score 0, no V contribution),
+// and an evicted token costs 8 written bytes instead of D + 4 D/64.
 __device__ void zero_row(const RowZero &z, int64_t page, int32_t pos, int32_t head) {
   if (z.kv_format == MEMOPT_KV_FP16) {
     const int64_t off = ((page * z.bs + pos) * z.H + head) * (int64_t)z.D;
@@ -56,54 +57,87 @@ __device__ void zero_row(const RowZero &z, int64_t page, int32_t pos, int32_t he
   } else {
     const Int4Page f(z.D);
     uint8_t *blk = (uint8_t *)z.k + (page * z.H + head) * f.block;
-    const int32_t dpl = z.D / 8;
-    for (int c = 0; c < 8; ++c) {
-      uint8_t *kb = blk + f.kcodes + f.k_byte(pos, c * dpl);
-      for (int w = 0; w < dpl / 8; ++w) reinterpret_cast<uint32_t *>(kb)[w] = 0x88888888u;
-      for (int u = 0; u < dpl / 4; ++u)
-        *reinterpret_cast<uint16_t *>(blk + f.vcodes + f.v_byte(pos, c * dpl + 4 * u)) = 0x8888u;
-    }
     for (int g = 0; g < f.G; ++g) {
-      reinterpret_cast<half_t *>(blk + f.kscales)[f.scale_idx(pos, g)] = (half_t)1.0f;
-      reinterpret_cast<half_t *>(blk + f.vscales)[f.scale_idx(pos, g)] = (half_t)1.0f;
+      reinterpret_cast<half_t *>(blk + f.kscales)[f.scale_idx(pos, g)] = (half_t)0.0f;
+      reinterpret_cast<half_t *>(blk + f.vscales)[f.scale_idx(pos, g)] = (half_t)0.0f;
     }
   }
 }
 
-// Zeroes the evicted tokens of one (page, head) block of the INT4 page pool,
-// one wave per block: lane l = 8p + c owns tokens p and p + 8 and dims
-// [c D/8, (c+1) D/8) of the block, the slot layout of page_format.hpp.
-// Write-only stores of exactly the bytes of evicted tokens: K codes (D/16
-// contiguous bytes per token), V codes (2-byte units interleaved with the
-// other token) and the fp16 scales (adjacent per token pair).
+// Zeroes the evicted tokens of one (page, head) block of the INT4 page pool
+// (scales to 0, as zero_row), one wave per block, with 2- and 4-byte stores
+// (the path for pools that zero_int4_scale_lines does not take): lane
+// l = 8p + c writes the K and V scales of groups c, c + 8, ... for tokens p
+// and p + 8, the two halves of one 32-bit scale word. Rewriting the codes as
+// well (8 to 16 bytes per token interleaved with kept tokens) cost 1.8-2x:
+// those partial lines become read-modify-writes in memory.
 __device__ __forceinline__ void zero_int4_block(uint8_t *blk, int32_t D, int lane, bool e0, bool e1) {
   if (!(e0 || e1)) return;
   const Int4Page f(D);
-  const int32_t bpl = f.BPL, p = lane >> 3, c = lane & 7;
-  uint8_t *ks = blk + f.kcodes + lane * bpl, *vs = blk + f.vcodes + lane * bpl;
-  if (bpl == 16) {
-    const uint2 k8 = {0x88888888u, 0x88888888u};
-    if (e0) *reinterpret_cast<uint2 *>(ks) = k8;
-    if (e1) *reinterpret_cast<uint2 *>(ks + 8) = k8;
-  } else {
-    for (int i = 0; i < bpl / 2; ++i) {
-      if (e0) ks[i] = 0x88;
-      if (e1) ks[bpl / 2 + i] = 0x88;
+  const int32_t p = lane >> 3, c = lane & 7;
+  half_t *ksc = reinterpret_cast<half_t *>(blk + f.kscales), *vsc = reinterpret_cast<half_t *>(blk + f.vscales);
+  for (int32_t g = c; g < f.G; g += 8) {
+    const int32_t i0 = g * 16 + 2 * p;  // scale_idx(p, g); scale_idx(p + 8, g) = i0 + 1
+    if (e0 && e1) {
+      *reinterpret_cast<uint32_t *>(ksc + i0) = 0u;
+      *reinterpret_cast<uint32_t *>(vsc + i0) = 0u;
+    } else {
+      const int32_t i = i0 + (e0 ? 0 : 1);
+      ksc[i] = (half_t)0.0f;
+      vsc[i] = (half_t)0.0f;
     }
   }
-  if (e0 && e1) {
-    for (int u = 0; u < bpl / 4; ++u) reinterpret_cast<uint32_t *>(vs)[u] = 0x88888888u;
-  } else {
-    const int half = e0 ? 0 : 1;
-    for (int u = 0; u < bpl / 4; ++u) reinterpret_cast<uint16_t *>(vs + 4 * u)[half] = 0x8888u;
-  }
-  // the first lane of each 64-dim scale group writes the group's scales
-  const int32_t dpl = D / 8, g = (c * dpl) / 64;
-  if ((c * dpl) % 64 == 0) {
-    half_t *ksc = reinterpret_cast<half_t *>(blk + f.kscales), *vsc = reinterpret_cast<half_t *>(blk + f.vscales);
-    const int32_t i0 = g * 16 + 2 * p;
-    if (e0) { ksc[i0] = (half_t)1.0f; vsc[i0] = (half_t)1.0f; }
-    if (e1) { ksc[i0 + 1] = (half_t)1.0f; vsc[i0 + 1] = (half_t)1.0f; }
+}
+
+// Zeroes the evicted tokens of a row's INT4 blocks (scales to 0, as
+// zero_row) by rewriting whole scale regions. A block's K scales and V
+// scales are one contiguous run of 64 G bytes (16 tokens x G groups x 2 B,
+// twice), so a wave covers 64 / (4 G) blocks per step, 4 G lanes each with
+// one 16-byte chunk: load the chunk, clear the evicted tokens' halves, store
+// it back. Writing full lines instead of single 2- or 4-byte scales avoids
+// the memory side's read-modify-write of partial lines: 1.6x faster on
+// config 3's shape. The steps are unrolled UL deep so the block-table and
+// scale loads of UL steps are in flight together.
+//   The read-modify-write is not atomic: a physical page must appear at most
+// once in the block tables of one call (one sequence owns a page, as the
+// pool's allocator hands them out). Requires G <= 16 and a 16-byte aligned
+// pool; the caller uses zero_int4_block otherwise.
+template <int NW>
+__device__ __forceinline__ void zero_int4_scale_lines(uint8_t *pool, const Int4Page &f, int32_t H, int32_t h,
+                                                      const int32_t *bt, const uint32_t *evbits, int32_t nlb,
+                                                      int64_t total_pool_blocks, int32_t wave, int32_t lane) {
+  constexpr int UL = 8;
+  const int32_t lpb = 4 * f.G, bpw = 64 / lpb, jb = lane / lpb, q = lane % lpb;
+  const int32_t gmask = 16 * f.G - 1;  // scale index inside the K (or V) run
+  for (int32_t lb0 = wave * bpw * UL; lb0 < nlb; lb0 += NW * bpw * UL) {
+    uint32_t mm[UL];  // evicted tokens of the lane's block, 0 if none or unmapped
+    int32_t ph[UL];
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      const int32_t lb = lb0 + u * bpw + jb;
+      mm[u] = (jb < bpw && lb < nlb) ? (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu : 0u;
+      ph[u] = mm[u] ? bt[lb] : -1;
+    }
+    uint4 v[UL];
+    uint4 *w[UL];
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      if (!(ph[u] >= 0 && ph[u] < total_pool_blocks)) mm[u] = 0;
+      w[u] = reinterpret_cast<uint4 *>(pool + ((int64_t)(mm[u] ? ph[u] : 0) * H + h) * f.block + f.kscales) + q;
+      if (mm[u]) v[u] = *w[u];
+    }
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      if (!mm[u]) continue;
+      uint32_t x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {  // half 8 q + k of the run; scale_idx(t, g) = 16 g + 2 (t & 7) + (t >> 3)
+        const int32_t i = (8 * q + k) & gmask;
+        const int32_t t = 8 * (i & 1) + ((i & 15) >> 1);
+        if ((mm[u] >> t) & 1) x[k >> 1] &= (k & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+      }
+      *w[u] = (uint4){x[0], x[1], x[2], x[3]};
+    }
   }
 }
 
@@ -256,16 +290,20 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
     const Int4Page f(z.D);
     const int32_t nlb = min((L + 15) / 16, M);
     const int32_t p = lane >> 3;
-    for (int32_t lb0 = wave * 64; lb0 < nlb; lb0 += NW * 64) {
-      const int32_t phys_l = lb0 + lane < nlb ? bt[lb0 + lane] : -1;
-      const int32_t cnt = min(64, nlb - lb0);
-      for (int i = 0; i < cnt; ++i) {
-        const int32_t lb = lb0 + i;
-        const uint32_t m16 = (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu;  // tokens 16 lb .. 16 lb + 15
-        const int32_t phys = __builtin_amdgcn_readlane(phys_l, i);
-        if (m16 == 0 || phys < 0 || phys >= total_pool_blocks) continue;  // wave-uniform
-        zero_int4_block((uint8_t *)z.k + ((int64_t)phys * z.H + h) * f.block, z.D, lane, (m16 >> p) & 1,
-                        (m16 >> (p + 8)) & 1);
+    if (f.G <= 16 && (reinterpret_cast<uintptr_t>(z.k) & 15) == 0) {
+      zero_int4_scale_lines<NW>((uint8_t *)z.k, f, z.H, h, bt, evbits, nlb, total_pool_blocks, wave, lane);
+    } else {
+      for (int32_t lb0 = wave * 64; lb0 < nlb; lb0 += NW * 64) {
+        const int32_t phys_l = lb0 + lane < nlb ? bt[lb0 + lane] : -1;
+        const int32_t cnt = min(64, nlb - lb0);
+        for (int i = 0; i < cnt; ++i) {
+          const int32_t lb = lb0 + i;
+          const uint32_t m16 = (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu;  // tokens 16 lb .. 16 lb + 15
+          const int32_t phys = __builtin_amdgcn_readlane(phys_l, i);
+          if (m16 == 0 || phys < 0 || phys >= total_pool_blocks) continue;  // wave-uniform
+          zero_int4_block((uint8_t *)z.k + ((int64_t)phys * z.H + h) * f.block, z.D, lane, (m16 >> p) & 1,
+                          (m16 >> (p + 8)) & 1);
+        }
       }
     }
   } else {

@@ -402,23 +402,23 @@ def keep_count(retain_ratio: float, L: int) -> int:
 
 
 def _zero_row(pools, phys: int, pos: int, head: int) -> None:
-    """Zero one (token, head) row of K and V in every pool format (INT4 pages:
-    codes 8 and scale 1.0, what quantizing a zero row yields)."""
+    """Zero one (token, head) row of K and V in every pool format. fp16: zeros.
+    INT4 pages: the row's K and V group scales set to 0 with its codes kept,
+    so every element dequantizes to (code - 8) * 0 = 0 (-0 for codes below 8)
+    and attention sees a zeroed row (this build's representation; the
+    reference zeroes fp16 rows only, src/csrc/kv_cache.cu:937-973)."""
     if pools["format"] == "fp16":
         pools["k"][phys, pos, head, :] = 0
         pools["v"][phys, pos, head, :] = 0
     else:
         D = pools["D"]
         G = D // GROUP
-        k_off, v_off, s_idx = int4_page_maps(D)
+        _, _, s_idx = int4_page_maps(D)
         blk = pools["pages"][phys, head]
-        blk[k_off[pos]] = 0x88
-        blk[8 * D + v_off[pos]] = 0x88
-        one = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
         for base in (16 * D, 16 * D + 32 * G):
             for g in range(G):
                 i = base + 2 * s_idx[pos, g]
-                blk[i], blk[i + 1] = one[0], one[1]
+                blk[i], blk[i + 1] = 0, 0
 
 
 def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
@@ -428,8 +428,7 @@ def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
     Per (seq, head): sink scores := 1e38 (:722-726); keep = keep_count;
     tau = keep-th largest boosted score; tokens with boosted score < tau are
     evicted (ties at tau kept); every evicted (token, head) row is zeroed
-    (fp16: zeros; INT4 pages: codes 8 and scale 1.0 — what quantizing a
-    zero row yields); pools = {"format": "fp16", "k", "v"} or
+    (fp16: zeros; INT4 pages: its scales set to 0, see _zero_row); pools = {"format": "fp16", "k", "v"} or
     {"format": "int4", "pages", "D"}. A logical block whose block_size positions are all
     evicted in this head votes is_block_free[phys] += 1; the vote that
     reaches H sets block_tables[seq, lb] = -1 (:993-1014).

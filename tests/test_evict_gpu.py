@@ -55,6 +55,37 @@ def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
     same_bits(ibf_d, ibf)
 
 
+@pytest.mark.parametrize("D", [128, 192, 1088])
+def test_evict_tokens_int4_head_dims(D):
+    """INT4 zeroing over the scale-line path (G = D / 64 groups: 2 and 3
+    give 8 and 5 blocks per wave step) and over the per-token fallback taken
+    when G > 16 (D = 1088)."""
+    rng = np.random.default_rng(D)
+    N, H, L, bs, r, sinks = 2, 3, 300, 16, 0.6, 4
+    M = (L + bs - 1) // bs
+    nb = N * M + 2
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    T = nb * bs
+    k = rng.standard_normal((T, H, D)).astype(np.float16)
+    v = rng.standard_normal((T, H, D)).astype(np.float16)
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)),
+                         to_dev(np.arange(T, dtype=np.int32)))
+    scores = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    scores[1, :, 32:48] = 1e-6  # one logical block evicted in every head -> unlinked
+    bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
+    ibf = np.zeros(nb, np.int32)
+    before = _pool_state("int4")
+    bt_d, ibf_d = to_dev(bt), to_dev(ibf)
+    memopt_C.evict_tokens(to_dev(scores), bt_d, ibf_d, r, sinks)
+    O.evict_tokens_intended(scores, bt, ibf, r, sinks, before, bs)
+    after = _pool_state("int4")
+    for key in before:
+        if isinstance(before[key], np.ndarray):
+            same_bits(after[key], before[key])
+    same_bits(bt_d, bt)
+    same_bits(ibf_d, ibf)
+
+
 def test_evict_then_free_sweep():
     memopt_C.init_pool(8, 16, 2, 64)
     bt = torch.tensor([[memopt_C.allocate_block() for _ in range(4)]], dtype=torch.int32, device=dev())

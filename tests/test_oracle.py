@@ -338,10 +338,11 @@ def _pools(fmt, nb, bs, H, D, rng):
 
 
 def _row(pools, p, s, h):
-    """K row (token s of page p, head h) as fp16 values, any pool format."""
+    """K and V rows (token s of page p, head h) as fp16 values, any pool format."""
     if pools["format"] == "fp16":
-        return pools["k"][p, s, h]
-    return O.from_int4_pages(pools["pages"][p:p + 1], pools["D"])[0][0, s, h]
+        return np.stack([pools["k"][p, s, h], pools["v"][p, s, h]])
+    k, v = O.from_int4_pages(pools["pages"][p:p + 1], pools["D"])
+    return np.stack([k[0, s, h], v[0, s, h]])
 
 
 @pytest.mark.parametrize("fmt", ["fp16", "int4"])
