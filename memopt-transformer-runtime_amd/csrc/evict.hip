@@ -143,6 +143,8 @@ __device__ __forceinline__ void zero_int4_scale_lines(uint8_t *pool, const Int4P
 
 // Longest score row handled (the evicted-token bitmask lives in LDS).
 static constexpr int32_t kEvictMaxLen = 1 << 19;
+// Keys kept in LDS for the last radix pass of a streamed row (24 KB).
+static constexpr int32_t kEvictCand = 6144;
 
 // One workgroup of NT threads per (seq, head): blockIdx.x = seq, blockIdx.y = head.
 // Thread tid owns tokens t = tid + i NT; with R > 0 their keys stay in
@@ -238,15 +240,70 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
   };
 
   // ---- A: radix select ----
+  // Streamed rows (R == 0) copy the keys that match the 16-bit prefix into
+  // LDS (cand, after the bitmask words) during the third pass, and the last
+  // pass reads them from there when they fit: four streamed passes over the
+  // row instead of five. After two 8-bit digits the matching keys are
+  // typically a fraction of a percent of the row.
+  __shared__ uint32_t s_cnt;
+  uint32_t *cand = evbits + (L + 63) / 64 * 2;
+  uint32_t ncand = 0xFFFFFFFFu;
   uint32_t prefix = 0, pmask = 0, k = (uint32_t)keep;
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = tid; i < NW * 256; i += NT) (&hist[0][0])[i] = 0;
-    if (tid == 0) suf[256] = 0;
+    if (tid == 0) {
+      suf[256] = 0;
+      s_cnt = 0;
+    }
     __syncthreads();
-    for_keys_hist([&](int32_t, uint32_t key) {
+    auto bump = [&](int32_t, uint32_t key) {
       if ((key & pmask) == prefix) atomicAdd(&hist[wave][(key >> shift) & 0xFF], 1u);
-    });
+    };
+    if (R == 0 && shift == 8) {
+      // Counts the key's digit and appends it to cand; every lane is active.
+      auto push = [&](int32_t t, uint32_t key) __attribute__((always_inline)) {
+        const bool m = t < L && (key & pmask) == prefix;
+        if (m) atomicAdd(&hist[wave][(key >> 8) & 0xFF], 1u);
+        const uint64_t bal = __ballot(m);
+        if (bal) {  // wave-uniform
+          uint32_t b0 = 0;
+          if (lane == 0) b0 = atomicAdd(&s_cnt, (uint32_t)__popcll(bal));
+          b0 = __builtin_amdgcn_readfirstlane(b0);
+          const uint32_t pos =
+              b0 + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+          if (m && pos < (uint32_t)kEvictCand) cand[pos] = key;
+        }
+      };
+      if constexpr (V4) {  // the float4 order of for_keys_hist
+        for (int32_t base = 0; base < L; base += 32 * NT) {
+          float4 v[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            v[j] = *reinterpret_cast<const float4 *>(row + min(base + 4 * (tid + j * NT), L - 4));
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int32_t t = base + 4 * (tid + j * NT);
+            push(t, t < sinks ? sink_key : order_key(v[j].x));
+            push(t + 1, t + 1 < sinks ? sink_key : order_key(v[j].y));
+            push(t + 2, t + 2 < sinks ? sink_key : order_key(v[j].z));
+            push(t + 3, t + 3 < sinks ? sink_key : order_key(v[j].w));
+          }
+        }
+      } else {
+        for (int32_t base = 0; base < L; base += 8 * NT) {
+          uint32_t kb[8];
+          keys_of(base + tid, IntC<8>{}, kb);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) push(base + tid + j * NT, kb[j]);
+        }
+      }
+    } else if (R == 0 && shift == 0 && ncand <= (uint32_t)kEvictCand) {
+      for (uint32_t i = tid; i < ncand; i += NT) bump(0, cand[i]);
+    } else {
+      for_keys_hist(bump);
+    }
     __syncthreads();
+    if (R == 0 && shift == 8) ncand = s_cnt;
     if (tid < 256) {
       uint32_t c = 0;
 #pragma unroll
@@ -395,6 +452,7 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
   MEMOPT_REQUIRE(seq_len <= kEvictMaxLen, MEMOPT_ERR_UNSUPPORTED,
                  "evict_tokens: seq_len > " + std::to_string(kEvictMaxLen) + " not supported");
   const size_t lds = (size_t)((seq_len + 63) / 64 * 2) * sizeof(uint32_t);
+  const size_t lds_cand = lds + kEvictCand * sizeof(uint32_t);  // streamed rows: + the candidate keys
   const dim3 grid(num_seqs, num_heads);
   hipStream_t st = (hipStream_t)stream;
   // Rows up to 8192 (32768) tokens keep their keys in registers with 256
@@ -406,11 +464,11 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
     hipLaunchKernelGGL((evict_tokens_kernel<1024, 32>), grid, dim3(1024), lds, st, attention_scores, block_tables,
                        is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
   else if (seq_len % 4 == 0 && ((uintptr_t)attention_scores & 15) == 0)
-    hipLaunchKernelGGL((evict_tokens_kernel<1024, 0, true>), grid, dim3(1024), lds, st, attention_scores,
+    hipLaunchKernelGGL((evict_tokens_kernel<1024, 0, true>), grid, dim3(1024), lds_cand, st, attention_scores,
                        block_tables, is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep,
                        sinks, z);
   else
-    hipLaunchKernelGGL((evict_tokens_kernel<1024, 0>), grid, dim3(1024), lds, st, attention_scores, block_tables,
+    hipLaunchKernelGGL((evict_tokens_kernel<1024, 0>), grid, dim3(1024), lds_cand, st, attention_scores, block_tables,
                        is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
   return check_launch("evict_tokens");
 }

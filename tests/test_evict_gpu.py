@@ -55,6 +55,33 @@ def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
     same_bits(ibf_d, ibf)
 
 
+@pytest.mark.parametrize("L", [40000, 40001])
+def test_evict_tokens_streamed_rows_many_ties(L):
+    """Streamed rows whose threshold bin holds far more keys than the LDS
+    candidate buffer (scores take 4 values): the last radix pass streams the
+    row again instead of reading the candidates."""
+    rng = np.random.default_rng(L)
+    N, H, bs, D, r, sinks = 1, 2, 16, 64, 0.6, 4
+    M = (L + bs - 1) // bs
+    nb = N * M + 1
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    T = nb * bs
+    k = rng.standard_normal((T, H, D)).astype(np.float16)
+    memopt_C.write_cache(to_dev(k), to_dev(k), to_dev(np.zeros((1, 1), np.int32)),
+                         to_dev(np.arange(T, dtype=np.int32)))
+    scores = rng.integers(1, 5, size=(N, H, L)).astype(np.float32)
+    bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
+    ibf = np.zeros(nb, np.int32)
+    before = _pool_state("int4")
+    bt_d, ibf_d = to_dev(bt), to_dev(ibf)
+    memopt_C.evict_tokens(to_dev(scores), bt_d, ibf_d, r, sinks)
+    O.evict_tokens_intended(scores, bt, ibf, r, sinks, before, bs)
+    after = _pool_state("int4")
+    same_bits(after["pages"], before["pages"])
+    same_bits(bt_d, bt)
+    same_bits(ibf_d, ibf)
+
+
 @pytest.mark.parametrize("D", [128, 192, 1088])
 def test_evict_tokens_int4_head_dims(D):
     """INT4 zeroing over the scale-line path (G = D / 64 groups: 2 and 3
