@@ -107,7 +107,8 @@ int memopt_free_blocks_count(int64_t *count);
  * contiguous; slot_mapping: int32 [num_tokens], slot = block*bs + pos.
  * FP16 pools get a scatter copy; INT4 pools get a fused group-64 quantize
  * into the page (codes bit-exact with memopt_quantize_kv_cache_int4, scales
- * stored as RNE fp16 of the fp32 scale). Slots outside the pool are skipped
+ * stored as RNE fp16 of the fp32 scale, 9360 = RNE(65504/7) stored as 9352
+ * so that 7 * scale stays finite). Slots outside the pool are skipped
  * on device; the caller validates them beforehand. */
 int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
                        int32_t num_heads, int32_t head_dim,

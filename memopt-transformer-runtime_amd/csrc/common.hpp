@@ -134,6 +134,17 @@ __device__ __forceinline__ float div7(float a) {
 // Group scale from the group's absmax: absmax / 7, or 1 for an all-zero group.
 __device__ __forceinline__ float scale_of(float absmax) { return absmax > 0.0f ? div7(absmax) : 1.0f; }
 
+// fp16 scale stored in an INT4 page: the RNE fp16 of the fp32 group scale,
+// except 9360, which is stored as 9352. 9360 is the RNE of 65504 / 7 (the
+// only fp16 absmax whose scale rounds up that far), and 7 * 9360 = 65520
+// rounds to inf in fp16, so a +-65504 input would dequantize to +-inf; with
+// 9352 it dequantizes to +-65464 (0.06 % low) and stays finite. Inf and NaN
+// scales pass through unchanged.
+__device__ __forceinline__ half_t page_scale(float s) {
+  const half_t h = (half_t)s;
+  return h == (half_t)9360.0f ? (half_t)9352.0f : h;
+}
+
 // Absmax of a 64-element group spread over LANES consecutive lanes (4 or 8,
 // aligned): DPP max inside the lane group.
 template <int LANES>

@@ -11,14 +11,18 @@
 //  * each wave keeps U pages in flight (loads for U pages are issued before
 //    any of them is consumed) and a workgroup runs NW waves over interleaved
 //    pages of one (b, h), so a CU holds tens of KiB of outstanding reads;
-//  * K nibbles become fp16 (bias + code) with one v_bfi_b32 against an fp16
-//    exponent pattern (0x6400 -> 1024 + n for bits 0-3, 0x5400 -> 64 + n for
-//    bits 4-7) and feed v_dot2_f32_f16 directly; the constant bias sum
-//    q . (bias + 8) is subtracted once per token, which leaves q . (code - 8);
-//  * V nibbles are unpacked the same way; the row-layout kernel subtracts the
-//    bias per element (exact fp16 code - 8) and accumulates with v_fma_mix_f32,
-//    the page-layout kernel accumulates bias + code with v_dot2_f32_f16 over a
-//    token pair and removes bias * (sum of weights) once at the end;
+//  * K nibbles become fp16 (64 + code) with one v_bfi_b32 against the fp16
+//    exponent pattern 0x5400 (the nibble in bits 4-7, after a shift for the
+//    even ones) and feed v_dot2_f32_f16 directly; the constant bias sum
+//    q . (64 + 8) is subtracted once per token, which leaves q . (code - 8);
+//  * V nibbles are unpacked against 0x6400 (1024 + n, bits 0-3) and 0x5400
+//    (64 + n, bits 4-7) without shifts, and the bias is subtracted per pair
+//    (exact fp16 code - 8). The row-layout kernel accumulates in fp32; the
+//    page-layout kernel accumulates with v_dot2_f32_f16 over a token pair
+//    against fp16 weights p * (V scale), kept <= 2^15 by raising the softmax
+//    reference point. No bias is carried in the accumulators: removing
+//    1032 * (sum of weights) at the end cost ~1e-2 absolute on output dims
+//    near zero next to a token with a V scale in the hundreds;
 //  * the softmax running max is wave-uniform and lazily raised: it is updated
 //    (with a wave max and a rescale of the accumulators) only when some score
 //    exceeds it by more than 8 in log2 units, so the common page costs no
@@ -89,6 +93,18 @@ __device__ __forceinline__ void unpack_biased(uint32_t w, uint32_t r[4]) {
   r[3] = bfi(kHiMask, w8, kMagic64);
 }
 
+// The same pairs all biased by 64: (e0,e4) and (e2,e6) are shifted into bits
+// 4-7 / 20-23 first. Two shifts more than unpack_biased, and a bias sum of
+// 72 * sum(q) instead of up to 1032 * sum(q): the K dot products start from
+// minus that sum, so a 14x smaller bias keeps 14x more of the fp32 mantissa
+// for the score itself at large |q|.
+__device__ __forceinline__ void unpack_biased64(uint32_t w, uint32_t r[4]) {
+  r[0] = bfi(kHiMask, w << 4, kMagic64);
+  r[1] = bfi(kHiMask, w, kMagic64);
+  r[2] = bfi(kHiMask, w >> 4, kMagic64);
+  r[3] = bfi(kHiMask, w >> 8, kMagic64);
+}
+
 // Same pairs as exact (code - 8) values.
 __device__ __forceinline__ void unpack_exact(uint32_t w, half2_t h[4]) {
   uint32_t r[4];
@@ -145,8 +161,8 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_kernel(const DecodeParams
       qp[k][1] = half2_t{e01.y, e45.y};
       qp[k][2] = half2_t{e23.x, e67.x};
       qp[k][3] = half2_t{e23.y, e67.y};
-      bias = fmaf(1032.0f, (float)e01.x + (float)e45.x + (float)e23.x + (float)e67.x, bias);
-      bias = fmaf(72.0f, (float)e01.y + (float)e45.y + (float)e23.y + (float)e67.y, bias);
+      bias = fmaf(72.0f, ((float)e01.x + (float)e45.x) + ((float)e23.x + (float)e67.x), bias);
+      bias = fmaf(72.0f, ((float)e01.y + (float)e45.y) + ((float)e23.y + (float)e67.y), bias);
     }
   }
 
@@ -186,7 +202,7 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_kernel(const DecodeParams
 #pragma unroll
       for (int k = 0; k < NWORD; ++k) {
         uint32_t r[4];
-        unpack_biased(kw[u].word(k), r);
+        unpack_biased64(kw[u].word(k), r);
 #pragma unroll
         for (int j = 0; j < 4; ++j) dot = __builtin_amdgcn_fdot2(as_half2(r[j]), qp[k][j], dot, false);
       }
@@ -316,16 +332,17 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
       qp[k][1] = half2_t{e01.y, e45.y};
       qp[k][2] = half2_t{e23.x, e67.x};
       qp[k][3] = half2_t{e23.y, e67.y};
-      bias = fmaf(1032.0f, (float)e01.x + (float)e45.x + (float)e23.x + (float)e67.x, bias);
-      bias = fmaf(72.0f, (float)e01.y + (float)e45.y + (float)e23.y + (float)e67.y, bias);
+      bias = fmaf(1032.0f, ((float)e01.x + (float)e45.x) + ((float)e23.x + (float)e67.x), bias);
+      bias = fmaf(72.0f, ((float)e01.y + (float)e45.y) + ((float)e23.y + (float)e67.y), bias);
     }
   }
 
-  // acc accumulates weight * (bias + code) with the bias of unpack_biased
-  // (1024 for dims 4u, 4u+2; 64 for dims 4u+1, 4u+3); wsum = sum of the fp16
-  // weights actually used, so the bias is removed exactly once at the end.
-  float m = -INFINITY, l = 0.0f, wsum = 0.0f;
-  const half2_t kOnes = {(half_t)1.0f, (half_t)1.0f};
+  // acc accumulates weight * (code - 8) over exact fp16 code values: no bias
+  // rides along, so a heavy token adds nothing to dims where its code is 8,
+  // and the fp32 rounding of each v_dot2 stays relative to the output itself.
+  // m starts finite so that exp2(-inf - m) = 0 needs no select for masked
+  // tokens; the first visible score raises it.
+  float m = -3.0e38f, l = 0.0f;
   float acc[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; ++i) acc[i] = 0.0f;
@@ -386,42 +403,61 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
       s1 += xor2(s1);
       s0 += half_mirror(s0);
       s1 += half_mirror(s1);
+      s0 *= p.qk_scale_log2;
+      s1 *= p.qk_scale_log2;
       // Whole page inside the window (the common case): no per-token mask.
       const int32_t tok0 = bt.lp[u] * 16;
-      const bool full = bt.ok[u] && tok0 >= kr.win_lo && tok0 + 16 <= kr.hi;
-      bool v0 = full, v1 = full;
       half2_t sv = bt.sv[u];
-      if (!full) {  // wave-uniform
+      if (!(bt.ok[u] && tok0 >= kr.win_lo && tok0 + 16 <= kr.hi)) {  // wave-uniform
         const int32_t t0 = tok0 + pp, t1 = t0 + 8;
-        v0 = bt.ok[u] && t0 < kr.hi && (t0 >= kr.win_lo || t0 < kr.sink_end);
-        v1 = bt.ok[u] && t1 < kr.hi && (t1 >= kr.win_lo || t1 < kr.sink_end);
+        const bool v0 = bt.ok[u] && t0 < kr.hi && (t0 >= kr.win_lo || t0 < kr.sink_end);
+        const bool v1 = bt.ok[u] && t1 < kr.hi && (t1 >= kr.win_lo || t1 < kr.sink_end);
+        s0 = v0 ? s0 : -INFINITY;
+        s1 = v1 ? s1 : -INFINITY;
         // Masked tokens may carry any scale bits (NaN past the context).
         sv = half2_t{v0 ? sv.x : (half_t)0.0f, v1 ? sv.y : (half_t)0.0f};
       }
-      s0 = v0 ? s0 * p.qk_scale_log2 : -INFINITY;
-      s1 = v1 ? s1 * p.qk_scale_log2 : -INFINITY;
       const float smax = fmaxf(s0, s1);
       if (__any(smax > m + 8.0f)) {  // wave-uniform, rare after the first pages
         const float mn = fmaxf(m, wave_max(smax));
         const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
         l *= alpha;
-        wsum *= alpha;
 #pragma unroll
         for (int d = 0; d < DPL; ++d) acc[d] *= alpha;
         m = mn;
       }
-      const float p0 = v0 ? fast_exp2(s0 - m) : 0.0f;
-      const float p1 = v1 ? fast_exp2(s1 - m) : 0.0f;
+      float p0 = fast_exp2(s0 - m);  // masked tokens: s = -inf, p = 0
+      float p1 = fast_exp2(s1 - m);
+      // The V weights p * (V scale) enter the accumulation as fp16, so they
+      // must stay finite: p reaches 2^8 under the lazy max and a V scale
+      // reaches 9352, past 65504. When a weight of the wave exceeds 2^15
+      // (possible only for V scales above 128), the reference point m is
+      // raised by the integer e that brings the largest weight to <= 2^14,
+      // and everything accumulated so far is scaled by 2^-e. The softmax is
+      // unchanged (m cancels in o / l); weights far below the largest one
+      // lose nothing that shows in the output.
+      const float sv0 = (float)sv.x, sv1 = (float)sv.y;
+      float x0 = p0 * sv0, x1 = p1 * sv1;
+      if (__any(fmaxf(x0, x1) > 32768.0f)) {  // wave-uniform
+        const float e = ceilf(__log2f(wave_max(fmaxf(x0, x1)))) - 14.0f;
+        const float alpha = fast_exp2(-e);
+        l *= alpha;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] *= alpha;
+        m += e;
+        p0 *= alpha;
+        p1 *= alpha;
+        x0 *= alpha;
+        x1 *= alpha;
+      }
       l += p0 + p1;
-      const half2_t wpair = {(half_t)(p0 * (float)sv.x), (half_t)(p1 * (float)sv.y)};
-      wsum = __builtin_amdgcn_fdot2(wpair, kOnes, wsum, false);
+      const half2_t wpair = {(half_t)x0, (half_t)x1};
 #pragma unroll
       for (int k = 0; k < VW; ++k) {
-        uint32_t r[4];
-        unpack_biased(bt.vw[u].word(k), r);
+        half2_t hv[4];
+        unpack_exact(bt.vw[u].word(k), hv);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[4 * k + j] = __builtin_amdgcn_fdot2(as_half2(r[j]), wpair, acc[4 * k + j], false);
+        for (int j = 0; j < 4; ++j) acc[4 * k + j] = __builtin_amdgcn_fdot2(hv[j], wpair, acc[4 * k + j], false);
       }
     }
   };
@@ -440,10 +476,6 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
     base += kStep;
   }
 
-  // Remove the code bias: slot 4u+j of a V word holds dim 4u+j, biased by
-  // 1032 (j even) or 72 (j odd), i.e. (bias + 8) with the -8 code offset.
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) acc[d] = fmaf(-((d & 1) ? 72.0f : 1032.0f), wsum, acc[d]);
   // Sum the 8 token-pair lanes sharing this lane's dims (lanes c, c+8, ...).
   l += dpp_f32<0x128>(l);  // row_ror:8
   l = xor16_sum(l);

@@ -17,10 +17,14 @@
 //   V: 2-byte units interleaved: unit u (4 dims, u = 0..BPL/4-1) occupies
 //      bytes [l*BPL + 4u, +2) for token p and [l*BPL + 4u + 2, +2) for p+8,
 //      so one 32-bit word holds the same 4 dims of both tokens.
-//   scales (fp16, RNE of the fp32 scale): index g*16 + 2*p + h for token
-//      8*h + p, group g — the two tokens of a lane are adjacent.
-// 16-token pages only. Zero rows (never written / evicted) are code 8 (0x88
-// bytes) with scale 1.0, exactly what quantizing a zero row produces.
+//   scales (fp16, RNE of the fp32 scale, except that 9360 = RNE(65504 / 7)
+//      is stored as 9352 so that 7 * scale stays finite in fp16): index
+//      g*16 + 2*p + h for token 8*h + p, group g — the two tokens of a lane
+//      are adjacent.
+// 16-token pages only. Rows never written are code 8 (0x88 bytes) with scale
+// 1.0, exactly what quantizing a zero row produces. Rows removed by
+// evict_tokens keep their codes and get scale 0 in every group, so they
+// dequantize to +-0 like the reference's zeroed fp16 rows.
 #pragma once
 #include <stdint.h>
 

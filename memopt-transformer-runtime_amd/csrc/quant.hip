@@ -167,8 +167,8 @@ __global__ __launch_bounds__(kThreads) void write_int4_kernel(
     *reinterpret_cast<uint16_t *>(vb) = (uint16_t)(wv & 0xFFFFu);
     *reinterpret_cast<uint16_t *>(vb + 4) = (uint16_t)(wv >> 16);
     if ((d0 & 63) == 0) {
-      reinterpret_cast<half_t *>(blk + f.kscales)[f.scale_idx(pos, d0 >> 6)] = (half_t)s_k;
-      reinterpret_cast<half_t *>(blk + f.vscales)[f.scale_idx(pos, d0 >> 6)] = (half_t)s_v;
+      reinterpret_cast<half_t *>(blk + f.kscales)[f.scale_idx(pos, d0 >> 6)] = page_scale(s_k);
+      reinterpret_cast<half_t *>(blk + f.vscales)[f.scale_idx(pos, d0 >> 6)] = page_scale(s_v);
     }
   }
 }
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void write_int4_pages_kernel(
       __builtin_nontemporal_store(w, reinterpret_cast<u32x2_t *>(blk + codes_off + lane * f.BPL));
     }
     if (c % GL == 0)
-      __builtin_nontemporal_store(as_u32(half2_t{(half_t)sc[0], (half_t)sc[1]}),
+      __builtin_nontemporal_store(as_u32(half2_t{page_scale(sc[0]), page_scale(sc[1])}),
                                   reinterpret_cast<uint32_t *>(blk + scales_off + 2 * f.scale_idx(p, (c * DPL) / 64)));
     return;
   }
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void write_int4_pages_kernel(
       *reinterpret_cast<uint16_t *>(vb) = (uint16_t)(w & 0xFFFFu);
       *reinterpret_cast<uint16_t *>(vb + 4) = (uint16_t)(w >> 16);
     }
-    if ((d0 & 63) == 0) reinterpret_cast<half_t *>(blk + scales_off)[f.scale_idx(pos, d0 >> 6)] = (half_t)sc;
+    if ((d0 & 63) == 0) reinterpret_cast<half_t *>(blk + scales_off)[f.scale_idx(pos, d0 >> 6)] = page_scale(sc);
   }
 }
 

@@ -22,9 +22,10 @@ to_int4_pages / from_int4_pages
     Placement of the same group-64 codes in this build's INT4 page buffer
     ([nb, H, block], block = K codes | V codes | K scales | V scales, token
     pairs interleaved for the wave64 decode kernel); scales are RNE fp16 of
-    the fp32 scale. This format has no reference counterpart; pinned by the
-    writer/reader round trip and by direct comparison with ``quantize_int4``
-    of the token-major pool.
+    the fp32 scale (9360 stored as 9352, ``page_scales``). This format has no
+    reference counterpart; pinned by the writer/reader round trip, by direct
+    comparison with ``quantize_int4`` of the token-major pool, and by a
+    per-element loop over ``Int4Page``'s byte formulas.
 write_cache
     src/csrc/kv_cache.cu:228-260. Pinned by the invariant pool[slot] == row.
 paged_attention
@@ -81,7 +82,8 @@ def quantize_int4(cache: np.ndarray, group_size: int = GROUP) -> Tuple[np.ndarra
     Follows src/csrc/quantization.cu:129-202: per 64 consecutive elements of
     the flattened tensor, ``scale = absmax > 0 ? absmax / 7 : 1`` in IEEE fp32
     (:166-168), ``code = clamp((int)roundf(v / scale) + 8, 0, 15)`` (:183-186),
-    ``byte = code[2i] | code[2i+1] << 4`` (:198-200).
+    ``byte = code[2i] | code[2i+1] << 4`` (:198-200). NaN elements are left
+    out of the absmax (fmaxf) and get code 8 ((int)NaN = 0 on the device).
 
     Returns (packed uint8 with last dim halved, scales float32 [numel/64]).
     """
@@ -89,8 +91,12 @@ def quantize_int4(cache: np.ndarray, group_size: int = GROUP) -> Tuple[np.ndarra
     c = np.ascontiguousarray(cache)
     assert c.dtype == np.float16 and c.size % GROUP == 0 and c.shape[-1] % 2 == 0
     g = c.reshape(-1, GROUP).astype(np.float32)
-    absmax = np.abs(g).max(axis=1)
-    scale = np.where(absmax > 0, absmax / np.float32(7.0), np.float32(1.0)).astype(np.float32)
+    # fmaxf drops a NaN operand (quantization.cu:151, :166), so NaN elements
+    # never reach the absmax; an all-NaN group reduces to NaN, and NaN > 0 is
+    # false, which gives scale 1.0 like an all-zero group.
+    absmax = np.fmax.reduce(np.abs(g), axis=1)
+    with np.errstate(invalid="ignore"):
+        scale = np.where(absmax > 0, absmax / np.float32(7.0), np.float32(1.0)).astype(np.float32)
     with np.errstate(invalid="ignore", divide="ignore"):
         q = g / scale[:, None]
     r = _roundf(q)
@@ -231,13 +237,22 @@ def int4_page_maps(D: int):
     return k_off, v_off, s_idx
 
 
+def page_scales(scales: np.ndarray) -> np.ndarray:
+    """fp16 scales stored in INT4 pages: RNE fp16 of the fp32 scale, except
+    9360 (= RNE(65504 / 7), the scale of a group whose absmax is 65504), which
+    is stored as 9352 so that 7 * scale, the largest dequantized magnitude,
+    stays finite in fp16 (7 * 9360 = 65520 rounds to inf)."""
+    sc = np.asarray(scales, dtype=np.float32).astype(np.float16)
+    return np.where(sc == np.float16(9360.0), np.float16(9352.0), sc)
+
+
 def to_int4_pages(k_pool: np.ndarray, v_pool: np.ndarray) -> np.ndarray:
     """fp16 pools [nb, 16, H, D] (K, V) -> INT4 page buffer u8 [nb, H, block].
 
     Codes are the reference's group-64 codes of the token-major pools
     (src/csrc/quantization.cu:115-116 on a contiguous [nb, bs, H, D] tensor:
-    groups = (page, token, head, 64-dim chunk)); scales are stored as RNE
-    fp16 of the fp32 scale.
+    groups = (page, token, head, 64-dim chunk)); scales are stored as
+    :func:`page_scales` of the fp32 scale.
     """
     nb, bs, H, D = k_pool.shape
     assert bs == PAGE_TOKENS and D % GROUP == 0
@@ -248,7 +263,7 @@ def to_int4_pages(k_pool: np.ndarray, v_pool: np.ndarray) -> np.ndarray:
         packed, scales = quantize_int4(pool)
         codes = packed.reshape(nb, bs, H, D // 2).transpose(0, 2, 1, 3)          # [nb, H, t, j]
         out[:, :, code_base + off.reshape(-1)] = codes.reshape(nb, H, -1)
-        sc = scales.reshape(nb, bs, H, G).transpose(0, 2, 1, 3).astype(np.float16)  # [nb, H, t, g]
+        sc = page_scales(scales.reshape(nb, bs, H, G).transpose(0, 2, 1, 3))  # [nb, H, t, g]
         sb = sc.view(np.uint8).reshape(nb, H, bs, G, 2)
         idx = scale_base + 2 * s_idx
         out[:, :, idx.reshape(-1)] = sb[..., 0].reshape(nb, H, -1)
@@ -576,7 +591,9 @@ def decode_int4_torch(q, pages, block_tables, context_lens, window, sinks):
     gather, sinks U window selection, fp32 SDPA, fp16 cast — the torch-only
     route of src/memopt/triton_attention.py:473-550 after
     src/csrc/quantization.cu:232-270), vectorized per sequence. torch CPU
-    tensors in, fp16 [B, 1, H, D] out."""
+    tensors in, fp16 [B, 1, H, D] out. Pages with a block-table entry < 0
+    contribute no keys, and a sequence with no visible key outputs 0, as in
+    :func:`paged_attention`."""
     import torch
     import torch.nn.functional as F
     B, _, H, D = q.shape
@@ -584,10 +601,12 @@ def decode_int4_torch(q, pages, block_tables, context_lens, window, sinks):
     for b in range(B):
         ctx = int(context_lens[b])
         pg = block_tables[b, : (ctx + PAGE_TOKENS - 1) // PAGE_TOKENS].long()
-        k, v = dequant_pages_torch(pages[pg], D)
+        k, v = dequant_pages_torch(pages[pg.clamp(min=0)], D)
         k, v = k.reshape(-1, H, D)[:ctx], v.reshape(-1, H, D)[:ctx]
         j = torch.arange(ctx)
-        keep = (j >= ctx - window) | (j < sinks)
+        keep = ((j >= ctx - window) | (j < sinks)) & (pg >= 0).repeat_interleave(PAGE_TOKENS)[:ctx]
+        if not bool(keep.any()):
+            continue
         k, v = k[keep].float().permute(1, 0, 2)[None], v[keep].float().permute(1, 0, 2)[None]
         o = F.scaled_dot_product_attention(q[b:b + 1].float().permute(0, 2, 1, 3), k, v,
                                            scale=float(np.float32(1.0) / np.sqrt(np.float32(D))))

@@ -23,8 +23,12 @@ def assert_close(got, want, atol=ATOL, rtol=RTOL, what=""):
     w = want.detach().float().cpu().numpy() if isinstance(want, torch.Tensor) else np.asarray(want, np.float32)
     assert g.shape == w.shape, (g.shape, w.shape)
     err = np.abs(g - w)
-    bad = err > atol + rtol * np.abs(w)
-    assert not bad.any(), f"{what}: {bad.sum()} elements off, max abs err {err.max():.3e}"
+    tol = atol + rtol * np.abs(w)
+    bad = ~(err <= tol)
+    if bad.any():
+        i = np.unravel_index(np.argmax(np.where(bad, err / tol, -1.0)), g.shape)
+        raise AssertionError(f"{what}: {bad.sum()} elements off, max abs err {np.nanmax(err):.3e}; "
+                             f"worst at {tuple(int(x) for x in i)}: got {g[i]!r}, want {w[i]!r}")
 
 
 def same_bits(got, want):

@@ -448,3 +448,154 @@ def test_rounding_shortcut_matches_roundf():
         assert O.round_shortcut_mismatches(b, b + 1) == 0
     assert O.round_shortcut_mismatches(lo, hi, h=0.5) > 0
     assert O.round_shortcut_mismatches(lo, hi, h=0.4999999) > 0
+
+
+# ---------------------------------------------------------------------------
+# Non-finite groups: the reference reduces the absmax with fmaxf, which drops
+# a NaN operand (src/csrc/quantization.cu:151, :166)
+# ---------------------------------------------------------------------------
+
+def _nonfinite_groups():
+    rng = np.random.default_rng(11)
+    g = (rng.standard_normal((8, 64)) * 2).astype(np.float16)
+    g[0, 5] = np.nan                        # one NaN among finite values
+    g[1, :] = np.nan                        # all NaN
+    g[2, :] = 0
+    g[2, 7] = np.nan                        # NaN among zeros
+    g[3, 9] = np.inf                        # +inf
+    g[4, 0], g[4, 1] = -np.inf, np.nan      # -inf next to a NaN
+    g[5, :] = 65504
+    g[5, ::2] = -65504                      # the fp16 extremes
+    g[6, 3], g[6, 4] = np.nan, 65504        # NaN next to the largest finite value
+    return g
+
+
+def test_quantize_nonfinite_groups_match_c_restatement():
+    g = _nonfinite_groups()
+    p1, s1 = O.quantize_int4(g)
+    p2, s2 = O.quantize_int4_c(g)
+    assert np.array_equal(p1, p2)
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+
+
+def test_quantize_nan_left_out_of_absmax():
+    g = _nonfinite_groups()
+    p, s = O.quantize_int4(g)
+    codes = O.unpack_codes(p).reshape(-1, 64)
+    finite = np.where(np.isnan(g[0]), np.float16(0), np.abs(g[0])).astype(np.float32)
+    assert s[0] == np.float32(finite.max()) / np.float32(7)      # the NaN never reaches the absmax
+    assert codes[0, 5] == 8                                      # (int)NaN = 0 -> code 8
+    assert s[1] == 1.0 and (codes[1] == 8).all()                 # all NaN: like an all-zero group
+    assert s[2] == 1.0 and (codes[2] == 8).all()
+    assert np.isinf(s[3]) and (codes[3] == 8).all()              # inf scale: every quotient is 0 or NaN
+    assert np.isinf(s[4]) and (codes[4] == 8).all()
+    assert s[6] == np.float32(65504) / np.float32(7) and codes[6, 4] == 15 and codes[6, 3] == 8
+
+
+def test_page_scale_keeps_extremes_finite():
+    """Every positive finite fp16 absmax: the page scale is the RNE fp16 of
+    the fp32 scale except for 65504, and 7 * page scale stays <= 65504."""
+    a = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    s = a / np.float32(7)
+    ps = O.page_scales(s)
+    assert np.array_equal(ps == s.astype(np.float16), a != 65504)
+    assert ps[a == 65504] == np.float16(9352)
+    assert (ps.astype(np.float32) * 7 <= 65504).all()
+    k = np.zeros((1, 16, 1, 64), np.float16)
+    k[0, :, 0, 0] = 65504
+    k[0, 3, 0, 1] = -65504
+    pages = O.to_int4_pages(k, k)
+    kd, vd = O.from_int4_pages(pages, 64)
+    assert np.isfinite(kd.astype(np.float32)).all() and np.isfinite(vd.astype(np.float32)).all()
+    assert kd[0, 0, 0, 0] == np.float16(65464) and kd[0, 3, 0, 1] == np.float16(-65464)
+
+
+def _page_k_byte(t, d, D):
+    """Int4Page::k_byte (memopt-transformer-runtime_amd/csrc/page_format.hpp)."""
+    dpl = D // 8
+    c, r = d // dpl, d % dpl
+    return (8 * (t & 7) + c) * dpl + (t >> 3) * (dpl // 2) + r // 2
+
+
+def _page_v_byte(t, d, D):
+    """Int4Page::v_byte."""
+    dpl = D // 8
+    c, r = d // dpl, d % dpl
+    return (8 * (t & 7) + c) * dpl + (r // 4) * 4 + (t >> 3) * 2 + (r % 4) // 2
+
+
+def _page_scale_idx(t, g):
+    """Int4Page::scale_idx."""
+    return g * 16 + 2 * (t & 7) + (t >> 3)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_int4_pages_per_element_loop(D):
+    """to_int4_pages equals a page buffer built one element at a time from
+    the page-format formulas and the exact-rational quantizer."""
+    rng = np.random.default_rng(12 + D)
+    nb, H, G = 2, 3, D // 64
+    kp = (rng.standard_normal((nb, 16, H, D)) * np.where(rng.random((nb, 16, H, D)) < 0.01, 8, 1)).astype(np.float16)
+    vp = (rng.standard_normal((nb, 16, H, D)) * 3).astype(np.float16)
+    vp[1, 5, 2, :64] = 65504                      # the clamped page scale
+    got = O.to_int4_pages(kp, vp)
+    want = np.zeros_like(got)
+    for pool, code_base, scale_base, byte in ((kp, 0, 16 * D, _page_k_byte), (vp, 8 * D, 16 * D + 32 * G, _page_v_byte)):
+        for b in range(nb):
+            for t in range(16):
+                for h in range(H):
+                    for g in range(G):
+                        codes, scale = exact_quant_group(pool[b, t, h, 64 * g:64 * g + 64])
+                        for i, code in enumerate(codes):
+                            d = 64 * g + i
+                            want[b, h, code_base + byte(t, d, D)] |= code << (4 * (d & 1))
+                        sc = np.float16(float(scale))
+                        if sc == np.float16(9360):
+                            sc = np.float16(9352)
+                        j = scale_base + 2 * _page_scale_idx(t, g)
+                        want[b, h, j:j + 2] = np.frombuffer(sc.tobytes(), np.uint8)
+    assert np.array_equal(got, want)
+
+
+def test_write_cache_loop():
+    """oracle.write_cache against a token-by-token loop of pool[slot // bs, slot % bs] = row."""
+    rng = np.random.default_rng(13)
+    nb, bs, H, D, T = 9, 16, 2, 64, 70
+    pool = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    rows = rng.standard_normal((T, H, D)).astype(np.float16)
+    slots = rng.permutation(nb * bs)[:T].astype(np.int32)
+    want = pool.copy()
+    for t in range(T):
+        s = int(slots[t])
+        for h in range(H):
+            for d in range(D):
+                want[s // bs, s % bs, h, d] = rows[t, h, d]
+    got = pool.copy()
+    O.write_cache(got, rows, slots)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("seed,B,H,D,ctx,W,sinks,unlink", [
+    (0, 2, 4, 128, [300, 77], 1 << 20, 0, 0),
+    (1, 3, 2, 64, [1000, 17, 256], 200, 4, 2),
+    (2, 2, 2, 128, [513, 1], 64, 20, 1),
+    (3, 1, 3, 64, [160], 16, 4, 10),      # every page unlinked: zeros
+])
+def test_decode_int4_torch_matches_composition_oracle(seed, B, H, D, ctx, W, sinks, unlink):
+    """The CPU baseline's vectorized decode (bench.py times it) computes the
+    composition oracle's function: windows, sinks, unlinked pages, empty sets."""
+    rng = np.random.default_rng(seed)
+    M = (max(ctx) + 15) // 16
+    nb = B * M + 3
+    kp = (rng.standard_normal((nb, 16, H, D)) * np.where(rng.random((nb, 16, H, D)) < 0.005, 10, 1)).astype(np.float16)
+    vp = rng.standard_normal((nb, 16, H, D)).astype(np.float16)
+    q = rng.standard_normal((B, 1, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:B * M].reshape(B, M).astype(np.int32)
+    for i in range(unlink):
+        bt[0, i % M] = -1
+    cl = np.array(ctx, np.int32)
+    pages = O.to_int4_pages(kp, vp)
+    want = O.paged_attention_int4(q, pages, bt, cl, 1 << 30, W, num_sink_tokens=sinks).astype(np.float32)
+    got = O.decode_int4_torch(torch.as_tensor(q), torch.as_tensor(pages), torch.as_tensor(bt), torch.as_tensor(cl),
+                              min(W, 1 << 30), sinks).float().numpy()
+    assert np.abs(got - want).max() <= 1e-3
