@@ -226,7 +226,28 @@ typedef struct memopt_attn_desc {
 } memopt_attn_desc;
 
 int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes);
+/* A call whose workspace pointer is NULL with workspace_bytes 0 (for instance
+ * through memopt_dynamic_sparse_attention) runs its decode unsplit. */
 int memopt_paged_attention(const memopt_attn_desc *desc, void *stream);
+
+/* Bytes of the per-GPU static scratch of memopt_paged_attention_noalloc. */
+#define MEMOPT_NOALLOC_SCRATCH_BYTES (4LL << 20)
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Computes exactly what memopt_paged_attention computes for
+ * the same descriptor (desc->workspace is ignored) and allocates nothing: the
+ * decode kernels' split-K partials, and the staged K/V of a multi-query call
+ * when they fit, live in a static device array of
+ * MEMOPT_NOALLOC_SCRATCH_BYTES (4 MiB) per GPU, held until the process ends.
+ * Multi-query calls whose staging does not fit run the in-kernel staging
+ * kernel, which needs no scratch. A decode whose partials exceed the array
+ * (B * H * splits * (head_dim + 2) * 4 bytes; splits grow only while B * H
+ * is below two workgroups per CU) returns MEMOPT_ERR_INVALID. Every call on
+ * a GPU shares that GPU's array, so calls that overlap on one GPU (other
+ * streams or host threads) race: the caller serializes them. The first call
+ * on each device resolves the array's device address there. */
+int memopt_paged_attention_noalloc(const memopt_attn_desc *desc, void *stream);
 
 #ifdef __cplusplus
 }

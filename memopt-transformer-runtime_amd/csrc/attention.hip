@@ -17,6 +17,9 @@
 //     online softmax. INT4 elements are dequantized to fp16 exactly as the
 //     reference's dequantize kernel would (fp16(RNE((code-8)*scale))) before
 //     use, so it computes the reference composition.
+#include <mutex>
+#include <string>
+
 #include "attention.hpp"
 #include "page_format.hpp"
 
@@ -195,6 +198,57 @@ static int decode_workspace(const memopt_attn_desc &d, int32_t *splits, int64_t 
   return MEMOPT_OK;
 }
 
+// Split count and partials buffer of a decode call: the caller's workspace
+// when the shape splits; a call that passes no workspace at all (the
+// reference signature, memopt_dynamic_sparse_attention) runs unsplit.
+static int decode_plan(const memopt_attn_desc &d, int32_t *splits) {
+  int64_t need;
+  decode_workspace(d, splits, &need);
+  if (need > 0 && d.workspace == nullptr && d.workspace_bytes == 0) {
+    *splits = 1;
+    return MEMOPT_OK;
+  }
+  MEMOPT_REQUIRE(need == 0 || (d.workspace && d.workspace_bytes >= need), MEMOPT_ERR_INVALID,
+                 "paged_attention: workspace too small (need " + std::to_string(need) + " bytes)");
+  return MEMOPT_OK;
+}
+
+// Scratch of memopt_paged_attention_noalloc: split-K partials (and staged
+// K/V of small multi-query calls) for callers that cannot allocate. Each GPU
+// holds its own copy until the process ends; every noalloc call on a GPU
+// shares it. Host code never passes `scratch` itself to a kernel (on the host
+// it names a stand-in, not device memory): it resolves the device address
+// once per device with hipGetSymbolAddress and passes that.
+static __device__ __align__(256) uint8_t scratch[MEMOPT_NOALLOC_SCRATCH_BYTES];
+
+static constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device (nullptr + error set on
+// failure). Resolved on the first call per device, with that device current.
+static void *scratch_address() {
+  static std::mutex mu;
+  static void *addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    set_error("paged_attention_noalloc: no usable current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      set_error(std::string("paged_attention_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev] = ptr;
+  }
+  return addr[dev];
+}
+
 }  // namespace memopt
 
 using namespace memopt;
@@ -229,10 +283,8 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
 
   if (use_decode_int4(d)) {
     int32_t splits;
-    int64_t need;
-    decode_workspace(d, &splits, &need);
-    MEMOPT_REQUIRE(need == 0 || (d.workspace && d.workspace_bytes >= need), MEMOPT_ERR_INVALID,
-                   "paged_attention: workspace too small (need " + std::to_string(need) + " bytes)");
+    rc = decode_plan(d, &splits);
+    if (rc != MEMOPT_OK) return rc;
     DecodeParams p;
     p.q = (const half_t *)d.query;
     p.out = (half_t *)d.out;
@@ -280,10 +332,8 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
 
   if (use_decode_fp16(d)) {
     int32_t splits;
-    int64_t need;
-    decode_workspace(d, &splits, &need);
-    MEMOPT_REQUIRE(need == 0 || (d.workspace && d.workspace_bytes >= need), MEMOPT_ERR_INVALID,
-                   "paged_attention: workspace too small (need " + std::to_string(need) + " bytes)");
+    rc = decode_plan(d, &splits);
+    if (rc != MEMOPT_OK) return rc;
     DecodeParams p;
     p.q = (const half_t *)d.query;
     p.out = (half_t *)d.out;
@@ -344,6 +394,35 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
                  "paged_attention: q_len/batch > 65535 not supported by the generic kernel");
   hipLaunchKernelGGL(generic_attention_kernel, dim3(d.num_heads, d.q_len, d.batch), dim3(64), 0, s, g);
   return check_launch("paged_attention(generic)");
+}
+
+int memopt_paged_attention_noalloc(const memopt_attn_desc *desc, void *stream) {
+  MEMOPT_REQUIRE(desc, MEMOPT_ERR_INVALID, "paged_attention_noalloc: null descriptor");
+  memopt_attn_desc d = *desc;
+  d.workspace = nullptr;
+  d.workspace_bytes = 0;
+  int rc = validate(d);
+  if (rc != MEMOPT_OK) return rc;
+  if (d.batch == 0 || d.q_len == 0 || d.num_heads == 0 || d.head_dim == 0) return MEMOPT_OK;
+  int64_t need = 0;
+  if (use_decode_int4(d) || use_decode_fp16(d)) {
+    int32_t splits;
+    decode_workspace(d, &splits, &need);
+    MEMOPT_REQUIRE(need <= MEMOPT_NOALLOC_SCRATCH_BYTES, MEMOPT_ERR_INVALID,
+                   "paged_attention_noalloc: the split-K partials need " + std::to_string(need) +
+                       " bytes, more than the " + std::to_string((long long)MEMOPT_NOALLOC_SCRATCH_BYTES) +
+                       "-byte static scratch");
+  } else if (prefill_supported(d)) {
+    need = prefill_workspace_bytes(d);
+    if (need > MEMOPT_NOALLOC_SCRATCH_BYTES) need = 0;  // in-kernel staging: no scratch
+  }
+  if (need > 0) {
+    void *ws = scratch_address();
+    if (ws == nullptr) return MEMOPT_ERR_HIP;
+    d.workspace = ws;
+    d.workspace_bytes = MEMOPT_NOALLOC_SCRATCH_BYTES;
+  }
+  return memopt_paged_attention(&d, stream);
 }
 
 int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_len, int32_t num_heads,

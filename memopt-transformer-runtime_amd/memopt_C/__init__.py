@@ -101,6 +101,7 @@ _c_dsa = _sig("memopt_dynamic_sparse_attention",
               [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _i32, _vp, _i32, _vp, _i32, _i32, _vp, _vp])
 _c_ws = _sig("memopt_attention_workspace_size", [ctypes.POINTER(AttnDesc), ctypes.POINTER(_i64)])
 _c_attn = _sig("memopt_paged_attention", [ctypes.POINTER(AttnDesc), _vp])
+_c_attn_noalloc = _sig("memopt_paged_attention_noalloc", [ctypes.POINTER(AttnDesc), _vp])
 
 KV_FP16, KV_INT4, KV_INT4_ROWS = 0, 1, 2
 _FORMATS = {"fp16": KV_FP16, "int4": KV_INT4}
@@ -522,7 +523,7 @@ def _int4_pages_base(key_cache, value_cache, num_heads, head_dim):
 
 
 def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size,
-                    num_sink_tokens, causal, key_scales, value_scales, kv_layout, out):
+                    num_sink_tokens, causal, key_scales, value_scales, kv_layout, out, alloc_workspace=True):
     """Validate like src/csrc/attention.cu:383-439 and fill an AttnDesc.
 
     Returns (desc, out, workspace, keepalive) or (None, out, None, ()) for empty shapes.
@@ -606,7 +607,7 @@ def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, m
     need = _i64()
     _check(_c_ws(ctypes.byref(d), ctypes.byref(need)))
     ws = None
-    if need.value > 0:
+    if need.value > 0 and alloc_workspace:
         ws = torch.empty(need.value, dtype=torch.uint8, device=query.device)
         d.workspace, d.workspace_bytes = ws.data_ptr(), need.value
     return d, out, ws, keep
@@ -646,17 +647,25 @@ class PreparedAttention:
     each call launches on the current stream with a single C-ABI call and
     returns ``out`` (overwritten in place). Intended for decode loops where
     only the tensor *contents* change between steps.
+
+    ``no_alloc=True`` allocates no workspace and launches through
+    ``memopt_paged_attention_noalloc``, whose split-K partials live in a
+    static per-GPU scratch array; no call allocates device memory, which suits
+    capture into a HIP graph. Calls sharing that array must not overlap on
+    one GPU.
     """
 
     def __init__(self, query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size, *,
-                 num_sink_tokens=0, causal=False, key_scales=None, value_scales=None, kv_layout=None, out=None):
+                 num_sink_tokens=0, causal=False, key_scales=None, value_scales=None, kv_layout=None, out=None,
+                 no_alloc=False):
         _require(isinstance(query, torch.Tensor) and query.is_cuda, "query must be a CUDA tensor")
         self.device = query.device
         with torch.cuda.device(self.device):
             self._d, self.out, self._ws, self._keep = _attention_desc(
                 query, key_cache, value_cache, block_tables, context_lens, max_seq_len, window_size,
-                num_sink_tokens, causal, key_scales, value_scales, kv_layout, out)
+                num_sink_tokens, causal, key_scales, value_scales, kv_layout, out, alloc_workspace=not no_alloc)
         self._dp = ctypes.byref(self._d) if self._d is not None else None
+        self._fn = _c_attn_noalloc if no_alloc else _c_attn
 
     @property
     def workspace_bytes(self) -> int:
@@ -666,5 +675,5 @@ class PreparedAttention:
     def __call__(self, stream: Optional[int] = None) -> torch.Tensor:
         if self._dp is not None:
             s = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
-            _check(_c_attn(self._dp, s))
+            _check(self._fn(self._dp, s))
         return self.out
