@@ -117,8 +117,10 @@ int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
 /* Replaces evict_cache(block_tables, attention_scores, retain_ratio,
  * num_sink_tokens) — src/csrc/kv_cache.cu:379-559. scores: f32
  * [num_blocks, block_size, H]. Per (block, head): keep = max(1,
- * floor(r*bs)) largest scores, zero rows scoring below the keep-th
- * largest (sinks ignored, as in the reference). */
+ * floor(r*bs)); rows scoring below the keep-th largest of the scores above
+ * -1e38 (below -1e38 itself when fewer than keep exceed it) are zeroed: the
+ * reference's selection with its -1e38 sentinel. Sinks ignored, as in the
+ * reference. block_size up to 8192. */
 int memopt_evict_cache(const float *attention_scores, int64_t num_blocks,
                        float retain_ratio, int32_t num_sink_tokens, void *stream);
 
@@ -132,9 +134,13 @@ int memopt_evict_cache(const float *attention_scores, int64_t num_blocks,
  * (INT4: every group scale of the row set to 0, codes kept, so the row
  * dequantizes to zeros). A logical block with all block_size positions
  * evicted votes is_block_free[phys] += 1; the vote reaching H unlinks
- * block_tables[seq, lb] = -1. No seq_len cap. INT4 pools: a physical page
- * must appear at most once across block_tables (the pool's allocator hands
- * each page to one sequence); the scale rewrite of a page is not atomic. */
+ * block_tables[seq, lb] = -1. No seq_len cap (rows longer than 32768
+ * tokens run as several workgroups per row). A physical page listed more
+ * than once in block_tables (shared between sequences) receives the union
+ * of their evictions: INT4 pools detect it and clear that call's scales
+ * atomically. The library keeps per-device scratch for this (page marks
+ * sized to the pool, the long-row workspace), allocated on first use and
+ * grown as needed; calls on one device must not overlap. */
 int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs,
                         int32_t num_heads, int32_t seq_len, int32_t *block_tables,
                         int32_t max_blocks_per_seq, int32_t *is_block_free,

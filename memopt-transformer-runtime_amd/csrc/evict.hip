@@ -11,6 +11,8 @@
 //     counts one token per 32-token run, so no block is ever freed);
 //   * no seq_len cap (the reference rejects seq_len > 4096).
 // evict_cache: src/csrc/kv_cache.cu:379-483 (per (block, head) selection).
+#include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -31,7 +33,16 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 struct RowZero {
   int32_t kv_format, H, D, bs;
   void *k, *v, *ks, *vs;
+  // INT4 pools: *alias_flag == epoch when some physical page appears more
+  // than once in this call's block tables (set by mark_pages_kernel).
+  const uint32_t *alias_flag;
+  uint32_t epoch;
 };
+
+// Whether this call's block tables alias a physical page (wave-uniform).
+__device__ __forceinline__ bool pages_aliased(const RowZero &z) {
+  return z.alias_flag != nullptr && *z.alias_flag == z.epoch;
+}
 
 // Zero (page, pos, head) in both K and V. fp16: D halves. INT4 pages: the
 // row's D/64 fp16 scales in K and V set to 0 and its codes left in place:
@@ -98,25 +109,31 @@ __device__ __forceinline__ void zero_int4_block(uint8_t *blk, int32_t D, int lan
 // the memory side's read-modify-write of partial lines: 1.6x faster on
 // config 3's shape. The steps are unrolled UL deep so the block-table and
 // scale loads of UL steps are in flight together.
-//   The read-modify-write is not atomic: a physical page must appear at most
-// once in the block tables of one call (one sequence owns a page, as the
-// pool's allocator hands them out). Requires G <= 16 and a 16-byte aligned
-// pool; the caller uses zero_int4_block otherwise.
+//   The plain read-modify-write assumes a physical page appears once in the
+// call's block tables (one sequence owns a page, as the pool's allocator
+// hands them out). When mark_pages_kernel found a page listed twice, the
+// chunk's words are cleared with atomic ANDs instead, so evictions of every
+// row that lists the page survive (their union). Requires G <= 16 and a
+// 16-byte aligned pool; the caller uses zero_int4_block otherwise. Logical
+// blocks [lb_begin, lb_end) of the row, waves wave, wave + NW, ...
 template <int NW>
 __device__ __forceinline__ void zero_int4_scale_lines(uint8_t *pool, const Int4Page &f, int32_t H, int32_t h,
-                                                      const int32_t *bt, const uint32_t *evbits, int32_t nlb,
-                                                      int64_t total_pool_blocks, int32_t wave, int32_t lane) {
+                                                      const int32_t *bt, const uint32_t *evbits, int32_t lb_begin,
+                                                      int32_t lb_end, int64_t total_pool_blocks, int32_t wave,
+                                                      int32_t lane, bool aliased) {
   constexpr int UL = 8;
   const int32_t lpb = 4 * f.G, bpw = 64 / lpb, jb = lane / lpb, q = lane % lpb;
   const int32_t gmask = 16 * f.G - 1;  // scale index inside the K (or V) run
-  for (int32_t lb0 = wave * bpw * UL; lb0 < nlb; lb0 += NW * bpw * UL) {
+  const int32_t nlb = lb_end;
+  for (int32_t lb0 = lb_begin + wave * bpw * UL; lb0 < nlb; lb0 += NW * bpw * UL) {
     uint32_t mm[UL];  // evicted tokens of the lane's block, 0 if none or unmapped
     int32_t ph[UL];
 #pragma unroll
-    for (int u = 0; u < UL; ++u) {
+    for (int u = 0; u < UL; ++u) {  // bitmask and block-table loads are independent
       const int32_t lb = lb0 + u * bpw + jb;
-      mm[u] = (jb < bpw && lb < nlb) ? (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu : 0u;
-      ph[u] = mm[u] ? bt[lb] : -1;
+      const bool in = jb < bpw && lb < nlb;
+      mm[u] = in ? (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu : 0u;
+      ph[u] = in ? bt[lb] : -1;
     }
     uint4 v[UL];
     uint4 *w[UL];
@@ -124,43 +141,140 @@ __device__ __forceinline__ void zero_int4_scale_lines(uint8_t *pool, const Int4P
     for (int u = 0; u < UL; ++u) {
       if (!(ph[u] >= 0 && ph[u] < total_pool_blocks)) mm[u] = 0;
       w[u] = reinterpret_cast<uint4 *>(pool + ((int64_t)(mm[u] ? ph[u] : 0) * H + h) * f.block + f.kscales) + q;
-      if (mm[u]) v[u] = *w[u];
+      if (mm[u] && !aliased) v[u] = *w[u];
     }
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
       if (!mm[u]) continue;
-      uint32_t x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      uint32_t keepm[4] = {~0u, ~0u, ~0u, ~0u};
 #pragma unroll
       for (int k = 0; k < 8; ++k) {  // half 8 q + k of the run; scale_idx(t, g) = 16 g + 2 (t & 7) + (t >> 3)
         const int32_t i = (8 * q + k) & gmask;
         const int32_t t = 8 * (i & 1) + ((i & 15) >> 1);
-        if ((mm[u] >> t) & 1) x[k >> 1] &= (k & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+        if ((mm[u] >> t) & 1) keepm[k >> 1] &= (k & 1) ? 0x0000FFFFu : 0xFFFF0000u;
       }
-      *w[u] = (uint4){x[0], x[1], x[2], x[3]};
+      if (aliased) {
+        uint32_t *wd = reinterpret_cast<uint32_t *>(w[u]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (keepm[k] != ~0u) atomicAnd(wd + k, keepm[k]);
+      } else {
+        *w[u] = (uint4){v[u].x & keepm[0], v[u].y & keepm[1], v[u].z & keepm[2], v[u].w & keepm[3]};
+      }
     }
   }
 }
 
-// Longest score row handled (the evicted-token bitmask lives in LDS).
-static constexpr int32_t kEvictMaxLen = 1 << 19;
-// Keys kept in LDS for the last radix pass of a streamed row (24 KB).
-static constexpr int32_t kEvictCand = 6144;
+// Rows up to kShortRow tokens run evict_tokens_kernel (one workgroup per
+// row, keys in registers); longer rows run the split kernels below.
+static constexpr int32_t kShortRow = 1024 * 32;
+
+// hist[digit] += 1 for the lanes with m. Keys of one row often share their
+// leading digits (and a bracket's candidates share more), so most lanes of
+// a wave can hit one bin, and same-address LDS atomics serialize: the digit
+// of the wave's first matching lane is added with one atomic by one lane
+// when 16 or more lanes share it; only the other lanes issue their own.
+__device__ __forceinline__ void hist_add_agg(uint32_t *hist, uint32_t digit, bool m) {
+  const uint64_t act = __ballot(m);
+  if (act) {  // wave-uniform
+    const int lead = __builtin_ctzll(act);
+    const uint32_t d0 = __builtin_amdgcn_readlane(digit, lead);
+    const uint64_t same = __ballot(m && digit == d0);
+    const uint32_t n_same = (uint32_t)__popcll(same);
+    if (n_same >= 16) {
+      if ((int)(threadIdx.x & 63) == lead) atomicAdd(&hist[d0], n_same);
+      m = m && digit != d0;
+    }
+  }
+  if (m) atomicAdd(&hist[digit], 1u);
+}
+
+template <int NT>
+struct SelectShared {
+  uint32_t hist[NT / 64][256];
+  uint32_t prefix, k;
+};
+
+// Key of the k-th largest (1 <= k <= number of keys) of the keys handed out
+// by visit(f), which calls f(key) for every key of the calling thread. Four
+// 8-bit radix passes (MSB first): per-wave LDS histograms of the digit among
+// keys matching the prefix so far; then wave 0 alone sums the waves' bins
+// (4 per lane), forms suffix sums with a wave scan and picks the digit, so
+// a pass costs two workgroup barriers. AGG: histogram through hist_add_agg
+// (for keys that mostly share their leading digits). Every thread of the
+// workgroup calls it.
+template <int NT, bool AGG, typename Visit>
+__device__ uint32_t radix_select(Visit visit, uint32_t k, SelectShared<NT> &sh) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint32_t prefix = 0, pmask = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < NW * 256; i += NT) (&sh.hist[0][0])[i] = 0;
+    __syncthreads();
+    visit([&](uint32_t key) {
+      const bool m = (key & pmask) == prefix;
+      const uint32_t digit = (key >> shift) & 0xFF;
+      if constexpr (AGG) {
+        hist_add_agg(sh.hist[wave], digit, m);
+      } else if (m) {
+        atomicAdd(&sh.hist[wave][digit], 1u);
+      }
+    });
+    __syncthreads();
+    if (wave == 0) {
+      // lane owns bins 4 lane .. 4 lane + 3
+      uint32_t c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += sh.hist[w][4 * lane + j];
+        c[j] = v;
+      }
+      const uint32_t tot = c[0] + c[1] + c[2] + c[3];
+      // above = sum of the totals of lanes > lane (exclusive suffix scan)
+      uint32_t inc = tot;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_down(inc, off, 64);
+        if (lane + off < 64) inc += o;
+      }
+      uint32_t above = inc - tot;
+      // suffix count of bin 4 lane + j = above + c[j] + ... + c[3]
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        const uint32_t upto = above + c[j];  // keys with digit >= 4 lane + j
+        if (upto >= k && above < k) {
+          sh.prefix = prefix | ((uint32_t)(4 * lane + j) << shift);
+          sh.k = k - above;
+        }
+        above = upto;
+      }
+    }
+    __syncthreads();
+    prefix = sh.prefix;
+    k = sh.k;
+    pmask |= 0xFFu << shift;
+  }
+  return prefix;
+}
+
+__device__ __forceinline__ uint32_t token_key(const float *row, int32_t t, int32_t sinks) {
+  return t < sinks ? order_key(1e38f) : order_key(row[t]);
+}
 
 // One workgroup of NT threads per (seq, head): blockIdx.x = seq, blockIdx.y = head.
-// Thread tid owns tokens t = tid + i NT; with R > 0 their keys stay in
-// registers (rows up to R NT tokens are read once), with R == 0 the row is
-// streamed from memory in batches of 8 loads per pass.
-//  A. tau = key of the keep-th largest sink-boosted score, by a 4-pass 8-bit
-//     radix select (MSB first): per-wave LDS histograms of the digit among
-//     keys matching the prefix so far, then a parallel suffix sum over the
-//     256 bins picks the digit.
+// Thread tid owns tokens t = tid + i NT, i < R; their keys stay in registers,
+// so the row is read once (rows up to R NT tokens).
+//  A. tau = key of the keep-th largest sink-boosted score, by radix_select.
 //  B. evicted-token bitmask in LDS (key < tau, sinks excluded), then zero the
 //     evicted (token, head) rows.
 //  C. block votes: a full logical block whose every token is evicted votes
 //     is_block_free[phys] += 1; the vote that reaches H unlinks it. A head
 //     votes only after its own zeroing, so the H-th vote (the unlink) comes
 //     after every head has read the block-table entry.
-template <int NT, int R, bool V4 = false>
+template <int NT, int R>
 __global__ __launch_bounds__(NT) void evict_tokens_kernel(
     const float *__restrict__ scores, int32_t *__restrict__ block_tables, int32_t *__restrict__ is_block_free,
     int32_t H, int32_t L, int32_t M, int64_t total_pool_blocks, int32_t keep, int32_t sinks, RowZero z) {
@@ -168,165 +282,32 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
   const int32_t n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float *row = scores + ((int64_t)n * H + h) * L;
-  __shared__ uint32_t hist[NW][256];
-  __shared__ uint32_t suf[257];
-  __shared__ uint32_t s_prefix, s_k;
+  __shared__ SelectShared<NT> sh;
   extern __shared__ uint32_t evbits[];  // (L + 63) / 64 * 2 words
 
-  const uint32_t sink_key = order_key(1e38f);
-  // All loads of a batch are issued first (index clamped into the row),
-  // then turned into keys: a load placed under the sink test would be waited
-  // on before the next one is issued.
-  auto keys_of = [&](int32_t t0, auto nc, uint32_t *kout) __attribute__((always_inline)) {
-    constexpr int N = decltype(nc)::value;
-    float v[N];
+  // All loads are issued first (index clamped into the row), then turned
+  // into keys: a load placed under the sink test would be waited on before
+  // the next one is issued.
+  uint32_t kreg[R];
+  {
+    float v[R];
 #pragma unroll
-    for (int j = 0; j < N; ++j) v[j] = row[min(t0 + j * NT, L - 1)];
+    for (int j = 0; j < R; ++j) v[j] = row[min(tid + j * NT, L - 1)];
 #pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const uint32_t kv = order_key(v[j]);
-      kout[j] = t0 + j * NT < sinks ? sink_key : kv;
-    }
-  };
-  uint32_t kreg[R > 0 ? R : 1];
-  if constexpr (R > 0) keys_of(tid, IntC<R>{}, kreg);
+    for (int j = 0; j < R; ++j) kreg[j] = tid + j * NT < sinks ? order_key(1e38f) : order_key(v[j]);
+  }
   // Calls f(t, key) for every token of this thread.
   auto for_keys = [&](auto f) __attribute__((always_inline)) {
-    if constexpr (R > 0) {
 #pragma unroll
-      for (int i = 0; i < R; ++i) {
-        const int32_t t = tid + i * NT;
-        if (t < L) f(t, kreg[i]);
-      }
-    } else {
-      for (int32_t base = 0; base < L; base += 8 * NT) {
-        uint32_t kb[8];
-        keys_of(base + tid, IntC<8>{}, kb);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int32_t t = base + tid + j * NT;
-          if (t < L) f(t, kb[j]);
-        }
-      }
-    }
-  };
-
-  // Radix-pass visitor: streamed rows whose length is a multiple of 4 (and a
-  // 16-byte aligned base) are read as float4, a quarter of the load
-  // instructions of the token-per-lane order; the histograms do not depend
-  // on the visiting order.
-  auto for_keys_hist = [&](auto f) __attribute__((always_inline)) {
-    if constexpr (R == 0 && V4) {
-      for (int32_t base = 0; base < L; base += 32 * NT) {
-        float4 v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          v[j] = *reinterpret_cast<const float4 *>(row + min(base + 4 * (tid + j * NT), L - 4));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int32_t t = base + 4 * (tid + j * NT);
-          auto one = [&](int32_t tq, float x) __attribute__((always_inline)) {
-            if (tq < L) f(tq, tq < sinks ? sink_key : order_key(x));
-          };
-          one(t, v[j].x);
-          one(t + 1, v[j].y);
-          one(t + 2, v[j].z);
-          one(t + 3, v[j].w);
-        }
-      }
-    } else {
-      for_keys(f);
+    for (int i = 0; i < R; ++i) {
+      const int32_t t = tid + i * NT;
+      if (t < L) f(t, kreg[i]);
     }
   };
 
   // ---- A: radix select ----
-  // Streamed rows (R == 0) copy the keys that match the 16-bit prefix into
-  // LDS (cand, after the bitmask words) during the third pass, and the last
-  // pass reads them from there when they fit: four streamed passes over the
-  // row instead of five. After two 8-bit digits the matching keys are
-  // typically a fraction of a percent of the row.
-  __shared__ uint32_t s_cnt;
-  uint32_t *cand = evbits + (L + 63) / 64 * 2;
-  uint32_t ncand = 0xFFFFFFFFu;
-  uint32_t prefix = 0, pmask = 0, k = (uint32_t)keep;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < NW * 256; i += NT) (&hist[0][0])[i] = 0;
-    if (tid == 0) {
-      suf[256] = 0;
-      s_cnt = 0;
-    }
-    __syncthreads();
-    auto bump = [&](int32_t, uint32_t key) {
-      if ((key & pmask) == prefix) atomicAdd(&hist[wave][(key >> shift) & 0xFF], 1u);
-    };
-    if (R == 0 && shift == 8) {
-      // Counts the key's digit and appends it to cand; every lane is active.
-      auto push = [&](int32_t t, uint32_t key) __attribute__((always_inline)) {
-        const bool m = t < L && (key & pmask) == prefix;
-        if (m) atomicAdd(&hist[wave][(key >> 8) & 0xFF], 1u);
-        const uint64_t bal = __ballot(m);
-        if (bal) {  // wave-uniform
-          uint32_t b0 = 0;
-          if (lane == 0) b0 = atomicAdd(&s_cnt, (uint32_t)__popcll(bal));
-          b0 = __builtin_amdgcn_readfirstlane(b0);
-          const uint32_t pos =
-              b0 + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-          if (m && pos < (uint32_t)kEvictCand) cand[pos] = key;
-        }
-      };
-      if constexpr (V4) {  // the float4 order of for_keys_hist
-        for (int32_t base = 0; base < L; base += 32 * NT) {
-          float4 v[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            v[j] = *reinterpret_cast<const float4 *>(row + min(base + 4 * (tid + j * NT), L - 4));
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int32_t t = base + 4 * (tid + j * NT);
-            push(t, t < sinks ? sink_key : order_key(v[j].x));
-            push(t + 1, t + 1 < sinks ? sink_key : order_key(v[j].y));
-            push(t + 2, t + 2 < sinks ? sink_key : order_key(v[j].z));
-            push(t + 3, t + 3 < sinks ? sink_key : order_key(v[j].w));
-          }
-        }
-      } else {
-        for (int32_t base = 0; base < L; base += 8 * NT) {
-          uint32_t kb[8];
-          keys_of(base + tid, IntC<8>{}, kb);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) push(base + tid + j * NT, kb[j]);
-        }
-      }
-    } else if (R == 0 && shift == 0 && ncand <= (uint32_t)kEvictCand) {
-      for (uint32_t i = tid; i < ncand; i += NT) bump(0, cand[i]);
-    } else {
-      for_keys_hist(bump);
-    }
-    __syncthreads();
-    if (R == 0 && shift == 8) ncand = s_cnt;
-    if (tid < 256) {
-      uint32_t c = 0;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) c += hist[w][tid];
-      suf[tid] = c;
-    }
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {  // suf[i] := sum of bins >= i
-      const uint32_t v = (tid < 256 && tid + off < 256) ? suf[tid + off] : 0u;
-      __syncthreads();
-      if (tid < 256) suf[tid] += v;
-      __syncthreads();
-    }
-    if (tid < 256 && suf[tid] >= k && suf[tid + 1] < k) {
-      s_prefix = prefix | ((uint32_t)tid << shift);
-      s_k = k - suf[tid + 1];
-    }
-    __syncthreads();
-    prefix = s_prefix;
-    k = s_k;
-    pmask |= 0xFFu << shift;
-  }
-  const uint32_t tau = prefix;
+  const uint32_t tau = radix_select<NT, false>([&](auto f) { for_keys([&](int32_t, uint32_t key) { f(key); }); },
+                                               (uint32_t)keep, sh);
 
   // ---- B: evicted bitmask (the 64 lanes of a wave hold 64 consecutive tokens) ----
   const int32_t nwords = (L + 63) / 64 * 2;
@@ -341,14 +322,14 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
   });
   __syncthreads();
   auto ev = [&](int32_t t) { return (evbits[t >> 5] >> (t & 31)) & 1u; };
-
   const int32_t *bt = block_tables + (int64_t)n * M;
   if (z.kv_format == MEMOPT_KV_INT4) {
     const Int4Page f(z.D);
     const int32_t nlb = min((L + 15) / 16, M);
     const int32_t p = lane >> 3;
     if (f.G <= 16 && (reinterpret_cast<uintptr_t>(z.k) & 15) == 0) {
-      zero_int4_scale_lines<NW>((uint8_t *)z.k, f, z.H, h, bt, evbits, nlb, total_pool_blocks, wave, lane);
+      zero_int4_scale_lines<NW>((uint8_t *)z.k, f, z.H, h, bt, evbits, 0, nlb, total_pool_blocks, wave, lane,
+                                pages_aliased(z));
     } else {
       for (int32_t lb0 = wave * 64; lb0 < nlb; lb0 += NW * 64) {
         const int32_t phys_l = lb0 + lane < nlb ? bt[lb0 + lane] : -1;
@@ -409,17 +390,544 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
   }
 }
 
-// One wave per (block, head): lane i owns position i (bs <= 64).
-__global__ __launch_bounds__(64) void evict_cache_kernel(const float *__restrict__ scores, int32_t bs,
-                                                         int32_t H, int32_t keep, RowZero z) {
+// ---------------------------------------------------------------------------
+// Aliased physical pages (INT4 pools)
+// ---------------------------------------------------------------------------
+// marks[phys] = (epoch << 32) | (entry + 1) of the last block-table entry of
+// this call that names page phys; a second entry naming it within the same
+// call (same epoch) sets *flag = epoch. The epoch changes every call, so the
+// marks never need clearing. Only logical blocks that hold tokens of the row
+// count (lb < nlb).
+struct MarkArgs {
+  const int32_t *bt;
+  int64_t entries;  // num_seqs * max_blocks_per_seq (0: nothing to mark)
+  int32_t M, nlb;
+  int64_t total_pool_blocks;
+  unsigned long long *marks;
+  uint32_t *flag;
+  uint32_t epoch;
+};
+
+__device__ __forceinline__ void mark_entry(const MarkArgs &a, int64_t e) {
+  if ((int32_t)(e % a.M) >= a.nlb) return;
+  const int32_t phys = a.bt[e];
+  if (phys < 0 || phys >= a.total_pool_blocks) return;
+  const unsigned long long mine = ((unsigned long long)a.epoch << 32) | (uint32_t)(e + 1);
+  const unsigned long long old = atomicExch(&a.marks[phys], mine);
+  if ((uint32_t)(old >> 32) == a.epoch) atomicMax(a.flag, a.epoch);
+}
+
+__global__ __launch_bounds__(256) void mark_pages_kernel(const MarkArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e < a.entries) mark_entry(a, e);
+}
+
+// ---------------------------------------------------------------------------
+// Long rows (L > 32768): several workgroups per (seq, head)
+// ---------------------------------------------------------------------------
+// With one workgroup per row, config-5-sized batches ([4, 32, 131072] scores)
+// occupy 128 of the 256 CUs and read each row four times. Long rows instead
+// run four kernels:
+//  K1 one workgroup per row: a bracket [lo, hi] around the keep-th largest
+//     key from a 16 x 512-key sample spread over the row;
+//  K2 kClassifySplit workgroups per row: one read of the row sorts each token into
+//     kept (key > hi), evicted (key < lo, straight into the row's bitmask)
+//     or candidate (appended to the row's candidate list with its index);
+//  K3 one workgroup per row: if the bracket holds the keep-th key (fewer
+//     than keep keys above hi, at least keep at or above lo, the candidates
+//     fit), tau = the exact (keep - above)-th largest candidate and the
+//     candidates below it join the bitmask; otherwise (a miss, or heavy
+//     ties) an exact radix select over the whole row and a full bitmask;
+//  K4 kApplySplit workgroups per row: zero the evicted rows of a range of
+//     logical blocks, then vote for that range's fully evicted blocks.
+// The result is the same exact top-k as the single-workgroup kernel.
+static constexpr int32_t kSampleChunks = 16, kSampleChunk = 512, kSample = kSampleChunks * kSampleChunk;
+static constexpr int32_t kRowCand = 16384;  // candidate slots per row
+static constexpr int32_t kLdsKeys = 8192;   // candidate keys the resolve kernel stages in LDS
+static constexpr int32_t kLdsWords = 4096;  // bitmask words the resolve kernel merges per LDS round
+static constexpr int32_t kApplySplit = 32;  // apply workgroups per row
+static constexpr int32_t kClassifySplit = 8;   // classify workgroups per row
+
+// Per-row state in the long-row workspace.
+struct RowState {
+  uint32_t lo, hi, above, ncand, tau, pad[3];
+};
+
+struct LongRows {
+  const float *scores;
+  int32_t H, L, keep, sinks;
+  int32_t words;      // bitmask words per row ((L + 63) / 64 * 2)
+  RowState *state;    // [rows]
+  uint32_t *bits;     // [rows][words]
+  uint2 *cand;        // [rows][kRowCand] (key, token)
+};
+
+// K1: sample bracket. Sample rank of the keep-th key: ks = keep * n / L;
+// the bracket spans ks -+ (4 binomial sigmas + 8) sample ranks.
+// The same launch also marks the block-table entries (alias check, INT4
+// pools), grid-strided; only the apply kernel, three launches later, reads
+// the flag.
+__global__ __launch_bounds__(512) void evict_bracket_kernel(const LongRows lr, const MarkArgs ma) {
+  constexpr int NT = 512, PER = kSample / NT;
+  const int32_t r = blockIdx.x;
+  for (int64_t e = (int64_t)r * NT + threadIdx.x; e < ma.entries; e += (int64_t)gridDim.x * NT) mark_entry(ma, e);
+  const float *row = lr.scores + (int64_t)r * lr.L;
+  __shared__ uint32_t skeys[kSample];
+  __shared__ SelectShared<NT> sh;
+  {
+    float v[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int32_t i = threadIdx.x + j * NT, c = i / kSampleChunk;
+      const int32_t t = (int32_t)((int64_t)c * (lr.L - kSampleChunk) / (kSampleChunks - 1)) + i % kSampleChunk;
+      v[j] = row[t];
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int32_t i = threadIdx.x + j * NT, c = i / kSampleChunk;
+      const int32_t t = (int32_t)((int64_t)c * (lr.L - kSampleChunk) / (kSampleChunks - 1)) + i % kSampleChunk;
+      skeys[i] = t < lr.sinks ? order_key(1e38f) : order_key(v[j]);
+    }
+  }
+  __syncthreads();
+  const float ks = (float)lr.keep * (float)kSample / (float)lr.L;
+  const float margin = 4.0f * sqrtf(fmaxf(ks * (1.0f - ks / (float)kSample), 0.0f)) + 8.0f;
+  const int32_t r_hi = (int32_t)floorf(ks - margin), r_lo = (int32_t)ceilf(ks + margin);
+  // The bounds only need to bracket tau, so 16 bits of each suffice: the
+  // bin (top 16 bits) holding the sample key of rank r_hi, resp. r_lo, found
+  // with one histogram of the first byte for both ranks and one of the
+  // second byte per rank; hi = the top of its bin, lo = the bottom of its.
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ uint32_t h2[2][NW][256];
+  __shared__ uint32_t s_pick[2][2];  // [hi, lo] x (digit, remaining rank)
+  const int32_t want[2] = {r_hi, r_lo};
+  auto pick = [&](uint32_t (*hist)[256], int which, uint32_t k) {
+    // wave 0: the digit holding the k-th largest key and the rank left in it
+    if (wave == 0) {
+      uint32_t c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += hist[w][4 * lane + j];
+        c[j] = v;
+      }
+      const uint32_t tot = c[0] + c[1] + c[2] + c[3];
+      uint32_t inc = tot;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_down(inc, off, 64);
+        if (lane + off < 64) inc += o;
+      }
+      uint32_t above = inc - tot;
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        const uint32_t upto = above + c[j];
+        if (upto >= k && above < k) {
+          s_pick[which][0] = 4 * lane + j;
+          s_pick[which][1] = k - above;
+        }
+        above = upto;
+      }
+    }
+  };
+  for (int i = threadIdx.x; i < 2 * NW * 256; i += NT) (&h2[0][0][0])[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) hist_add_agg(h2[0][wave], skeys[threadIdx.x + j * NT] >> 24, true);
+  __syncthreads();
+  for (int which = 0; which < 2; ++which)
+    if (want[which] >= 1 && want[which] <= kSample) pick(h2[0], which, (uint32_t)want[which]);
+  __syncthreads();
+  const uint32_t d1[2] = {s_pick[0][0], s_pick[1][0]};
+  const uint32_t k1[2] = {s_pick[0][1], s_pick[1][1]};
+  for (int i = threadIdx.x; i < 2 * NW * 256; i += NT) (&h2[0][0][0])[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t key = skeys[threadIdx.x + j * NT];
+#pragma unroll
+    for (int which = 0; which < 2; ++which) hist_add_agg(h2[which][wave], (key >> 16) & 0xFF, (key >> 24) == d1[which]);
+  }
+  __syncthreads();
+  for (int which = 0; which < 2; ++which)
+    if (want[which] >= 1 && want[which] <= kSample) pick(h2[which], which, k1[which]);
+  __syncthreads();
+  const uint32_t hi = r_hi < 1 ? 0xFFFFFFFFu : (((d1[0] << 8) | s_pick[0][0]) << 16) | 0xFFFFu;
+  const uint32_t lo = r_lo > kSample ? 0u : ((d1[1] << 8) | s_pick[1][0]) << 16;
+  if (threadIdx.x == 0) {
+    RowState st = {};
+    st.lo = lo;
+    st.hi = hi;
+    lr.state[r] = st;
+  }
+}
+
+// K2: classify. Workgroup (r, s) covers 256-token units [s*w, (s+1)*w) of
+// row r (the row base is 16-byte aligned and L % 4 == 0 on this path); a
+// wave reads a unit as one float4 per lane (lane l holds tokens 4l .. 4l+3),
+// UL units' loads in flight. Evicted bits: a lane's 4 bits form a nibble,
+// the 8 nibbles of lanes 8w .. 8w+7 are OR-ed into bitmask word w with 3 DPP
+// steps. Candidates go to an LDS list first and reach the row's list with
+// one global atomic per workgroup. V4 = false (rows not float4-aligned):
+// the same tokens per lane, read as four scalar loads.
+template <bool V4>
+__global__ __launch_bounds__(512) void evict_classify_kernel(const LongRows lr) {
+  constexpr int NW = 8, UL = 4, kLdsCand = 4096;
+  const int32_t r = blockIdx.x, lane = threadIdx.x & 63;
+  const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const float *row = lr.scores + (int64_t)r * lr.L;
+  const RowState st = lr.state[r];
+  uint32_t *bits = lr.bits + (int64_t)r * lr.words;
+  uint2 *cand = lr.cand + (int64_t)r * kRowCand;
+  __shared__ uint2 lcand[kLdsCand];
+  __shared__ uint32_t s_n, s_above, s_base;
+  if (threadIdx.x == 0) s_n = s_above = 0;
+  __syncthreads();
+  const int32_t nunits = lr.L / 256 + (lr.L % 256 != 0);
+  const int32_t per = (nunits + kClassifySplit - 1) / kClassifySplit;
+  const int32_t u_begin = blockIdx.y * per, u_end = min(nunits, u_begin + per);
+  const uint32_t sink_key = order_key(1e38f);
+  uint32_t above = 0;
+  for (int32_t u0 = u_begin + wave * UL; u0 < u_end; u0 += NW * UL) {
+    float4 v[UL];
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      if constexpr (V4) {
+        v[u] = *reinterpret_cast<const float4 *>(row + min((u0 + u) * 256 + 4 * lane, lr.L - 4));
+      } else {
+        const int32_t t = (u0 + u) * 256 + 4 * lane;
+        v[u] = make_float4(row[min(t, lr.L - 1)], row[min(t + 1, lr.L - 1)], row[min(t + 2, lr.L - 1)],
+                           row[min(t + 3, lr.L - 1)]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      const int32_t unit = u0 + u;
+      if (unit >= u_end) break;  // wave-uniform
+      const int32_t t0 = unit * 256 + 4 * lane;
+      const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      uint32_t nib = 0, ncand = 0;
+      uint32_t ck[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int32_t t = t0 + j;
+        const bool valid = t < lr.L;
+        const uint32_t key = t < lr.sinks ? sink_key : order_key(x[j]);
+        ck[j] = key;
+        nib |= (uint32_t)(valid && t >= lr.sinks && key < st.lo) << j;
+        above += (uint32_t)(valid && key > st.hi);
+        ncand += (uint32_t)(valid && key >= st.lo && key <= st.hi);
+      }
+      // bitmask word 8 unit + lane / 8: nibbles of the lane's group of 8
+      uint32_t w = nib << (4 * (lane & 7));
+      w |= __builtin_bit_cast(uint32_t, dpp_f32<0xB1>(__builtin_bit_cast(float, w)));   // quad_perm [1,0,3,2]
+      w |= __builtin_bit_cast(uint32_t, dpp_f32<0x4E>(__builtin_bit_cast(float, w)));   // quad_perm [2,3,0,1]
+      w |= __builtin_bit_cast(uint32_t, dpp_f32<0x141>(__builtin_bit_cast(float, w)));  // row_half_mirror
+      if ((lane & 7) == 0 && unit * 8 + (lane >> 3) < lr.words) bits[unit * 8 + (lane >> 3)] = w;
+      if (__ballot(ncand != 0)) {  // wave-uniform
+        // exclusive prefix of the lanes' candidate counts (0..4) over the wave
+        uint32_t pre = 0, tot = 0;
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+          const uint64_t bb = __ballot((ncand >> b) & 1);
+          pre += (uint32_t)__popcll(bb & ((1ull << lane) - 1)) << b;
+          tot += (uint32_t)__popcll(bb) << b;
+        }
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&s_n, tot);
+        base = __builtin_amdgcn_readfirstlane(base) + pre;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int32_t t = t0 + j;
+          if (t < lr.L && ck[j] >= st.lo && ck[j] <= st.hi) {
+            if (base < (uint32_t)kLdsCand) lcand[base] = make_uint2(ck[j], (uint32_t)t);
+            ++base;
+          }
+        }
+      }
+    }
+  }
+  // wave totals of the kept count
+  for (int off = 32; off >= 1; off >>= 1) above += __shfl_xor(above, off, 64);
+  if (lane == 0 && above) atomicAdd(&s_above, above);
+  __syncthreads();
+  const uint32_t n = s_n;
+  if (threadIdx.x == 0) {
+    if (s_above) atomicAdd(&lr.state[r].above, s_above);
+    s_base = n ? atomicAdd(&lr.state[r].ncand, n) : 0u;
+  }
+  __syncthreads();
+  if (n > (uint32_t)kLdsCand) {
+    // more candidates than the LDS list holds: mark the row's list as full
+    // (the resolve kernel then selects over the whole row)
+    if (threadIdx.x == 0) atomicAdd(&lr.state[r].ncand, (uint32_t)kRowCand + 1);
+    return;
+  }
+  const uint32_t base = s_base;
+  for (uint32_t i = threadIdx.x; i < n; i += 512)
+    if (base + i < (uint32_t)kRowCand) cand[base + i] = lcand[i];
+}
+
+// K3: resolve tau and finish the bitmask.
+__global__ __launch_bounds__(1024) void evict_resolve_kernel(const LongRows lr) {
+  constexpr int NT = 1024;
+  const int32_t r = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const float *row = lr.scores + (int64_t)r * lr.L;
+  __shared__ SelectShared<NT> sh;
+  const RowState st = lr.state[r];
+  uint32_t *bits = lr.bits + (int64_t)r * lr.words;
+  const uint2 *cand = lr.cand + (int64_t)r * kRowCand;
+  const uint32_t keep = (uint32_t)lr.keep;
+  if (st.above < keep && st.above + st.ncand >= keep && st.ncand <= (uint32_t)kRowCand) {
+    const uint32_t nc = st.ncand;
+    // the candidates' keys are read four times: from LDS when they fit
+    __shared__ uint32_t lkeys[kLdsKeys];
+    const bool in_lds = nc <= (uint32_t)kLdsKeys;
+    if (in_lds)
+      for (uint32_t i = tid; i < nc; i += NT) lkeys[i] = cand[i].x;
+    __syncthreads();
+    const uint32_t tau = in_lds ? radix_select<NT, true>(
+                                      [&](auto f) {
+                                        for (uint32_t i = tid; i < nc; i += NT) f(lkeys[i]);
+                                      },
+                                      keep - st.above, sh)
+                                : radix_select<NT, true>(
+                                      [&](auto f) {
+                                        for (uint32_t i = tid; i < nc; i += NT) f(cand[i].x);
+                                      },
+                                      keep - st.above, sh);
+    // The evicted candidates' bits: OR-ed into an LDS copy of a range of
+    // kLdsWords bitmask words, which is then merged into the row's words
+    // with coalesced accesses (this workgroup alone owns the row's bitmask
+    // now), instead of one global atomic per candidate.
+    __shared__ uint32_t lbits[kLdsWords];
+    for (int32_t w0 = 0; w0 < lr.words; w0 += kLdsWords) {
+      for (int i = tid; i < kLdsWords; i += NT) lbits[i] = 0;
+      __syncthreads();
+      for (uint32_t i = tid; i < nc; i += NT) {
+        const uint2 c = cand[i];
+        const int32_t w = (int32_t)(c.y >> 5) - w0;
+        if (c.x < tau && (int32_t)c.y >= lr.sinks && w >= 0 && w < kLdsWords) atomicOr(&lbits[w], 1u << (c.y & 31));
+      }
+      __syncthreads();
+      for (int i = tid; i < kLdsWords && w0 + i < lr.words; i += NT)
+        if (lbits[i]) bits[w0 + i] |= lbits[i];
+      __syncthreads();
+    }
+    if (tid == 0) lr.state[r].tau = tau;
+    return;
+  }
+  // Bracket missed (or too many ties for the candidate list): exact select
+  // over the whole row, then every bitmask word rewritten.
+  const uint32_t tau = radix_select<NT, true>(
+      [&](auto f) {
+        for (int32_t t0 = 0; t0 < lr.L; t0 += 8 * NT) {
+          float v[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = row[min(t0 + tid + j * NT, lr.L - 1)];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int32_t t = t0 + tid + j * NT;
+            if (t < lr.L) f(t < lr.sinks ? order_key(1e38f) : order_key(v[j]));
+          }
+        }
+      },
+      keep, sh);
+  const int32_t nw64 = (lr.L + 63) / 64;
+  for (int32_t w = tid >> 6; w < nw64; w += NT / 64) {
+    const int32_t t = w * 64 + lane;
+    const bool e = t < lr.L && t >= lr.sinks && token_key(row, min(t, lr.L - 1), lr.sinks) < tau;
+    const uint64_t b = __ballot(e);
+    if (lane == 0) {
+      bits[2 * w] = (uint32_t)b;
+      bits[2 * w + 1] = (uint32_t)(b >> 32);
+    }
+  }
+  if (tid == 0) lr.state[r].tau = tau;
+}
+
+// K4: zero the evicted rows of logical blocks [lb_begin, lb_end) of row
+// (seq n, head h), then vote for the fully evicted ones (after this
+// workgroup's own zeroing, so the H-th vote, the unlink, follows every
+// head's reads of the block-table entry).
+__global__ __launch_bounds__(256) void evict_apply_kernel(const LongRows lr, int32_t *__restrict__ block_tables,
+                                                          int32_t *__restrict__ is_block_free, int32_t M,
+                                                          int64_t total_pool_blocks, RowZero z) {
+  constexpr int NT = 256, NW = NT / 64;
+  const int32_t r = blockIdx.x, n = r / lr.H, h = r % lr.H, tid = threadIdx.x, lane = tid & 63;
+  const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t *evbits = lr.bits + (int64_t)r * lr.words;
+  const int32_t *bt = block_tables + (int64_t)n * M;
+  const int32_t nlb = min((lr.L + z.bs - 1) / z.bs, M);
+  const int32_t per = (nlb + kApplySplit - 1) / kApplySplit;
+  const int32_t lb_begin = blockIdx.y * per, lb_end = min(nlb, lb_begin + per);
+  auto ev = [&](int32_t t) { return (evbits[t >> 5] >> (t & 31)) & 1u; };
+  if (lb_begin < lb_end) {
+    if (z.kv_format == MEMOPT_KV_INT4) {
+      const Int4Page f(z.D);
+      if (f.G <= 16 && (reinterpret_cast<uintptr_t>(z.k) & 15) == 0) {
+        zero_int4_scale_lines<NW>((uint8_t *)z.k, f, z.H, h, bt, evbits, lb_begin, lb_end, total_pool_blocks, wave,
+                                  lane, pages_aliased(z));
+      } else {
+        const int32_t p = lane >> 3;
+        for (int32_t lb = lb_begin + wave; lb < lb_end; lb += NW) {
+          const uint32_t m16 = (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu;
+          const int32_t phys = bt[lb];
+          if (m16 == 0 || phys < 0 || phys >= total_pool_blocks) continue;  // wave-uniform
+          zero_int4_block((uint8_t *)z.k + ((int64_t)phys * z.H + h) * f.block, z.D, lane, (m16 >> p) & 1,
+                          (m16 >> (p + 8)) & 1);
+        }
+      }
+    } else {
+      const int32_t t_end = min(lr.L, lb_end * z.bs);
+      for (int32_t t0 = lb_begin * z.bs + wave * 64; t0 < t_end; t0 += NW * 64) {
+        const int32_t t = t0 + lane, lb = t / z.bs;
+        bool e = t < t_end && ev(t);
+        int32_t phys = -1;
+        if (e) {
+          phys = bt[lb];
+          e = phys >= 0 && phys < total_pool_blocks;
+        }
+        uint64_t mask = __ballot(e);
+        while (mask) {  // the wave zeroes each evicted row, 16 bytes per lane
+          const int j = __builtin_ctzll(mask);
+          mask &= mask - 1;
+          const int32_t tj = t0 + j, pj = __shfl(phys, j, 64), lbj = tj / z.bs;
+          const int64_t off = (((int64_t)pj * z.bs + (tj - lbj * z.bs)) * z.H + h) * (int64_t)z.D;
+          half_t *kr = (half_t *)z.k + off, *vr = (half_t *)z.v + off;
+          if ((z.D & 7) == 0) {
+            const uint4 zero = {0u, 0u, 0u, 0u};
+            for (int d = 8 * lane; d < z.D; d += 512) {
+              *reinterpret_cast<uint4 *>(kr + d) = zero;
+              *reinterpret_cast<uint4 *>(vr + d) = zero;
+            }
+          } else {
+            for (int d = lane; d < z.D; d += 64) {
+              kr[d] = (half_t)0.0f;
+              vr[d] = (half_t)0.0f;
+            }
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int32_t full_end = min(lb_end, min(lr.L / z.bs, M));
+  for (int32_t lb = lb_begin + tid; lb < full_end; lb += NT) {
+    bool all = true;
+    for (int j = 0; j < z.bs && all; ++j) all = ev(lb * z.bs + j);
+    if (!all) continue;
+    const int32_t phys = bt[lb];
+    if (phys < 0 || phys >= total_pool_blocks) continue;
+    const int prev = atomicAdd(&is_block_free[phys], 1);
+    if (prev + 1 == lr.H) block_tables[(int64_t)n * M + lb] = -1;
+  }
+}
+
+// evict_cache, src/csrc/kv_cache.cu:379-483: one workgroup per (block, head)
+// and any block_size up to kEvictCacheMaxBs (the scores of a block live in
+// LDS). The reference selects keep = max(1, (int)(r * bs)) times the largest
+// remaining score above -1e38 and evicts scores below the last one selected
+// (-1e38 when fewer than keep scores exceed it). Here: tau is the keep-th
+// largest of the scores above -1e38 when there are at least keep of them,
+// else -1e38, and position i is evicted when s_i < tau, i.e. when at least
+// keep scores above -1e38 exceed s_i (or, in the short case, s_i < -1e38).
+static constexpr int32_t kEvictCacheMaxBs = 8192;
+
+__global__ __launch_bounds__(256) void evict_cache_kernel(const float *__restrict__ scores, int32_t bs, int32_t H,
+                                                          int32_t keep, RowZero z) {
   const int64_t blk = blockIdx.x;
-  const int32_t h = blockIdx.y, i = threadIdx.x;
-  if (i >= bs) return;
-  const float si = scores[(blk * bs + i) * H + h];
-  int greater = 0;
-  for (int j = 0; j < bs; ++j) greater += scores[(blk * bs + j) * H + h] > si ? 1 : 0;
-  // Score below the keep-th largest <=> at least `keep` scores strictly above it.
-  if (greater >= keep) zero_row(z, blk, i, h);
+  const int32_t h = blockIdx.y;
+  extern __shared__ float ssc[];
+  __shared__ int32_t s_valid;
+  if (threadIdx.x == 0) s_valid = 0;
+  __syncthreads();
+  int32_t nv = 0;
+  for (int32_t i = threadIdx.x; i < bs; i += 256) {
+    const float v = scores[(blk * bs + i) * H + h];
+    ssc[i] = v;
+    nv += v > -1e38f ? 1 : 0;
+  }
+  if (nv) atomicAdd(&s_valid, nv);
+  __syncthreads();
+  const bool enough = s_valid >= keep;
+  for (int32_t i = threadIdx.x; i < bs; i += 256) {
+    const float si = ssc[i];
+    bool evict;
+    if (enough) {
+      int32_t greater = 0;
+      for (int32_t j = 0; j < bs; ++j) greater += (ssc[j] > -1e38f && ssc[j] > si) ? 1 : 0;
+      evict = greater >= keep;
+    } else {
+      evict = si < -1e38f;
+    }
+    if (evict) zero_row(z, blk, i, h);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Library-owned device state of evict_tokens (per device): the page marks
+// and alias flag, and the long-row workspace. Allocated on first use and
+// grown when a larger pool or batch needs more; calls on one device must
+// not overlap (they mutate the same pool anyway).
+// ---------------------------------------------------------------------------
+struct EvictScratch {
+  unsigned long long *marks = nullptr;
+  int64_t nmarks = 0;
+  uint32_t *flag = nullptr;
+  uint8_t *ws = nullptr;
+  int64_t ws_bytes = 0;
+  uint32_t epoch = 0;
+};
+
+static constexpr int kEvictMaxDevices = 64;
+static std::mutex g_evict_mu;
+static EvictScratch g_evict[kEvictMaxDevices];
+
+static int evict_scratch(int64_t nmarks, int64_t ws_bytes, EvictScratch *out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kEvictMaxDevices) {
+    (void)hipGetLastError();
+    set_error("evict_tokens: no usable current device");
+    return MEMOPT_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_evict_mu);
+  EvictScratch &es = g_evict[dev];
+  auto fail = [](const char *what, hipError_t e) {
+    (void)hipGetLastError();
+    set_error(std::string("evict_tokens: ") + what + ": " + hipGetErrorString(e));
+    return MEMOPT_ERR_HIP;
+  };
+  if (es.flag == nullptr) {
+    hipError_t e = hipMalloc((void **)&es.flag, 256);
+    if (e != hipSuccess) return fail("hipMalloc(flag)", e);
+    e = hipMemset(es.flag, 0, 256);
+    if (e != hipSuccess) return fail("hipMemset(flag)", e);
+  }
+  if (nmarks > es.nmarks) {
+    if (es.marks) (void)hipFree(es.marks);
+    es.marks = nullptr;
+    es.nmarks = 0;
+    hipError_t e = hipMalloc((void **)&es.marks, nmarks * sizeof(unsigned long long));
+    if (e != hipSuccess) return fail("hipMalloc(marks)", e);
+    e = hipMemset(es.marks, 0, nmarks * sizeof(unsigned long long));  // epoch 0 is never used
+    if (e != hipSuccess) return fail("hipMemset(marks)", e);
+    es.nmarks = nmarks;
+  }
+  if (ws_bytes > es.ws_bytes) {
+    if (es.ws) (void)hipFree(es.ws);
+    es.ws = nullptr;
+    es.ws_bytes = 0;
+    const hipError_t e = hipMalloc((void **)&es.ws, ws_bytes);
+    if (e != hipSuccess) return fail("hipMalloc(workspace)", e);
+    es.ws_bytes = ws_bytes;
+  }
+  if (++es.epoch == 0) es.epoch = 1;
+  *out = es;
+  return MEMOPT_OK;
 }
 
 }  // namespace memopt
@@ -445,30 +953,65 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
   // keep = clamp((int)ceilf(r * L), 1, L), in fp32 as src/csrc/kv_cache.cu:754-755.
   int keep = (int)ceilf(retain_ratio * (float)seq_len);
   keep = keep < 1 ? 1 : (keep > seq_len ? seq_len : keep);
-  RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key, p.value, p.key_scales, p.value_scales};
   const int32_t sinks = num_sink_tokens < 0 ? 0 : (num_sink_tokens > seq_len ? seq_len : num_sink_tokens);
   MEMOPT_REQUIRE(p.kv_format != MEMOPT_KV_INT4 || p.block_size == 16, MEMOPT_ERR_UNSUPPORTED,
                  "evict_tokens: INT4 page pools use 16-token pages");
-  MEMOPT_REQUIRE(seq_len <= kEvictMaxLen, MEMOPT_ERR_UNSUPPORTED,
-                 "evict_tokens: seq_len > " + std::to_string(kEvictMaxLen) + " not supported");
-  const size_t lds = (size_t)((seq_len + 63) / 64 * 2) * sizeof(uint32_t);
-  const size_t lds_cand = lds + kEvictCand * sizeof(uint32_t);  // streamed rows: + the candidate keys
-  const dim3 grid(num_seqs, num_heads);
+  MEMOPT_REQUIRE((int64_t)seq_len + 256 * kClassifySplit < (1LL << 31), MEMOPT_ERR_UNSUPPORTED,
+                 "evict_tokens: seq_len too large");
+  const bool int4 = p.kv_format == MEMOPT_KV_INT4;
+  const bool long_rows = seq_len > kShortRow;
+  const int64_t rows = (int64_t)num_seqs * num_heads;
+  const int32_t words = (seq_len + 63) / 64 * 2;
+  const int64_t ws_bytes =
+      long_rows ? rows * (int64_t)(sizeof(RowState) + words * sizeof(uint32_t) + kRowCand * sizeof(uint2)) : 0;
+  EvictScratch es;
+  int rc = evict_scratch(int4 ? p.num_blocks : 0, ws_bytes, &es);
+  if (rc != MEMOPT_OK) return rc;
+  RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key,     p.value,
+            p.key_scales, p.value_scales, int4 ? es.flag : nullptr, es.epoch};
   hipStream_t st = (hipStream_t)stream;
+  // INT4 pools: pages listed twice in the block tables switch the scale
+  // rewrite to atomics.
+  MarkArgs ma{block_tables, 0, max_blocks_per_seq,
+              (int32_t)std::min<int64_t>((seq_len + 15) / 16, max_blocks_per_seq), total_pool_blocks,
+              es.marks, es.flag, es.epoch};
+  if (int4 && ma.nlb > 0) ma.entries = (int64_t)num_seqs * max_blocks_per_seq;
+  if (!long_rows && ma.entries > 0) {
+    hipLaunchKernelGGL(mark_pages_kernel, dim3((unsigned)((ma.entries + 255) / 256)), dim3(256), 0, st, ma);
+    rc = check_launch("evict_tokens(mark_pages)");
+    if (rc != MEMOPT_OK) return rc;
+  }
+  if (long_rows) {
+    LongRows lr;
+    lr.scores = attention_scores;
+    lr.H = num_heads;
+    lr.L = seq_len;
+    lr.keep = keep;
+    lr.sinks = sinks;
+    lr.words = words;
+    lr.state = reinterpret_cast<RowState *>(es.ws);
+    lr.bits = reinterpret_cast<uint32_t *>(es.ws + rows * sizeof(RowState));
+    lr.cand = reinterpret_cast<uint2 *>(es.ws + rows * (int64_t)(sizeof(RowState) + words * sizeof(uint32_t)));
+    MEMOPT_REQUIRE(rows < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "evict_tokens: too many (seq, head) rows");
+    hipLaunchKernelGGL(evict_bracket_kernel, dim3((unsigned)rows), dim3(512), 0, st, lr, ma);
+    if (seq_len % 4 == 0 && ((uintptr_t)attention_scores & 15) == 0)
+      hipLaunchKernelGGL(evict_classify_kernel<true>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr);
+    else
+      hipLaunchKernelGGL(evict_classify_kernel<false>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr);
+    hipLaunchKernelGGL(evict_resolve_kernel, dim3((unsigned)rows), dim3(1024), 0, st, lr);
+    hipLaunchKernelGGL(evict_apply_kernel, dim3((unsigned)rows, kApplySplit), dim3(256), 0, st, lr, block_tables,
+                       is_block_free, max_blocks_per_seq, total_pool_blocks, z);
+    return check_launch("evict_tokens(long rows)");
+  }
+  const size_t lds = (size_t)words * sizeof(uint32_t);
+  const dim3 grid(num_seqs, num_heads);
   // Rows up to 8192 (32768) tokens keep their keys in registers with 256
-  // (1024) threads; longer rows stream with 1024 threads.
+  // (1024) threads.
   if (seq_len <= 256 * 32)
     hipLaunchKernelGGL((evict_tokens_kernel<256, 32>), grid, dim3(256), lds, st, attention_scores, block_tables,
                        is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
-  else if (seq_len <= 1024 * 32)
-    hipLaunchKernelGGL((evict_tokens_kernel<1024, 32>), grid, dim3(1024), lds, st, attention_scores, block_tables,
-                       is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
-  else if (seq_len % 4 == 0 && ((uintptr_t)attention_scores & 15) == 0)
-    hipLaunchKernelGGL((evict_tokens_kernel<1024, 0, true>), grid, dim3(1024), lds_cand, st, attention_scores,
-                       block_tables, is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep,
-                       sinks, z);
   else
-    hipLaunchKernelGGL((evict_tokens_kernel<1024, 0>), grid, dim3(1024), lds_cand, st, attention_scores, block_tables,
+    hipLaunchKernelGGL((evict_tokens_kernel<1024, 32>), grid, dim3(1024), lds, st, attention_scores, block_tables,
                        is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
   return check_launch("evict_tokens");
 }
@@ -482,13 +1025,17 @@ int memopt_evict_cache(const float *attention_scores, int64_t num_blocks, float 
                  "evict_cache: retain_ratio must be in (0, 1]");
   MEMOPT_REQUIRE(num_blocks <= p.num_blocks, MEMOPT_ERR_INVALID,
                  "evict_cache: attention_scores num_blocks > pool.num_blocks");
-  MEMOPT_REQUIRE(p.block_size <= 64, MEMOPT_ERR_UNSUPPORTED, "evict_cache: block_size > 64 not supported");
+  MEMOPT_REQUIRE(p.block_size <= kEvictCacheMaxBs, MEMOPT_ERR_UNSUPPORTED,
+                 "evict_cache: block_size > " + std::to_string(kEvictCacheMaxBs) + " not supported");
   if (num_blocks == 0) return MEMOPT_OK;
   int keep = (int)(retain_ratio * (float)p.block_size);  // truncation, src/csrc/kv_cache.cu:426
   keep = keep < 1 ? 1 : (keep > p.block_size ? p.block_size : keep);
-  RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key, p.value, p.key_scales, p.value_scales};
-  hipLaunchKernelGGL(evict_cache_kernel, dim3((unsigned)num_blocks, p.num_heads), dim3(64), 0,
-                     (hipStream_t)stream, attention_scores, p.block_size, p.num_heads, keep, z);
+  RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key, p.value, p.key_scales, p.value_scales,
+            nullptr, 0};
+  MEMOPT_REQUIRE(num_blocks < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "evict_cache: too many blocks");
+  hipLaunchKernelGGL(evict_cache_kernel, dim3((unsigned)num_blocks, p.num_heads), dim3(256),
+                     (size_t)p.block_size * sizeof(float), (hipStream_t)stream, attention_scores, p.block_size,
+                     p.num_heads, keep, z);
   return check_launch("evict_cache");
 }
 

@@ -538,14 +538,19 @@ def literal_block_counts(evicted_row: np.ndarray, block_size: int) -> np.ndarray
 
 def evict_cache(key_pool, value_pool, scores, retain_ratio):
     """src/csrc/kv_cache.cu:379-483: per (block, head) keep = max(1,
-    (int)(r * bs)) (truncation, :426), threshold = keep-th largest score
-    (selection :436-447), zero positions with score < threshold. In place."""
+    (int)(r * bs)) (truncation, :426). The reference selects keep times the
+    largest remaining score strictly above -1e38 (:436-447, its sentinel), so
+    the threshold is the keep-th largest of the scores above -1e38, or -1e38
+    itself when fewer than keep scores exceed it; positions with score <
+    threshold are zeroed (:466-480). In place."""
     nb, bs, H = scores.shape
     keep = max(1, min(bs, int(np.float32(retain_ratio) * np.float32(bs))))
+    floor = np.float32(-1e38)
     for b in range(nb):
         for h in range(H):
             row = scores[b, :, h].astype(np.float32)
-            thr = np.sort(row)[::-1][keep - 1]
+            above = row[row > floor]
+            thr = np.sort(above)[::-1][keep - 1] if above.size >= keep else floor
             for pos in np.nonzero(row < thr)[0]:
                 key_pool[b, pos, h, :] = 0
                 value_pool[b, pos, h, :] = 0

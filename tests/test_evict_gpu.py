@@ -22,9 +22,10 @@ def _pool_state(fmt):
 @pytest.mark.parametrize("N,H,L,bs,r,sinks", [
     (2, 4, 100, 16, 0.5, 4), (3, 2, 64, 16, 0.75, 0), (1, 8, 4096, 16, 0.75, 4),
     (2, 2, 8192, 16, 0.3, 4), (2, 3, 50, 8, 0.1, 2), (1, 2, 40, 16, 1.0, 4),
-    # 1024-thread kernels: keys in registers (L <= 32768), then streamed rows
-    # read as float4 (L % 4 == 0) and token by token (L % 4 != 0)
-    (1, 2, 20000, 16, 0.75, 4), (1, 2, 40000, 16, 0.6, 4), (1, 1, 40001, 16, 0.5, 3)])
+    # 1024-thread kernel with keys in registers (L <= 32768), then the split
+    # kernels for long rows (sample bracket, classify, resolve, apply)
+    (1, 2, 20000, 16, 0.75, 4), (1, 2, 40000, 16, 0.6, 4), (1, 1, 40001, 16, 0.5, 3),
+    (2, 3, 65536, 16, 0.75, 4), (1, 2, 33000, 32, 0.9, 0)])
 def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
     if fmt == "int4" and bs != 16:
         pytest.skip("the INT4 page pool uses 16-token pages")
@@ -56,10 +57,10 @@ def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
 
 
 @pytest.mark.parametrize("L", [40000, 40001])
-def test_evict_tokens_streamed_rows_many_ties(L):
-    """Streamed rows whose threshold bin holds far more keys than the LDS
-    candidate buffer (scores take 4 values): the last radix pass streams the
-    row again instead of reading the candidates."""
+def test_evict_tokens_long_rows_many_ties(L):
+    """Long rows whose sample bracket holds far more tokens than the
+    candidate list (scores take 4 values): the resolve kernel falls back to
+    an exact select over the whole row and rewrites the bitmask."""
     rng = np.random.default_rng(L)
     N, H, bs, D, r, sinks = 1, 2, 16, 64, 0.6, 4
     M = (L + bs - 1) // bs
@@ -80,6 +81,75 @@ def test_evict_tokens_streamed_rows_many_ties(L):
     same_bits(after["pages"], before["pages"])
     same_bits(bt_d, bt)
     same_bits(ibf_d, ibf)
+
+
+def _evict_case(fmt, N, H, L, D, r, sinks, scores, bt=None, seed=0, extra_pages=2):
+    """Fill a pool, evict on the GPU and with the oracle from the same state;
+    pages, block tables and votes must agree bit for bit."""
+    rng = np.random.default_rng(seed)
+    bs = 16
+    M = (L + bs - 1) // bs
+    nb = N * M + extra_pages
+    memopt_C.init_pool(nb, bs, H, D, kv_format=fmt)
+    T = nb * bs
+    k = rng.standard_normal((T, H, D)).astype(np.float16)
+    v = rng.standard_normal((T, H, D)).astype(np.float16)
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)),
+                         to_dev(np.arange(T, dtype=np.int32)))
+    if bt is None:
+        bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
+    ibf = np.zeros(nb, np.int32)
+    before = _pool_state(fmt)
+    bt_d, ibf_d = to_dev(bt), to_dev(ibf)
+    memopt_C.evict_tokens(to_dev(scores), bt_d, ibf_d, r, sinks)
+    O.evict_tokens_intended(scores, bt, ibf, r, sinks, before, bs)
+    after = _pool_state(fmt)
+    for key in before:
+        if isinstance(before[key], np.ndarray):
+            same_bits(after[key], before[key])
+    same_bits(bt_d, bt)
+    same_bits(ibf_d, ibf)
+
+
+@pytest.mark.parametrize("order", ["ascending", "descending", "blocks"])
+def test_evict_tokens_long_rows_ordered_scores(order):
+    """Scores that depend on the position (sorted either way, or constant per
+    64-token run): the sample bracket is stratified over the row and the
+    result must not depend on how representative it is."""
+    rng = np.random.default_rng(7)
+    N, H, L = 1, 2, 50000
+    s = np.sort(rng.lognormal(size=(N, H, L)).astype(np.float32), axis=-1)
+    if order == "descending":
+        s = s[:, :, ::-1].copy()
+    elif order == "blocks":
+        s = np.repeat(rng.lognormal(size=(N, H, (L + 63) // 64)).astype(np.float32), 64, axis=-1)[:, :, :L].copy()
+    _evict_case("int4", N, H, L, 64, 0.7, 4, s)
+
+
+def test_evict_tokens_longest_row():
+    """One row of 2^19 tokens (the longest the single-workgroup kernel of an
+    earlier design could not take): split kernels, INT4 pool."""
+    rng = np.random.default_rng(19)
+    L = 1 << 19
+    s = rng.lognormal(size=(1, 1, L)).astype(np.float32)
+    _evict_case("int4", 1, 1, L, 64, 0.75, 4, s, extra_pages=1)
+
+
+@pytest.mark.parametrize("L", [300, 40000])
+def test_evict_tokens_aliased_pages(L):
+    """Two sequences whose block tables share every third physical page
+    (prefix-sharing style): the INT4 scale rewrite switches to atomics, and
+    both sequences' evictions land on the shared pages (their union, as
+    applying the oracle sequence by sequence gives)."""
+    rng = np.random.default_rng(L + 1)
+    N, H, D, bs = 2, 2, 64, 16
+    M = (L + bs - 1) // bs
+    bt = rng.permutation(N * M + 2)[:N * M].reshape(N, M).astype(np.int32)
+    bt[1, ::3] = bt[0, ::3]
+    s = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    _evict_case("int4", N, H, L, D, 0.6, 4, s, bt=bt, seed=L + 1)
+    # the fp16 pool's zero stores need no atomics and give the same union
+    _evict_case("fp16", N, H, L, D, 0.6, 4, s, bt=bt, seed=L + 1)
 
 
 @pytest.mark.parametrize("D", [128, 192, 1088])
@@ -124,16 +194,20 @@ def test_evict_then_free_sweep():
     assert memopt_C.free_evicted_blocks(ibf) == [1] and memopt_C.free_blocks_count() == 5
 
 
-@pytest.mark.parametrize("fmt", ["fp16", "int4"])
-def test_evict_cache_vs_oracle(fmt):
-    rng = np.random.default_rng(5)
-    nb, bs, H, D = 6, 16, 4, 64
+@pytest.mark.parametrize("fmt,bs", [("fp16", 16), ("int4", 16), ("fp16", 128), ("fp16", 256), ("fp16", 8)])
+def test_evict_cache_vs_oracle(fmt, bs):
+    """evict_cache for pages of any size (the reference strides over
+    block_size, src/csrc/kv_cache.cu:409, :454)."""
+    rng = np.random.default_rng(5 + bs)
+    nb, H, D = 6, 4, 64
     memopt_C.init_pool(nb, bs, H, D, kv_format=fmt)
     T = nb * bs
     k = rng.standard_normal((T, H, D)).astype(np.float16)
     memopt_C.write_cache(to_dev(k), to_dev(k), to_dev(np.zeros((1, 1), np.int32)),
                          to_dev(np.arange(T, dtype=np.int32)))
     scores = rng.standard_normal((nb, bs, H)).astype(np.float32)
+    scores[0, : bs // 2, 0] = 0.25                     # ties
+    scores[1, :, 1] = -np.inf                          # nothing above the reference's -1e38 sentinel
     memopt_C.evict_cache(to_dev(np.zeros((1, 1), np.int32)), to_dev(scores), 0.4)
     if fmt == "fp16":
         kp = k.reshape(nb, bs, H, D).copy()

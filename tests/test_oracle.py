@@ -412,6 +412,46 @@ def test_evict_cache_brute_force():
                 assert (kp[b, p, h] == 0).all() == (scores[b, p, h] < tau)
 
 
+def _evict_cache_literal(row, keep):
+    """The reference's selection loop, src/csrc/kv_cache.cu:436-447, step by
+    step in fp32: keep times take the largest remaining score above the
+    running best (starting at the -1e38 sentinel), mark it taken; the last
+    best is the threshold."""
+    s = [np.float32(x) for x in row]
+    thr = np.float32(-1e38)
+    for _ in range(keep):
+        best, best_pos = np.float32(-1e38), -1
+        for pos, x in enumerate(s):
+            if x > best:
+                best, best_pos = x, pos
+        thr = best
+        if best_pos >= 0:
+            s[best_pos] = np.float32(-1e38)
+    return [bool(np.float32(x) < thr) for x in row]
+
+
+@pytest.mark.parametrize("bs,r", [(8, 0.4), (16, 0.75), (128, 0.3), (256, 0.9)])
+def test_evict_cache_matches_reference_selection_loop(bs, r):
+    """oracle.evict_cache against the reference's own selection loop,
+    including ties, -inf and scores at or below the -1e38 sentinel."""
+    rng = np.random.default_rng(bs)
+    nb, H, D = 3, 2, 16
+    scores = rng.standard_normal((nb, bs, H)).astype(np.float32)
+    scores[0, : bs // 2, 0] = 0.5                          # ties
+    scores[1, :, 0] = -np.inf                              # nothing above the sentinel
+    scores[1, :3, 1] = np.float32(-1e38)                   # at the sentinel
+    scores[2, : bs - 1, 1] = np.float32(-2e38)             # fewer than keep above it
+    kp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    vp = kp.copy()
+    O.evict_cache(kp, vp, scores, r)
+    keep = max(1, min(bs, int(np.float32(r) * np.float32(bs))))
+    for b in range(nb):
+        for h in range(H):
+            want = _evict_cache_literal(scores[b, :, h], keep)
+            got = [bool((kp[b, p, h] == 0).all()) for p in range(bs)]
+            assert got == want, (b, h)
+
+
 def test_division_shortcut_matches_ieee_on_fp16_domain():
     """The device quantizer replaces the per-element IEEE division v / scale by
     y = RN(1/scale), q0 = RN(v*y), r = fma(-q0, scale, v), q = fma(r, y, q0)
