@@ -473,7 +473,6 @@ __global__ __launch_bounds__(512) void evict_bracket_kernel(const LongRows lr, c
   for (int64_t e = (int64_t)r * NT + threadIdx.x; e < ma.entries; e += (int64_t)gridDim.x * NT) mark_entry(ma, e);
   const float *row = lr.scores + (int64_t)r * lr.L;
   __shared__ uint32_t skeys[kSample];
-  __shared__ SelectShared<NT> sh;
   {
     float v[PER];
 #pragma unroll

@@ -740,16 +740,21 @@ struct IntC {
 
 // LDS-DMA copy (buffer_load ... lds): lane i's 16 bytes at buffer offset
 // voff + soff land at LDS byte m0v + 16 i. Written as inline assembly so the
-// compiler does not track it: its wait-count pass cannot tell the LDS
-// buffers apart and would wait for the next tiles' copies before every
-// operand read of the current one. Callers wait for completion themselves
-// (s_waitcnt vmcnt before the barrier that publishes a tile).
+// compiler does not track it: with the builtin, its wait-count pass cannot
+// tell the LDS buffers apart (it waits for the next tiles' copies before
+// operand reads of the current one) and the barrier's release fence turns
+// the counted wait below into vmcnt(0). Callers wait for completion
+// themselves (s_waitcnt vmcnt before the barrier that publishes a tile).
+// m0 is an input operand ("{m0}"), so the compiler sets it and knows it is
+// read; nothing is clobbered behind its back. The s_nop is the one wait
+// state the hardware needs between an SALU write of m0 and an LDS DMA that
+// reads it.
 __device__ __forceinline__ void buffer_load_lds16_m0(__amdgpu_buffer_rsrc_t r, uint32_t m0v, uint32_t voff,
                                                      uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
-               : "s"(m0v), "v"(voff), "s"(r), "s"(soff)
-               : "memory", "m0");
+               : "v"(voff), "s"(r), "s"(soff), "{m0}"(m0v)
+               : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_u32(const void *p) {
