@@ -51,3 +51,30 @@ class _LazyExtension:
 
 
 memopt_C = _LazyExtension()
+
+
+def dequant_pages_dev(pages, D):
+    """INT4 page buffer -> fp16 pools (K, V) [nb, 16, H, D] on the GPU; equals
+    oracle.from_int4_pages (checked in tests/test_oracle.py)."""
+    import oracle as O
+    return O.dequant_pages_torch(pages, D)
+
+
+def reference_decode_dev(q, kpool, vpool, bt, ctx, W, sinks):
+    """fp32 attention of one query per (b, h) over sinks U window on the GPU."""
+    B, _, H, D = q.shape
+    bs = kpool.shape[1]
+    out = torch.zeros(B, H, D, device=q.device)
+    for b in range(B):
+        c = int(ctx[b])
+        pages = bt[b, : (c + bs - 1) // bs].long()
+        ok = (pages >= 0).repeat_interleave(bs)[:c]
+        k = kpool[pages.clamp(min=0)].reshape(-1, H, D)[:c].float()
+        v = vpool[pages.clamp(min=0)].reshape(-1, H, D)[:c].float()
+        j = torch.arange(c, device=q.device)
+        vis = ((j >= c - W) | (j < sinks)) & ok
+        k, v = k[vis].permute(1, 0, 2), v[vis].permute(1, 0, 2)     # [H, n, D]
+        s = (k @ q[b, 0].float()[:, :, None]).squeeze(-1) / D ** 0.5  # [H, n]
+        p = torch.softmax(s, dim=-1)
+        out[b] = (p[:, None, :] @ v).squeeze(1)
+    return out.half()[:, None]

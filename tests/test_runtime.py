@@ -76,3 +76,26 @@ def test_policy_snapshot():
     s._lock.release()
     t.join(5)
     assert got == [R.Policy(0.5, True)]
+
+
+def test_threshold_policy_rule():
+    """MemoryScheduler.adjust_policy's rule (src/memopt/scheduler.py:357-369):
+    high -> drop ratio + INT4, low -> full + fp16, dead band -> unchanged."""
+    p = R.ThresholdPolicy(vram_high_threshold=0.85, vram_low_threshold=0.5, drop_retain_ratio=0.75)
+    assert R.read_policy(p) == R.Policy(1.0, False)
+    assert p.adjust_policy(0.7) is False and R.read_policy(p) == R.Policy(1.0, False)   # dead band
+    assert p.adjust_policy(0.85) is True and R.read_policy(p) == R.Policy(0.75, True)   # at the high mark
+    assert p.adjust_policy(0.6) is False and R.read_policy(p) == R.Policy(0.75, True)   # hysteresis
+    assert p.adjust_policy(0.5) is True and R.read_policy(p) == R.Policy(1.0, False)    # at the low mark
+    # config 5's forcing: any allocation crosses a tiny high mark
+    f = R.ThresholdPolicy(vram_high_threshold=1e-9, vram_low_threshold=0.0, drop_retain_ratio=0.75)
+    assert f.adjust_policy(1e-6) and (f.retain_ratio, f.use_int4) == (0.75, True)
+
+
+@pytest.mark.parametrize("kw", [dict(vram_high_threshold=0.0), dict(vram_high_threshold=1.5),
+                                dict(vram_low_threshold=0.9, vram_high_threshold=0.9),
+                                dict(drop_retain_ratio=1.0), dict(drop_retain_ratio=-0.1)])
+def test_threshold_policy_validation(kw):
+    """SchedulerConfig's range checks (src/memopt/scheduler.py:90-106)."""
+    with pytest.raises(ValueError):
+        R.ThresholdPolicy(**kw)

@@ -271,3 +271,74 @@ def test_chunk_call_workspace_is_bounded_by_the_window():
     want = O.paged_attention(q.cpu().numpy(), kd, vd, bt.cpu().numpy(), ctx.cpu().numpy(), S, W, sinks,
                              causal=True)
     assert_close(out, want, what="chunk call at the end of a long context")
+
+
+def test_config5_through_policy_forward():
+    """BASELINE configs[4] at full size through the policy path: 4 x 131072
+    tokens in an fp16 pool drawn from a fragmented FIFO free list; a
+    ThresholdPolicy with MemoryScheduler's rule and a near-zero high mark
+    flips to INT4 + retain 0.75; PolicyForward converts the pool, appends,
+    decodes, and (second step) evicts. Checked: the policy and pool format,
+    both steps' decode outputs against fp32 attention over the pool they
+    read, exactly ceil(0.75 L) rows kept per (sequence, head) with the sinks
+    kept, and a decode over the evicted pool."""
+    from gpu_helpers import dequant_pages_dev, reference_decode_dev
+    R = _runtime()
+    B, H, D, L, sinks, spare = 4, 32, 128, 131072, 4, 4096
+    nb = B * (L // 16) + spare
+    cache = R.PagedKVCache(nb, H, D, 16, kv_format="fp16")
+    got = [memopt_C.allocate_block() for _ in range(nb)]
+    for i in torch.randperm(nb, generator=torch.Generator().manual_seed(5)).tolist():
+        memopt_C.free_block(got[i])
+    seqs = list(range(B))
+    for s in seqs:
+        cache.add_sequence(s)
+    g = torch.Generator(device=dev()).manual_seed(5)
+
+    def kv(T):
+        out = []
+        for _ in range(2):
+            x = torch.randn(B, T, H, D, device=dev(), generator=g)
+            m = torch.rand(B, T, H, D, device=dev(), generator=g) < 0.01
+            out.append(torch.where(m, x * 8, x).half())
+            del x, m
+        return out
+
+    for t0 in range(0, L - 2, 8192):
+        k, v = kv(min(8192, L - 2 - t0))
+        cache.append(seqs, k, v)
+        del k, v
+    assert cache.linked_pages(seqs) == B * (L // 16)
+    policy = R.ThresholdPolicy(vram_high_threshold=1e-9, vram_low_threshold=0.0, drop_retain_ratio=0.75)
+    assert policy.adjust_policy() and (policy.retain_ratio, policy.use_int4) == (0.75, True)
+    pf = R.PolicyForward(cache, policy, window_size=-1, num_sink_tokens=sinks)
+
+    def check_decode(out, b):
+        pages = memopt_C.get_int4_pages()
+        bt = cache.block_tables([b])
+        used = torch.clamp(bt[0].long(), min=0)
+        kp, vp = dequant_pages_dev(pages[used], D)
+        local = torch.where(bt[0] >= 0, torch.arange(bt.shape[1], device=dev(), dtype=torch.int32), -1)[None]
+        want = reference_decode_dev(q[b:b + 1], kp, vp, local, cache.context_lens([b]), cache.length(b), sinks)
+        assert_close(out[b:b + 1], want, what=f"config5 policy b={b}")
+        del kp, vp
+
+    q = torch.randn(B, 1, H, D, device=dev(), generator=g).half()
+    k1, v1 = kv(1)
+    out1 = pf.step(seqs, q, k1, v1)                      # no scores: convert, append, decode
+    assert pf.conversions == 1 and cache.kv_format == "int4" and pf.last_policy == R.Policy(0.75, True)
+    check_decode(out1, 0)
+    k2, v2 = kv(1)
+    scores = torch.exp(torch.randn(B, H, L, device=dev(), generator=g))
+    out2 = pf.step(seqs, q, k2, v2, scores)              # append, decode, evict
+    assert all(cache.length(s) == L for s in seqs)
+    # exactly ceil(0.75 L) rows per (sequence 0, head) survive; sinks survive
+    bt0 = cache.block_tables([0])[0]
+    kpool, _ = dequant_pages_dev(memopt_C.get_int4_pages()[torch.clamp(bt0.long(), min=0)], D)
+    zero_rows = (kpool.reshape(-1, H, D)[:L] == 0).all(dim=-1)
+    zero_rows |= (bt0 < 0).repeat_interleave(16)[:L, None]
+    assert torch.equal(zero_rows.sum(dim=0).cpu(), torch.full((H,), L - int(np.ceil(np.float32(0.75) * L))))
+    assert not zero_rows[:sinks].any()
+    del kpool, zero_rows
+    check_decode(pf.attend(seqs, q), 1)                  # decode over the evicted pool
+    assert out2.shape == (B, 1, H, D) and torch.isfinite(out2).all()
