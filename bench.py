@@ -32,6 +32,8 @@ sys.path.insert(0, os.path.join(ROOT, "memopt-transformer-runtime_amd"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0
+# The decode kernel instance the library launches for D=128 INT4 pages (default shape).
+INT4_DECODE_KERNEL = "decode_int4_pages_kernel<128, 8, 1>"
 
 CFG2 = dict(batch=16, heads=32, head_dim=128, ctx=4096, block=16, outlier_frac=0.005, outlier_mult=10.0, seed=0)
 
@@ -348,7 +350,7 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
     nbytes //= copies  # bytes per step (copies are equal up to unlinked pages)
     ms, _ = time_steps(torch, calls, steps, warmup, pre_sleep_cycles=20_000_000)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"kernel": "decode_int4_pages_kernel<128, 4, 2>", "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
+    return {"kernel": INT4_DECODE_KERNEL, "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
             "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "evict_tokens_ms": round(evict_ms[0], 4), "pages_unlinked": unlinked,
             "page_sets_rotated": copies,
@@ -439,7 +441,7 @@ def bench_long_context_policy(torch, memopt_C, cfg, steps=20, warmup=3):
     nbytes = linked * per_page
     gbs = nbytes / (ms * 1e-3) / 1e9
     evict_ms = time_evict(torch, memopt_C, scores, bt, nb, cfg)
-    return {"kernel": "decode_int4_pages_kernel<128, 4, 2>", "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
+    return {"kernel": INT4_DECODE_KERNEL, "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
             "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
             "evict_tokens_ms": round(evict_ms, 4), "pages_unlinked": B * nbps - linked,
             "policy": {"use_int4": pf.last_policy.use_int4, "retain_ratio": pf.last_policy.retain_ratio},
@@ -511,7 +513,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profile_traffic("decode_int4_config2_pmc.txt"),
-                     "kernel": "decode_int4_pages_kernel<128, 4, 2>", "kernel_ms": round(region_ms, 5)},
+                     "kernel": INT4_DECODE_KERNEL, "kernel_ms": round(region_ms, 5)},
     }
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))

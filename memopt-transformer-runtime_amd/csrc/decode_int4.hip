@@ -60,7 +60,7 @@ struct LaneChunk<128> {
   static constexpr int kWords = 4;
   __device__ __forceinline__ void load(const uint8_t *p) { w = *reinterpret_cast<const uint4 *>(p); }
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kStreamLoad);
     w = make_uint4(v.x, v.y, v.z, v.w);
   }
   __device__ __forceinline__ uint32_t word(int i) const {
@@ -73,7 +73,7 @@ struct LaneChunk<64> {
   static constexpr int kWords = 2;
   __device__ __forceinline__ void load(const uint8_t *p) { w = *reinterpret_cast<const uint2 *>(p); }
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kStreamLoad);
     w = make_uint2(v.x, v.y);
   }
   __device__ __forceinline__ uint32_t word(int i) const { return i == 0 ? w.x : w.y; }
@@ -377,8 +377,8 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
       const __amdgpu_buffer_rsrc_t r = block_rsrc(uniform_ptr(hbase + pg * p.kv_ps));
       bt.kw[u].load(r, koff);
       bt.vw[u].load(r, voff);
-      bt.sk[u] = as_half2(__builtin_amdgcn_raw_buffer_load_b32(r, (int)ksoff, 0, 0));
-      bt.sv[u] = as_half2(__builtin_amdgcn_raw_buffer_load_b32(r, (int)vsoff, 0, 0));
+      bt.sk[u] = as_half2(__builtin_amdgcn_raw_buffer_load_b32(r, (int)ksoff, 0, kStreamLoad));
+      bt.sv[u] = as_half2(__builtin_amdgcn_raw_buffer_load_b32(r, (int)vsoff, 0, kStreamLoad));
     }
   };
   auto consume = [&](const Batch &bt) {
@@ -555,13 +555,16 @@ static int device_cus() {
 }
 
 // Launch shape (waves per workgroup, pages per double-buffered batch). The
-// default (4, 2) measured fastest on MI355X for 16 x 32 heads x 4096 tokens;
-// MEMOPT_DECODE_SHAPE="NW,U" selects another compiled shape for tuning sweeps.
+// default (8, 1) measured fastest on MI355X for 16 x 32 heads x 4096 tokens
+// with streaming loads: 47.6-48.8 us against 49.0-49.7 for (4, 2) and 51-55
+// for shapes with more pages in flight per CU ((4, 4), (8, 2), (8, 4),
+// (16, 2), triple buffering), which lose more to the memory system than
+// they hide; MEMOPT_DECODE_SHAPE="NW,U" selects another compiled shape.
 struct DecodeShape {
   int nw, u;
 };
 static DecodeShape decode_shape() {
-  DecodeShape s = {4, 2};
+  DecodeShape s = {8, 1};
   if (const char *e = std::getenv("MEMOPT_DECODE_SHAPE")) {
     int a = 0, c = 0;
     if (std::sscanf(e, "%d,%d", &a, &c) == 2 &&
