@@ -204,12 +204,16 @@ struct SelectShared {
 // (for keys that mostly share their leading digits). Every thread of the
 // workgroup calls it.
 template <int NT, bool AGG, typename Visit>
-__device__ uint32_t radix_select(Visit visit, uint32_t k, SelectShared<NT> &sh) {
+__device__ uint32_t radix_select(Visit visit, uint32_t k, SelectShared<NT> &sh, uint32_t fixed = 0,
+                                 int fixed_bytes = 0) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  uint32_t prefix = 0, pmask = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
+  // The top fixed_bytes bytes of every visited key equal those of `fixed`:
+  // those passes are skipped.
+  uint32_t pmask = fixed_bytes > 0 ? ~0u << (32 - 8 * fixed_bytes) : 0u;
+  uint32_t prefix = fixed & pmask;
+  for (int shift = 24 - 8 * fixed_bytes; shift >= 0; shift -= 8) {
     for (int i = tid; i < NW * 256; i += NT) (&sh.hist[0][0])[i] = 0;
     __syncthreads();
     visit([&](uint32_t key) {
@@ -438,8 +442,10 @@ __global__ __launch_bounds__(256) void mark_pages_kernel(const MarkArgs a) {
 //     fit), tau = the exact (keep - above)-th largest candidate and the
 //     candidates below it join the bitmask; otherwise (a miss, or heavy
 //     ties) an exact radix select over the whole row and a full bitmask;
-//  K4 kApplySplit workgroups per row: zero the evicted rows of a range of
-//     logical blocks, then vote for that range's fully evicted blocks.
+//  K4 zero the evicted rows and vote for fully evicted blocks: for INT4
+//     pools, workgroups over (sequence, range of logical blocks) covering
+//     all heads of each page (evict_apply_pages_kernel); otherwise
+//     kApplySplit workgroups per row, each over a range of logical blocks.
 // The result is the same exact top-k as the single-workgroup kernel.
 static constexpr int32_t kSampleChunks = 16, kSampleChunk = 512, kSample = kSampleChunks * kSampleChunk;
 static constexpr int32_t kRowCand = 16384;  // candidate slots per row
@@ -688,16 +694,18 @@ __global__ __launch_bounds__(1024) void evict_resolve_kernel(const LongRows lr) 
     if (in_lds)
       for (uint32_t i = tid; i < nc; i += NT) lkeys[i] = cand[i].x;
     __syncthreads();
+    // Candidates lie in [lo, hi]: the bytes lo and hi share are common to all.
+    const int fb = st.lo == st.hi ? 4 : __builtin_clz(st.lo ^ st.hi) / 8;
     const uint32_t tau = in_lds ? radix_select<NT, true>(
                                       [&](auto f) {
                                         for (uint32_t i = tid; i < nc; i += NT) f(lkeys[i]);
                                       },
-                                      keep - st.above, sh)
+                                      keep - st.above, sh, st.lo, fb)
                                 : radix_select<NT, true>(
                                       [&](auto f) {
                                         for (uint32_t i = tid; i < nc; i += NT) f(cand[i].x);
                                       },
-                                      keep - st.above, sh);
+                                      keep - st.above, sh, st.lo, fb);
     // The evicted candidates' bits: OR-ed into an LDS copy of a range of
     // kLdsWords bitmask words, which is then merged into the row's words
     // with coalesced accesses (this workgroup alone owns the row's bitmask
@@ -823,6 +831,89 @@ __global__ __launch_bounds__(256) void evict_apply_kernel(const LongRows lr, int
     if (phys < 0 || phys >= total_pool_blocks) continue;
     const int prev = atomicAdd(&is_block_free[phys], 1);
     if (prev + 1 == lr.H) block_tables[(int64_t)n * M + lb] = -1;
+  }
+}
+
+// K4 for INT4 pools on the scale-line path (G <= 16, 16-byte aligned pool):
+// work items are (logical block, head) pairs of one sequence in page-major
+// order, so the H scale runs of a physical page (one per head, a block
+// apart) are rewritten together instead of one head's runs spread over the
+// whole pool: evicting a quarter of the tokens touches nearly every run, and
+// the rewrite is bound by random accesses to memory rows. Workgroup
+// (n, y) owns logical blocks [y * per, (y + 1) * per) of sequence n for all
+// heads; per * H is about 256 items, one pass of its 4 waves. The votes
+// follow the workgroup's own zeroing; a page's H votes of this sequence all
+// come from this workgroup, and the unlink writes only this sequence's entry.
+__global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows lr, int32_t *__restrict__ block_tables,
+                                                                int32_t *__restrict__ is_block_free, int32_t M,
+                                                                int64_t total_pool_blocks, RowZero z, int32_t nlb,
+                                                                int32_t per) {
+  constexpr int NT = 256, NW = NT / 64, UL = 8;
+  const int32_t n = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int32_t H = lr.H;
+  const uint32_t *bits = lr.bits + (int64_t)n * H * lr.words;  // row (n, h) at h * words
+  const int32_t *bt = block_tables + (int64_t)n * M;
+  const int32_t lb_begin = blockIdx.y * per, lb_end = min(nlb, lb_begin + per);
+  const int32_t items = max(0, lb_end - lb_begin) * H;
+  auto mask16 = [&](int32_t lb, int32_t h) { return (bits[(int64_t)h * lr.words + (lb >> 1)] >> ((lb & 1) * 16)) & 0xFFFFu; };
+  const Int4Page f(z.D);
+  uint8_t *pool = (uint8_t *)z.k;
+  const bool aliased = pages_aliased(z);
+  // Same line rewrite as zero_int4_scale_lines: 4 G lanes per 16-token
+  // block, one 16-byte chunk each, UL steps of 64 / (4 G) blocks in flight.
+  const int32_t lpb = 4 * f.G, bpw = 64 / lpb, jb = lane / lpb, q = lane % lpb;
+  const int32_t gmask = 16 * f.G - 1;
+  for (int32_t i0 = wave * bpw * UL; i0 < items; i0 += NW * bpw * UL) {
+    uint32_t mm[UL];
+    int32_t ph[UL], hh[UL];
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      const int32_t i = i0 + u * bpw + jb;
+      const bool in = jb < bpw && i < items;
+      const int32_t lb = lb_begin + i / H, h = i % H;
+      hh[u] = h;
+      mm[u] = in ? mask16(lb, h) : 0u;
+      ph[u] = in ? bt[lb] : -1;
+    }
+    uint4 v[UL];
+    uint4 *w[UL];
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      if (!(ph[u] >= 0 && ph[u] < total_pool_blocks)) mm[u] = 0;
+      w[u] = reinterpret_cast<uint4 *>(pool + ((int64_t)(mm[u] ? ph[u] : 0) * H + hh[u]) * f.block + f.kscales) + q;
+      if (mm[u] && !aliased) v[u] = *w[u];
+    }
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      if (!mm[u]) continue;
+      uint32_t keepm[4] = {~0u, ~0u, ~0u, ~0u};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {  // half 8 q + k of the run; scale_idx(t, g) = 16 g + 2 (t & 7) + (t >> 3)
+        const int32_t i = (8 * q + k) & gmask;
+        const int32_t t = 8 * (i & 1) + ((i & 15) >> 1);
+        if ((mm[u] >> t) & 1) keepm[k >> 1] &= (k & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+      }
+      if (aliased) {
+        uint32_t *wd = reinterpret_cast<uint32_t *>(w[u]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (keepm[k] != ~0u) atomicAnd(wd + k, keepm[k]);
+      } else {
+        *w[u] = (uint4){v[u].x & keepm[0], v[u].y & keepm[1], v[u].z & keepm[2], v[u].w & keepm[3]};
+      }
+    }
+  }
+  __syncthreads();
+  const int32_t full_end = min(lb_end, min(lr.L / 16, M));
+  const int32_t vitems = max(0, full_end - lb_begin) * H;
+  for (int32_t i = tid; i < vitems; i += NT) {
+    const int32_t lb = lb_begin + i / H, h = i % H;
+    if (mask16(lb, h) != 0xFFFFu) continue;
+    const int32_t phys = bt[lb];
+    if (phys < 0 || phys >= total_pool_blocks) continue;
+    const int prev = atomicAdd(&is_block_free[phys], 1);
+    if (prev + 1 == H) block_tables[(int64_t)n * M + lb] = -1;
   }
 }
 
@@ -998,8 +1089,16 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
     else
       hipLaunchKernelGGL(evict_classify_kernel<false>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr);
     hipLaunchKernelGGL(evict_resolve_kernel, dim3((unsigned)rows), dim3(1024), 0, st, lr);
-    hipLaunchKernelGGL(evict_apply_kernel, dim3((unsigned)rows, kApplySplit), dim3(256), 0, st, lr, block_tables,
-                       is_block_free, max_blocks_per_seq, total_pool_blocks, z);
+    const int32_t nlb = std::min((seq_len + p.block_size - 1) / p.block_size, max_blocks_per_seq);
+    if (int4 && p.head_dim / 64 <= 16 && ((uintptr_t)p.key & 15) == 0) {
+      const int32_t per = std::max(1, 256 / num_heads);
+      hipLaunchKernelGGL(evict_apply_pages_kernel, dim3((unsigned)num_seqs, (unsigned)((nlb + per - 1) / per)),
+                         dim3(256), 0, st, lr, block_tables, is_block_free, max_blocks_per_seq, total_pool_blocks, z,
+                         nlb, per);
+    } else {
+      hipLaunchKernelGGL(evict_apply_kernel, dim3((unsigned)rows, kApplySplit), dim3(256), 0, st, lr, block_tables,
+                         is_block_free, max_blocks_per_seq, total_pool_blocks, z);
+    }
     return check_launch("evict_tokens(long rows)");
   }
   const size_t lds = (size_t)words * sizeof(uint32_t);

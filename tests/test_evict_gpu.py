@@ -152,13 +152,17 @@ def test_evict_tokens_aliased_pages(L):
     _evict_case("fp16", N, H, L, D, 0.6, 4, s, bt=bt, seed=L + 1)
 
 
-@pytest.mark.parametrize("D", [128, 192, 1088])
-def test_evict_tokens_int4_head_dims(D):
+@pytest.mark.parametrize("D,N,H,L", [(128, 2, 3, 300), (192, 2, 3, 300), (1088, 2, 3, 300),
+                                     (128, 1, 3, 40000), (192, 1, 5, 40000), (64, 1, 40, 33000),
+                                     (1088, 1, 1, 33000)])
+def test_evict_tokens_int4_head_dims(D, N, H, L):
     """INT4 zeroing over the scale-line path (G = D / 64 groups: 2 and 3
     give 8 and 5 blocks per wave step) and over the per-token fallback taken
-    when G > 16 (D = 1088)."""
-    rng = np.random.default_rng(D)
-    N, H, L, bs, r, sinks = 2, 3, 300, 16, 0.6, 4
+    when G > 16 (D = 1088), for short rows (one workgroup per row) and long
+    rows (the page-major apply over all heads of a page; 40 heads give 6
+    logical blocks per workgroup, 240 items)."""
+    rng = np.random.default_rng(D + L)
+    bs, r, sinks = 16, 0.6, 4
     M = (L + bs - 1) // bs
     nb = N * M + 2
     memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
@@ -168,7 +172,7 @@ def test_evict_tokens_int4_head_dims(D):
     memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)),
                          to_dev(np.arange(T, dtype=np.int32)))
     scores = rng.lognormal(size=(N, H, L)).astype(np.float32)
-    scores[1, :, 32:48] = 1e-6  # one logical block evicted in every head -> unlinked
+    scores[N - 1, :, 32:48] = 1e-6  # one logical block evicted in every head -> unlinked
     bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
     ibf = np.zeros(nb, np.int32)
     before = _pool_state("int4")
