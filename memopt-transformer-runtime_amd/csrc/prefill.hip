@@ -854,16 +854,23 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   const int32_t vis_lo = causal ? qpos - p.W + 1 : ctx - p.W;
   const int32_t wq_last = min(qw0 + 31, p.Lq - 1);
   const int32_t wpos_lo = ctx - p.Lq + qw0, wpos_hi = ctx - p.Lq + wq_last;
-  // Every (key, query) slot of the tile is visible: no mask needed.
+  // Every (key, query) slot of the tile is visible: no mask needed. The
+  // position part of that test is a range of tile bases fixed per wave, so
+  // each tile pays two compares instead of re-deriving it.
+  const int32_t full_lo = causal ? wpos_hi - p.W + 1 : ctx - p.W;
+  const int32_t full_hi = wq_last != qw0 + 31 ? INT32_MIN : min(kv_lim - TK, causal ? wpos_lo - TK + 1 : INT32_MAX);
   auto tile_full = [&](int32_t tb, int4 fl) {
-    return (fl.x & fl.y & fl.z & fl.w) != 0 && tb + TK <= kv_lim &&
-           (causal ? (tb + TK - 1 <= wpos_lo && tb >= wpos_hi - p.W + 1) : (tb >= ctx - p.W)) &&
-           wq_last == qw0 + 31;
+    return (fl.x & fl.y & fl.z & fl.w) != 0 && tb >= full_lo && tb <= full_hi;
   };
 
   const int32_t *vrow = reinterpret_cast<const int32_t *>(ws + (int64_t)units * L::kBlock) + (int64_t)b * MC;
   const StageMap sm = stage_map(ctx, p.M * p.bs, p.Lq, p.W, p.sinks, causal);
-  auto tile_slot = [&](int32_t it) { return (uint32_t)sm.slot(tile_base(it) / 16); };
+  // Sink tiles sit at slots 4 it; the staged chunks of the window tiles are
+  // one contiguous run, so window tile it sits at slot_w + 4 it (cheaper in
+  // scalar instructions than the general chunk -> slot map, which runs for
+  // every copy and flag load of every tile).
+  const int32_t slot_w = n_tiles > sink_tiles ? sm.slot(4 * t_first) - 4 * sink_tiles : 0;
+  auto tile_slot = [&](int32_t it) { return (uint32_t)(4 * it + (it < sink_tiles ? 0 : slot_w)); };
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(ws + ((int64_t)b * p.H + h) * MC * L::kBlock), (short)0, (int)(MC * CS), 0x00020000);
   uint32_t kvoff, vvoff;
@@ -984,18 +991,17 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   };
   const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
   // exp2 of one S block, packed to fp16 in PV B-operand order; adds the
-  // probabilities to the running sum.
+  // probabilities to the running sum from the packed words themselves (the
+  // same pairs rebuilt from the half8 operands cost 12 conversions a tile).
   auto probs = [&](const float16_t &s, half8_t (&pb)[2], float &ls) __attribute__((always_inline)) {
+    uint32_t w[8];
 #pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2) {
+    for (int i = 0; i < 8; ++i)
+      w[i] = as_u32(half2_t{(half_t)fast_exp2(s[2 * i] * cs), (half_t)fast_exp2(s[2 * i + 1] * cs)});
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const half2_t pp2 = {(half_t)fast_exp2(s[8 * g2 + e] * cs), (half_t)fast_exp2(s[8 * g2 + e + 1] * cs)};
-        ls = __builtin_amdgcn_fdot2(pp2, ones, ls, false);
-        pb[g2][e] = pp2.x;
-        pb[g2][e + 1] = pp2.y;
-      }
-    }
+    for (int i = 0; i < 8; ++i) ls = __builtin_amdgcn_fdot2(as_half2(w[i]), ones, ls, false);
+    pb[0] = __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
+    pb[1] = __builtin_bit_cast(half8_t, make_uint4(w[4], w[5], w[6], w[7]));
   };
   auto qk_block = [&](const uint8_t *kt, int blk, float16_t &acc) __attribute__((always_inline)) {
 #pragma unroll
