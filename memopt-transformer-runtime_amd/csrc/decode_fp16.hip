@@ -7,17 +7,19 @@
 // decode kernel:
 //  * keys advance in 16-token chunks (a page of block_size tokens holds
 //    block_size / 16 of them); one wave streams one chunk of one head per
-//    step: lane l owns token l / 4 of the chunk and dims
-//    [(l % 4) D/4, (l % 4 + 1) D/4), read as D/32 16-byte loads for K and as
-//    many for V;
+//    step. Lane l = 8p + c owns tokens p and p + 8 of the chunk and, of each
+//    128-byte line of a token's row (64 dims), the 16 bytes at 16c: one load
+//    instruction covers 8 whole lines (8 tokens x one line), so the loads
+//    can be streaming (non-temporal) without a line being fetched twice;
 //  * each wave keeps U chunks in flight (double-buffered batches) and a
 //    workgroup of NW waves interleaves the chunks of one (b, h); split-K
 //    partials (m, l, o) are merged by the shared combine kernel;
-//  * q . k is v_dot2_f32_f16 over the lane's dims plus 2 DPP steps across the
-//    token's 4 lanes; the softmax running max is wave-uniform and raised
+//  * q . k is v_dot2_f32_f16 over the lane's dims plus 3 DPP steps across
+//    the token's 8 lanes; the softmax running max is wave-uniform and raised
 //    lazily (only when a score exceeds it by more than 8 in log2 units);
-//  * V is accumulated in fp32 with mixed-precision FMAs; the 16 token lanes
-//    of each dim quarter are summed once at the end.
+//  * V is accumulated in fp32 with mixed-precision FMAs (both tokens of the
+//    lane into the same dims); the 8 token-pair lanes of each dim slice are
+//    summed once at the end.
 #include "attention.hpp"
 
 namespace memopt {
@@ -26,13 +28,13 @@ typedef uint32_t u32x4f_t __attribute__((ext_vector_type(4)));
 
 template <int D, int NW, int U>
 __global__ __launch_bounds__(NW * 64) void decode_fp16_kernel(const DecodeParams p) {
-  constexpr int DPL = D / 4;       // dims per lane
-  constexpr int NLD = DPL / 8;     // 16-byte loads per lane for K (and for V)
-  constexpr int NW2 = DPL / 2;     // half2 words per lane
+  constexpr int NL = D / 64;   // 128-byte lines per token row
+  constexpr int DPL = 8 * NL;  // dims per lane (8 of each line)
+  constexpr int NLD = 2 * NL;  // 16-byte loads per lane for K (and for V): 2 tokens x NL lines
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int32_t b = blockIdx.z, h = blockIdx.y, split = blockIdx.x;
-  const int t = lane >> 2, c = lane & 3;
+  const int pp = lane >> 3, c = lane & 7;
 
   __shared__ float s_acc[NW][D];
   __shared__ float s_ml[NW][2];
@@ -47,16 +49,17 @@ __global__ __launch_bounds__(NW * 64) void decode_fp16_kernel(const DecodeParams
   const int32_t end = (int32_t)((n_vis * (split + 1)) / p.splits);
   const int32_t cpp_shift = __builtin_ctz((uint32_t)(p.bs >> 4));  // chunks per page = 2^shift
 
-  half2_t qh[NW2];
+  // q over the lane's dims: 8 per line, dims 64 n + 8 c .. 64 n + 8 c + 7.
+  half2_t qh[4 * NL];
   {
-    const uint4 *qrow = reinterpret_cast<const uint4 *>(p.q + ((int64_t)b * p.H + h) * D + c * DPL);
+    const half_t *qrow = p.q + ((int64_t)b * p.H + h) * D + 8 * c;
 #pragma unroll
-    for (int k = 0; k < NLD; ++k) {
-      const uint4 u = qrow[k];
-      qh[4 * k + 0] = as_half2(u.x);
-      qh[4 * k + 1] = as_half2(u.y);
-      qh[4 * k + 2] = as_half2(u.z);
-      qh[4 * k + 3] = as_half2(u.w);
+    for (int n = 0; n < NL; ++n) {
+      const uint4 u = *reinterpret_cast<const uint4 *>(qrow + 64 * n);
+      qh[4 * n + 0] = as_half2(u.x);
+      qh[4 * n + 1] = as_half2(u.y);
+      qh[4 * n + 2] = as_half2(u.z);
+      qh[4 * n + 3] = as_half2(u.w);
     }
   }
 
@@ -68,7 +71,9 @@ __global__ __launch_bounds__(NW * 64) void decode_fp16_kernel(const DecodeParams
   const int32_t *btrow = p.bt + (int64_t)b * p.M;
   const uint8_t *kbase = p.kc + (int64_t)h * p.kv_hs;
   const uint8_t *vbase = p.vc + (int64_t)h * p.kv_hs;
-  const uint32_t loff = (uint32_t)(t * p.kv_ts) + (uint32_t)(c * DPL * 2);
+  // load k: token pp + 8 (k / NL), line k % NL
+  const uint32_t loff0 = (uint32_t)(pp * p.kv_ts) + (uint32_t)(16 * c);
+  const uint32_t loff8 = loff0 + (uint32_t)(8 * p.kv_ts);
   const int32_t nb32 = (int32_t)min(p.nb, (int64_t)INT32_MAX);
 
   // Slots past `end` (and unlinked pages) read chunk 0 of page 0 of this
@@ -93,50 +98,67 @@ __global__ __launch_bounds__(NW * 64) void decode_fp16_kernel(const DecodeParams
       const __amdgpu_buffer_rsrc_t rv =
           __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(vbase + off), (short)0, 0x7FFFFFFF, 0x00020000);
 #pragma unroll
-      for (int k = 0; k < NLD; ++k) bt.kw[u][k] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(loff + 16 * k), 0, 0);
+      for (int k = 0; k < NLD; ++k)
+        bt.kw[u][k] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)((k < NL ? loff0 : loff8) + 128 * (k % NL)), 0,
+                                                            kStreamLoad);
 #pragma unroll
-      for (int k = 0; k < NLD; ++k) bt.vw[u][k] = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)(loff + 16 * k), 0, 0);
+      for (int k = 0; k < NLD; ++k)
+        bt.vw[u][k] = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)((k < NL ? loff0 : loff8) + 128 * (k % NL)), 0,
+                                                            kStreamLoad);
     }
   };
   auto consume = [&](Batch &bt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float d = 0.0f;
+      float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-      for (int k = 0; k < NLD; ++k)
+      for (int n = 0; n < NL; ++n)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) d = __builtin_amdgcn_fdot2(as_half2(bt.kw[u][k][j]), qh[4 * k + j], d, false);
-      d += xor1(d);
-      d += xor2(d);
+        for (int j = 0; j < 4; ++j) {
+          d0 = __builtin_amdgcn_fdot2(as_half2(bt.kw[u][n][j]), qh[4 * n + j], d0, false);
+          d1 = __builtin_amdgcn_fdot2(as_half2(bt.kw[u][NL + n][j]), qh[4 * n + j], d1, false);
+        }
+      d0 += xor1(d0);
+      d1 += xor1(d1);
+      d0 += xor2(d0);
+      d1 += xor2(d1);
+      d0 += half_mirror(d0);
+      d1 += half_mirror(d1);
       const int32_t tok0 = bt.lc[u] * 16;
       const bool full = bt.ok[u] && tok0 >= kr.win_lo && tok0 + 16 <= kr.hi;
-      bool vis = full;
+      bool vis0 = full, vis1 = full;
       if (!full) {  // wave-uniform
-        const int32_t tk = tok0 + t;
-        vis = bt.ok[u] && tk < kr.hi && (tk >= kr.win_lo || tk < kr.sink_end);
+        const int32_t t0 = tok0 + pp, t1 = t0 + 8;
+        vis0 = bt.ok[u] && t0 < kr.hi && (t0 >= kr.win_lo || t0 < kr.sink_end);
+        vis1 = bt.ok[u] && t1 < kr.hi && (t1 >= kr.win_lo || t1 < kr.sink_end);
         // A masked token's V may hold any bits: it must not meet p = 0.
 #pragma unroll
-        for (int k = 0; k < NLD; ++k)
-          bt.vw[u][k] = vis ? bt.vw[u][k] : (u32x4f_t){0u, 0u, 0u, 0u};
+        for (int n = 0; n < NL; ++n) {
+          bt.vw[u][n] = vis0 ? bt.vw[u][n] : (u32x4f_t){0u, 0u, 0u, 0u};
+          bt.vw[u][NL + n] = vis1 ? bt.vw[u][NL + n] : (u32x4f_t){0u, 0u, 0u, 0u};
+        }
       }
-      const float s = vis ? d * p.qk_scale_log2 : -INFINITY;
-      if (__any(s > m + 8.0f)) {  // wave-uniform, rare after the first chunks
-        const float mn = fmaxf(m, wave_max(s));
+      const float s0 = vis0 ? d0 * p.qk_scale_log2 : -INFINITY;
+      const float s1 = vis1 ? d1 * p.qk_scale_log2 : -INFINITY;
+      const float smax = fmaxf(s0, s1);
+      if (__any(smax > m + 8.0f)) {  // wave-uniform, rare after the first chunks
+        const float mn = fmaxf(m, wave_max(smax));
         const float alpha = (mn == m) ? 1.0f : fast_exp2(m - mn);
         l *= alpha;
 #pragma unroll
         for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
         m = mn;
       }
-      const float pr = vis ? fast_exp2(s - m) : 0.0f;
-      l += pr;
+      const float p0 = vis0 ? fast_exp2(s0 - m) : 0.0f;
+      const float p1 = vis1 ? fast_exp2(s1 - m) : 0.0f;
+      l += p0 + p1;
 #pragma unroll
-      for (int k = 0; k < NLD; ++k)
+      for (int n = 0; n < NL; ++n)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const half2_t v2 = as_half2(bt.vw[u][k][j]);
-          acc[8 * k + 2 * j] = fmaf(pr, (float)v2.x, acc[8 * k + 2 * j]);
-          acc[8 * k + 2 * j + 1] = fmaf(pr, (float)v2.y, acc[8 * k + 2 * j + 1]);
+          const half2_t v0 = as_half2(bt.vw[u][n][j]), v1 = as_half2(bt.vw[u][NL + n][j]);
+          acc[8 * n + 2 * j] = fmaf(p1, (float)v1.x, fmaf(p0, (float)v0.x, acc[8 * n + 2 * j]));
+          acc[8 * n + 2 * j + 1] = fmaf(p1, (float)v1.y, fmaf(p0, (float)v0.y, acc[8 * n + 2 * j + 1]));
         }
     }
   };
@@ -155,24 +177,21 @@ __global__ __launch_bounds__(NW * 64) void decode_fp16_kernel(const DecodeParams
     base += kStep;
   }
 
-  // Sum the 16 token lanes of each dim quarter (lanes c, c + 4, ..., c + 60):
-  // row_ror 4 and 8 inside each row of 16, then across rows.
-  l += dpp_f32<0x124>(l);
-  l += dpp_f32<0x128>(l);
+  // Sum the 8 token-pair lanes sharing this lane's dims (lanes c, c+8, ...).
+  l += dpp_f32<0x128>(l);  // row_ror:8
   l = xor16_sum(l);
   l = xor32_sum(l);
 #pragma unroll
   for (int i = 0; i < DPL; ++i) {
     float v = acc[i];
-    v += dpp_f32<0x124>(v);
     v += dpp_f32<0x128>(v);
     v = xor16_sum(v);
     v = xor32_sum(v);
     acc[i] = v;
   }
-  if (t == 0) {
+  if (pp == 0) {
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) s_acc[wave][c * DPL + i] = acc[i];
+    for (int i = 0; i < DPL; ++i) s_acc[wave][64 * (i / 8) + 8 * c + (i % 8)] = acc[i];
     if (c == 0) {
       s_ml[wave][0] = m;
       s_ml[wave][1] = l;
