@@ -59,8 +59,9 @@ __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cas
 // Measured on MI355X (16 x 32 heads x 4096 tokens of INT4 pages, 285 MB per
 // step): 53.3 -> 48.8 us. Only for loads whose instruction covers whole
 // 128-byte lines: where several instructions each read part of a line (the
-// fp16 decode's per-lane row slices, the quantizer's fp16 reads), the line
-// was fetched again and those kernels ran 1.15-1.5x slower with the bit.
+// quantizer's fp16 reads, an fp16 decode layout with 16-byte row slices per
+// lane), the line was fetched again and those kernels ran 1.15-1.5x slower
+// with the bit.
 static constexpr int kStreamLoad = 2;
 
 // DPP lane exchange inside quads / rows of 16 (no LDS traffic).
