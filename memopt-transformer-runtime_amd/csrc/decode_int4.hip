@@ -579,7 +579,10 @@ int decode_splits(int32_t batch, int32_t heads, int32_t max_pages_visited) {
   const int64_t units = (int64_t)batch * heads;
   if (units <= 0) return 1;
   const DecodeShape sh = decode_shape();
-  const int64_t target_wgs = 2LL * device_cus();
+  // About 2 workgroups per CU; 3 when the batch has fewer (b, h) units than
+  // CUs (config 5's 128 units: 6 splits measured 1.5 % faster than 4, and
+  // 2, 3 or 8 slower).
+  const int64_t target_wgs = (units < device_cus() ? 3LL : 2LL) * device_cus();
   int64_t s = (target_wgs + units - 1) / units;
   // Keep at least 4 page batches per wave.
   const int64_t cap = max_pages_visited / (4LL * sh.nw * sh.u);
