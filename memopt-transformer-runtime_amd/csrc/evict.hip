@@ -437,6 +437,9 @@ __global__ __launch_bounds__(256) void mark_pages_kernel(const MarkArgs a) {
 //  K2 kClassifySplit workgroups per row: one read of the row sorts each token into
 //     kept (key > hi), evicted (key < lo, straight into the row's bitmask)
 //     or candidate (appended to the row's candidate list with its index);
+//     the same launch marks the block-table entries (alias check, INT4
+//     pools) over its whole grid; only the apply kernel, two launches
+//     later, reads the flag;
 //  K3 one workgroup per row: if the bracket holds the keep-th key (fewer
 //     than keep keys above hi, at least keep at or above lo, the candidates
 //     fit), tau = the exact (keep - above)-th largest candidate and the
@@ -470,13 +473,9 @@ struct LongRows {
 
 // K1: sample bracket. Sample rank of the keep-th key: ks = keep * n / L;
 // the bracket spans ks -+ (4 binomial sigmas + 8) sample ranks.
-// The same launch also marks the block-table entries (alias check, INT4
-// pools), grid-strided; only the apply kernel, three launches later, reads
-// the flag.
-__global__ __launch_bounds__(512) void evict_bracket_kernel(const LongRows lr, const MarkArgs ma) {
+__global__ __launch_bounds__(512) void evict_bracket_kernel(const LongRows lr) {
   constexpr int NT = 512, PER = kSample / NT;
   const int32_t r = blockIdx.x;
-  for (int64_t e = (int64_t)r * NT + threadIdx.x; e < ma.entries; e += (int64_t)gridDim.x * NT) mark_entry(ma, e);
   const float *row = lr.scores + (int64_t)r * lr.L;
   __shared__ uint32_t skeys[kSample];
   {
@@ -579,9 +578,14 @@ __global__ __launch_bounds__(512) void evict_bracket_kernel(const LongRows lr, c
 // one global atomic per workgroup. V4 = false (rows not float4-aligned):
 // the same tokens per lane, read as four scalar loads.
 template <bool V4>
-__global__ __launch_bounds__(512) void evict_classify_kernel(const LongRows lr) {
+__global__ __launch_bounds__(512) void evict_classify_kernel(const LongRows lr, const MarkArgs ma) {
   constexpr int NW = 8, UL = 4, kLdsCand = 4096;
   const int32_t r = blockIdx.x, lane = threadIdx.x & 63;
+  {  // the page marks, spread over the whole grid
+    const int64_t nthr = (int64_t)gridDim.x * gridDim.y * 512;
+    for (int64_t e = ((int64_t)blockIdx.y * gridDim.x + r) * 512 + threadIdx.x; e < ma.entries; e += nthr)
+      mark_entry(ma, e);
+  }
   const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const float *row = lr.scores + (int64_t)r * lr.L;
   const RowState st = lr.state[r];
@@ -688,11 +692,16 @@ __global__ __launch_bounds__(1024) void evict_resolve_kernel(const LongRows lr) 
   const uint32_t keep = (uint32_t)lr.keep;
   if (st.above < keep && st.above + st.ncand >= keep && st.ncand <= (uint32_t)kRowCand) {
     const uint32_t nc = st.ncand;
-    // the candidates' keys are read four times: from LDS when they fit
-    __shared__ uint32_t lkeys[kLdsKeys];
+    // the candidates are read four times for the select and once for the
+    // bitmask: from LDS when they fit
+    __shared__ uint32_t lkeys[kLdsKeys], lpos[kLdsKeys];
     const bool in_lds = nc <= (uint32_t)kLdsKeys;
     if (in_lds)
-      for (uint32_t i = tid; i < nc; i += NT) lkeys[i] = cand[i].x;
+      for (uint32_t i = tid; i < nc; i += NT) {
+        const uint2 c = cand[i];
+        lkeys[i] = c.x;
+        lpos[i] = c.y;
+      }
     __syncthreads();
     // Candidates lie in [lo, hi]: the bytes lo and hi share are common to all.
     const int fb = st.lo == st.hi ? 4 : __builtin_clz(st.lo ^ st.hi) / 8;
@@ -715,7 +724,7 @@ __global__ __launch_bounds__(1024) void evict_resolve_kernel(const LongRows lr) 
       for (int i = tid; i < kLdsWords; i += NT) lbits[i] = 0;
       __syncthreads();
       for (uint32_t i = tid; i < nc; i += NT) {
-        const uint2 c = cand[i];
+        const uint2 c = in_lds ? make_uint2(lkeys[i], lpos[i]) : cand[i];
         const int32_t w = (int32_t)(c.y >> 5) - w0;
         if (c.x < tau && (int32_t)c.y >= lr.sinks && w >= 0 && w < kLdsWords) atomicOr(&lbits[w], 1u << (c.y & 31));
       }
@@ -1083,11 +1092,11 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
     lr.bits = reinterpret_cast<uint32_t *>(es.ws + rows * sizeof(RowState));
     lr.cand = reinterpret_cast<uint2 *>(es.ws + rows * (int64_t)(sizeof(RowState) + words * sizeof(uint32_t)));
     MEMOPT_REQUIRE(rows < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "evict_tokens: too many (seq, head) rows");
-    hipLaunchKernelGGL(evict_bracket_kernel, dim3((unsigned)rows), dim3(512), 0, st, lr, ma);
+    hipLaunchKernelGGL(evict_bracket_kernel, dim3((unsigned)rows), dim3(512), 0, st, lr);
     if (seq_len % 4 == 0 && ((uintptr_t)attention_scores & 15) == 0)
-      hipLaunchKernelGGL(evict_classify_kernel<true>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr);
+      hipLaunchKernelGGL(evict_classify_kernel<true>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr, ma);
     else
-      hipLaunchKernelGGL(evict_classify_kernel<false>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr);
+      hipLaunchKernelGGL(evict_classify_kernel<false>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr, ma);
     hipLaunchKernelGGL(evict_resolve_kernel, dim3((unsigned)rows), dim3(1024), 0, st, lr);
     const int32_t nlb = std::min((seq_len + p.block_size - 1) / p.block_size, max_blocks_per_seq);
     if (int4 && p.head_dim / 64 <= 16 && ((uintptr_t)p.key & 15) == 0) {
