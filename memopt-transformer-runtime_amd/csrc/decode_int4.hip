@@ -3,20 +3,25 @@
 // dynamic_sparse_attention composition; TheRadDani/memopt-transformer-runtime
 // src/csrc/quantization.cu:232-270 and src/csrc/attention.cu:98-339).
 //
-// HBM-bound design for gfx950 (wave64):
-//  * one wave streams one (page, head) block per step: 16 tokens x D/2 bytes
-//    of K codes and of V codes (1 KiB each at D=128) with one 16-byte load per
-//    lane; lane l owns token l/4 and dims [(l%4)*D/4, (l%4+1)*D/4), which lie
-//    inside one 64-dim scale group;
-//  * each wave keeps U pages in flight (loads for U pages are issued before
-//    any of them is consumed) and a workgroup runs NW waves over interleaved
-//    pages of one (b, h), so a CU holds tens of KiB of outstanding reads;
-//  * K nibbles become fp16 (64 + code) with one v_bfi_b32 against the fp16
-//    exponent pattern 0x5400 (the nibble in bits 4-7, after a shift for the
-//    even ones) and feed v_dot2_f32_f16 directly; the constant bias sum
-//    q . (64 + 8) is subtracted once per token, which leaves q . (code - 8);
-//  * V nibbles are unpacked against 0x6400 (1024 + n, bits 0-3) and 0x5400
-//    (64 + n, bits 4-7) without shifts, and the bias is subtracted per pair
+// HBM-bound design for gfx950 (wave64), two kernels:
+//  * decode_int4_pages_kernel reads this build's INT4 page pool: one wave
+//    streams one (page, head) block per step (16 tokens x D/2 bytes of K
+//    codes and of V codes, 1 KiB each at D=128, plus the fp16 scales);
+//    lane l = 8p + c owns tokens p and p + 8 and dims [c*D/8, (c+1)*D/8),
+//    one 16-byte load each for K and V. The loads carry the non-temporal
+//    cache-policy bit: each instruction covers whole 128-byte lines that no
+//    later step reads again;
+//  * decode_int4_kernel reads the reference's token-major codes [nb, bs, H,
+//    D/2] with separate scales: lane l owns token l/4 and dims
+//    [(l%4)*D/4, (l%4+1)*D/4), inside one 64-dim scale group;
+//  * each wave keeps U pages in flight (the next batch's loads are issued
+//    before the current one is consumed) and a workgroup runs NW waves over
+//    interleaved pages of one (b, h);
+//  * K nibbles become fp16 (1024 + code or 64 + code) with one v_bfi_b32
+//    against the fp16 exponent patterns 0x6400 / 0x5400 and feed
+//    v_dot2_f32_f16 directly; the constant bias sum q . (bias) is taken off
+//    once per token, which leaves q . (code - 8);
+//  * V nibbles are unpacked the same way and the bias is subtracted per pair
 //    (exact fp16 code - 8). The row-layout kernel accumulates in fp32; the
 //    page-layout kernel accumulates with v_dot2_f32_f16 over a token pair
 //    against fp16 weights p * (V scale), kept <= 2^15 by raising the softmax
@@ -26,8 +31,8 @@
 //  * the softmax running max is wave-uniform and lazily raised: it is updated
 //    (with a wave max and a rescale of the accumulators) only when some score
 //    exceeds it by more than 8 in log2 units, so the common page costs no
-//    cross-lane reduction; the 4 partial dots of a token are summed with 2 DPP
-//    moves;
+//    cross-lane reduction; the partial dots of a token are summed with DPP
+//    moves (3 over the 8 lanes of a token pair in the page kernel);
 //  * only pages that intersect the sink range or the window are visited,
 //    block-table entries < 0 or >= num_kv_blocks are skipped, and split-K
 //    partials (m, l, o) are merged by a small log-sum-exp combine kernel.
