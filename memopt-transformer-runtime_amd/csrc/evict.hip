@@ -25,9 +25,11 @@ struct IntC {
   static constexpr int value = N;
 };
 
+// Order-preserving uint32 key of a float: negative values have every bit
+// flipped, others the sign bit set.
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
 
 struct RowZero {
@@ -192,15 +194,17 @@ __device__ __forceinline__ void hist_add_agg(uint32_t *hist, uint32_t digit, boo
 template <int NT>
 struct SelectShared {
   uint32_t hist[NT / 64][256];
+  uint32_t tot[256];  // bin totals over the waves (NT >= 512)
   uint32_t prefix, k;
 };
 
 // Key of the k-th largest (1 <= k <= number of keys) of the keys handed out
 // by visit(f), which calls f(key) for every key of the calling thread. Four
 // 8-bit radix passes (MSB first): per-wave LDS histograms of the digit among
-// keys matching the prefix so far; then wave 0 alone sums the waves' bins
-// (4 per lane), forms suffix sums with a wave scan and picks the digit, so
-// a pass costs two workgroup barriers. AGG: histogram through hist_add_agg
+// keys matching the prefix so far; then wave 0 sums the waves' bins (4 per
+// lane; with 8 or more waves, 256 threads form the bin totals first), forms
+// suffix sums with a wave scan and picks the digit, so a pass costs two
+// workgroup barriers (three with the totals). AGG: histogram through hist_add_agg
 // (for keys that mostly share their leading digits). Every thread of the
 // workgroup calls it.
 template <int NT, bool AGG, typename Visit>
@@ -226,14 +230,27 @@ __device__ uint32_t radix_select(Visit visit, uint32_t k, SelectShared<NT> &sh, 
       }
     });
     __syncthreads();
+    if constexpr (NW >= 8) {  // the bin totals by 256 threads, not by wave 0 alone
+      if (tid < 256) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += sh.hist[w][tid];
+        sh.tot[tid] = v;
+      }
+      __syncthreads();
+    }
     if (wave == 0) {
       // lane owns bins 4 lane .. 4 lane + 3
       uint32_t c[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         uint32_t v = 0;
+        if constexpr (NW >= 8) {
+          v = sh.tot[4 * lane + j];
+        } else {
 #pragma unroll
-        for (int w = 0; w < NW; ++w) v += sh.hist[w][4 * lane + j];
+          for (int w = 0; w < NW; ++w) v += sh.hist[w][4 * lane + j];
+        }
         c[j] = v;
       }
       const uint32_t tot = c[0] + c[1] + c[2] + c[3];
@@ -412,6 +429,23 @@ struct MarkArgs {
   uint32_t epoch;
 };
 
+// mark_entry in three steps, so that its two dependent memory round trips
+// overlap other work: the page of entry e (or -1) ...
+__device__ __forceinline__ int32_t mark_page(const MarkArgs &a, int64_t e) {
+  if (e >= a.entries || (int32_t)(e % a.M) >= a.nlb) return -1;
+  const int32_t phys = a.bt[e];
+  return phys >= 0 && phys < a.total_pool_blocks ? phys : -1;
+}
+// ... the exchange (its result, only read by mark_check and only where
+// phys >= 0, is left unset elsewhere, so that nothing waits for it) ...
+__device__ __forceinline__ void mark_swap(const MarkArgs &a, int64_t e, int32_t phys, unsigned long long &old) {
+  if (phys >= 0) old = atomicExch(&a.marks[phys], ((unsigned long long)a.epoch << 32) | (uint32_t)(e + 1));
+}
+// ... and the alias check.
+__device__ __forceinline__ void mark_check(const MarkArgs &a, int32_t phys, unsigned long long old) {
+  if (phys >= 0 && (uint32_t)(old >> 32) == a.epoch) atomicMax(a.flag, a.epoch);
+}
+
 __device__ __forceinline__ void mark_entry(const MarkArgs &a, int64_t e) {
   if ((int32_t)(e % a.M) >= a.nlb) return;
   const int32_t phys = a.bt[e];
@@ -429,95 +463,92 @@ __global__ __launch_bounds__(256) void mark_pages_kernel(const MarkArgs a) {
 // ---------------------------------------------------------------------------
 // Long rows (L > 32768): several workgroups per (seq, head)
 // ---------------------------------------------------------------------------
-// With one workgroup per row, config-5-sized batches ([4, 32, 131072] scores)
-// occupy 128 of the 256 CUs and read each row four times. Long rows instead
-// run four kernels:
-//  K1 one workgroup per row: a bracket [lo, hi] around the keep-th largest
-//     key from a 16 x 512-key sample spread over the row;
-//  K2 kClassifySplit workgroups per row: one read of the row sorts each token into
-//     kept (key > hi), evicted (key < lo, straight into the row's bitmask)
-//     or candidate (appended to the row's candidate list with its index);
-//     the same launch marks the block-table entries (alias check, INT4
-//     pools) over its whole grid; only the apply kernel, two launches
-//     later, reads the flag;
-//  K3 one workgroup per row: if the bracket holds the keep-th key (fewer
-//     than keep keys above hi, at least keep at or above lo, the candidates
-//     fit), tau = the exact (keep - above)-th largest candidate and the
-//     candidates below it join the bitmask; otherwise (a miss, or heavy
-//     ties) an exact radix select over the whole row and a full bitmask;
-//  K4 zero the evicted rows and vote for fully evicted blocks: for INT4
+// A row is cut into spans of kSpan tokens and takes three kernels:
+//  K1 evict_classify_long_kernel, one workgroup per span: it loads a
+//     16 x 512-key sample spread over the row and, once the sample is in,
+//     issues the loads of its whole span (32 float4 per thread, kept in
+//     registers). While those are in flight it computes a bracket [lo, hi]
+//     around the row's keep-th largest key from the sample (every span of
+//     a row derives the same bracket from the same sample). Each token is
+//     then kept (key > hi, counted), evicted (key < lo, a bit of the row's
+//     bitmask) or a candidate ((score, token) appended to its wave's list
+//     in LDS; the lists are copied to the span's list at the end). The
+//     same launch marks the block-table entries (alias check, INT4 pools)
+//     over its whole grid;
+//  K2 evict_resolve_long_kernel, one workgroup per row: when the bracket
+//     holds the keep-th key (fewer than keep keys above hi, at least keep
+//     at or above lo) and the candidates fit in LDS, it gathers the spans'
+//     lists, takes tau = the exact (keep - above)-th largest candidate and
+//     ORs the evicted ones into the bitmask; otherwise (a miss, heavy ties,
+//     too many candidates, a wave list that overflowed) an exact radix
+//     select over the whole row and a full bitmask;
+//  K3 zero the evicted rows and vote for fully evicted blocks: for INT4
 //     pools, workgroups over (sequence, range of logical blocks) covering
 //     all heads of each page (evict_apply_pages_kernel); otherwise
 //     kApplySplit workgroups per row, each over a range of logical blocks.
 // The result is the same exact top-k as the single-workgroup kernel.
+static constexpr int32_t kClsNT = 1024, kClsPer = 16;  // K1 threads per workgroup, float4 loads per thread
+static constexpr int32_t kClsWin = 6;  // K1 loads in flight per thread
+static constexpr int32_t kSpan = kClsNT * kClsPer * 4;  // tokens per K1 workgroup (65536)
 static constexpr int32_t kSampleChunks = 16, kSampleChunk = 512, kSample = kSampleChunks * kSampleChunk;
-static constexpr int32_t kRowCand = 16384;  // candidate slots per row
-static constexpr int32_t kLdsKeys = 8192;   // candidate keys the resolve kernel stages in LDS
-static constexpr int32_t kLdsWords = 4096;  // bitmask words the resolve kernel merges per LDS round
-static constexpr int32_t kApplySplit = 32;  // apply workgroups per row
-static constexpr int32_t kClassifySplit = 8;   // classify workgroups per row
-
-// Per-row state in the long-row workspace.
-struct RowState {
-  uint32_t lo, hi, above, ncand, tau, pad[3];
-};
+static constexpr int32_t kResNT = 1024;     // K2 threads per workgroup
+static constexpr int32_t kResCand = 8192;   // candidates K2 gathers in LDS
+static constexpr int32_t kLdsWords = 4096;  // bitmask words K2 merges per LDS round
+static constexpr int32_t kApplySplit = 32;  // apply workgroups per row (non-INT4 pools)
+static constexpr int32_t kRep = 16;         // copies of each first-byte bin of the bracket histogram
+static constexpr int32_t kWaveCand = 512;   // candidate list slots per K1 wave
+static constexpr int32_t kSpanCand = kWaveCand * (kClsNT / 64);  // per span (8192)
 
 struct LongRows {
   const float *scores;
   int32_t H, L, keep, sinks;
-  int32_t words;      // bitmask words per row ((L + 63) / 64 * 2)
-  RowState *state;    // [rows]
-  uint32_t *bits;     // [rows][words]
-  uint2 *cand;        // [rows][kRowCand] (key, token)
+  int32_t words;    // bitmask words per row ((L + 63) / 64 * 2)
+  int32_t spans;    // K1 workgroups per row (ceil(L / kSpan))
+  uint4 *slot;      // [rows][spans] (kept count, candidate count | kListLost, lo, hi)
+  uint32_t *bits;   // [rows][words] evicted tokens
+  uint2 *cand;      // [rows][spans][kSpanCand] (score bits, token) candidate lists
+};
+// Set in a slot's candidate count when a wave's list overflowed: the span's
+// list is incomplete, and the resolve selects over the whole row instead.
+static constexpr uint32_t kListLost = 0x80000000u;
+
+struct ClassifyLds {
+  uint32_t skeys[kSample];
+  uint32_t h1[256][kRep];  // first-byte histogram, lane l adds to copy l % kRep
+  uint32_t tot[256];       // its bin totals
+  uint32_t h2[2][256];     // second-byte histograms under the two picked first bytes
+  uint32_t pick[2][2];     // [hi, lo] x (digit, remaining rank)
+  uint32_t above, ncand;
+  uint32_t wcount[kClsNT / 64];
+  uint2 wcand[kClsNT / 64][kWaveCand];  // per-wave candidate lists
 };
 
-// K1: sample bracket. Sample rank of the keep-th key: ks = keep * n / L;
-// the bracket spans ks -+ (4 binomial sigmas + 8) sample ranks.
-__global__ __launch_bounds__(512) void evict_bracket_kernel(const LongRows lr) {
-  constexpr int NT = 512, PER = kSample / NT;
-  const int32_t r = blockIdx.x;
-  const float *row = lr.scores + (int64_t)r * lr.L;
-  __shared__ uint32_t skeys[kSample];
-  {
-    float v[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int32_t i = threadIdx.x + j * NT, c = i / kSampleChunk;
-      const int32_t t = (int32_t)((int64_t)c * (lr.L - kSampleChunk) / (kSampleChunks - 1)) + i % kSampleChunk;
-      v[j] = row[t];
-    }
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int32_t i = threadIdx.x + j * NT, c = i / kSampleChunk;
-      const int32_t t = (int32_t)((int64_t)c * (lr.L - kSampleChunk) / (kSampleChunks - 1)) + i % kSampleChunk;
-      skeys[i] = t < lr.sinks ? order_key(1e38f) : order_key(v[j]);
-    }
-  }
-  __syncthreads();
+// Bracket of the keep-th largest key from the sample keys in sm.skeys:
+// sample rank ks = keep * kSample / L, the bracket spans ks -+ (4 binomial
+// sigmas + 8) sample ranks. The bounds only need to bracket tau, so 16 bits
+// of each suffice: the bin (top 16 bits) holding the sample key of rank
+// r_hi, resp. r_lo, found with one histogram of the first byte for both
+// ranks and one of the second byte per rank; hi = the top of its bin, lo =
+// the bottom of its. Scores share few leading bytes (a first-byte bin can
+// hold most of a wave's keys, and same-address LDS atomics serialize), so
+// each first-byte bin has kRep copies, lane l adding to copy l % kRep.
+// Returns (lo, hi) to every thread. sm.h1 and sm.h2 must be zero and
+// sm.skeys complete (after a barrier) on entry; ends with a barrier.
+template <int NT>
+__device__ __forceinline__ uint2 sample_bracket(const LongRows &lr, ClassifyLds &sm) {
+  constexpr int PER = kSample / NT;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float ks = (float)lr.keep * (float)kSample / (float)lr.L;
   const float margin = 4.0f * sqrtf(fmaxf(ks * (1.0f - ks / (float)kSample), 0.0f)) + 8.0f;
   const int32_t r_hi = (int32_t)floorf(ks - margin), r_lo = (int32_t)ceilf(ks + margin);
-  // The bounds only need to bracket tau, so 16 bits of each suffice: the
-  // bin (top 16 bits) holding the sample key of rank r_hi, resp. r_lo, found
-  // with one histogram of the first byte for both ranks and one of the
-  // second byte per rank; hi = the top of its bin, lo = the bottom of its.
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  __shared__ uint32_t h2[2][NW][256];
-  __shared__ uint32_t s_pick[2][2];  // [hi, lo] x (digit, remaining rank)
   const int32_t want[2] = {r_hi, r_lo};
-  auto pick = [&](uint32_t (*hist)[256], int which, uint32_t k) {
-    // wave 0: the digit holding the k-th largest key and the rank left in it
+  // wave 0: the digit holding the k-th largest key of hist[256] and the rank left in it
+  auto pick = [&](const uint32_t *hist, int which, uint32_t k) {
     if (wave == 0) {
       uint32_t c[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t v = 0;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) v += hist[w][4 * lane + j];
-        c[j] = v;
-      }
+      for (int j = 0; j < 4; ++j) c[j] = hist[4 * lane + j];
       const uint32_t tot = c[0] + c[1] + c[2] + c[3];
       uint32_t inc = tot;
 #pragma unroll
@@ -530,242 +561,361 @@ __global__ __launch_bounds__(512) void evict_bracket_kernel(const LongRows lr) {
       for (int j = 3; j >= 0; --j) {
         const uint32_t upto = above + c[j];
         if (upto >= k && above < k) {
-          s_pick[which][0] = 4 * lane + j;
-          s_pick[which][1] = k - above;
+          sm.pick[which][0] = 4 * lane + j;
+          sm.pick[which][1] = k - above;
         }
         above = upto;
       }
     }
   };
-  for (int i = threadIdx.x; i < 2 * NW * 256; i += NT) (&h2[0][0][0])[i] = 0;
-  __syncthreads();
 #pragma unroll
-  for (int j = 0; j < PER; ++j) hist_add_agg(h2[0][wave], skeys[threadIdx.x + j * NT] >> 24, true);
+  for (int j = 0; j < PER; ++j) atomicAdd(&sm.h1[sm.skeys[tid + j * NT] >> 24][lane % kRep], 1u);
+  __syncthreads();
+  if (tid < 256) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int i = 0; i < kRep; ++i) t += sm.h1[tid][(i + tid) % kRep];
+    sm.tot[tid] = t;
+  }
   __syncthreads();
   for (int which = 0; which < 2; ++which)
-    if (want[which] >= 1 && want[which] <= kSample) pick(h2[0], which, (uint32_t)want[which]);
+    if (want[which] >= 1 && want[which] <= kSample) pick(sm.tot, which, (uint32_t)want[which]);
   __syncthreads();
-  const uint32_t d1[2] = {s_pick[0][0], s_pick[1][0]};
-  const uint32_t k1[2] = {s_pick[0][1], s_pick[1][1]};
-  for (int i = threadIdx.x; i < 2 * NW * 256; i += NT) (&h2[0][0][0])[i] = 0;
-  __syncthreads();
+  const uint32_t d1[2] = {sm.pick[0][0], sm.pick[1][0]};
+  const uint32_t k1[2] = {sm.pick[0][1], sm.pick[1][1]};
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const uint32_t key = skeys[threadIdx.x + j * NT];
+    const uint32_t key = sm.skeys[tid + j * NT];
 #pragma unroll
-    for (int which = 0; which < 2; ++which) hist_add_agg(h2[which][wave], (key >> 16) & 0xFF, (key >> 24) == d1[which]);
+    for (int which = 0; which < 2; ++which)
+      if ((key >> 24) == d1[which]) atomicAdd(&sm.h2[which][(key >> 16) & 0xFF], 1u);
   }
   __syncthreads();
   for (int which = 0; which < 2; ++which)
-    if (want[which] >= 1 && want[which] <= kSample) pick(h2[which], which, k1[which]);
+    if (want[which] >= 1 && want[which] <= kSample) pick(sm.h2[which], which, k1[which]);
   __syncthreads();
-  const uint32_t hi = r_hi < 1 ? 0xFFFFFFFFu : (((d1[0] << 8) | s_pick[0][0]) << 16) | 0xFFFFu;
-  const uint32_t lo = r_lo > kSample ? 0u : ((d1[1] << 8) | s_pick[1][0]) << 16;
-  if (threadIdx.x == 0) {
-    RowState st = {};
-    st.lo = lo;
-    st.hi = hi;
-    lr.state[r] = st;
-  }
+  const uint32_t hi = r_hi < 1 ? 0xFFFFFFFFu : (((d1[0] << 8) | sm.pick[0][0]) << 16) | 0xFFFFu;
+  const uint32_t lo = r_lo > kSample ? 0u : ((d1[1] << 8) | sm.pick[1][0]) << 16;
+  return make_uint2(lo, hi);
 }
 
-// K2: classify. Workgroup (r, s) covers 256-token units [s*w, (s+1)*w) of
-// row r (the row base is 16-byte aligned and L % 4 == 0 on this path); a
-// wave reads a unit as one float4 per lane (lane l holds tokens 4l .. 4l+3),
-// UL units' loads in flight. Evicted bits: a lane's 4 bits form a nibble,
-// the 8 nibbles of lanes 8w .. 8w+7 are OR-ed into bitmask word w with 3 DPP
-// steps. Candidates go to an LDS list first and reach the row's list with
-// one global atomic per workgroup. V4 = false (rows not float4-aligned):
-// the same tokens per lane, read as four scalar loads.
+// K1, workgroup (r, s): span s of row r. The sample is loaded and the
+// bracket computed first; then the span's loads are issued (all of them:
+// a wave stalls at issue once the memory pipeline is full, so loads
+// issued before the bracket would hold it back) and each float4 is
+// classified as it arrives. V4: the row base is 16-byte aligned and
+// L % 4 == 0, so a lane's 4 tokens are one float4; otherwise four scalar
+// loads. Lane l of wave w holds tokens t_span + 4096 j + 256 w + 4 l .. + 3
+// for j < kClsPer; bitmask word t / 32 gets the nibbles of lanes 8g .. 8g
+// + 7, OR-ed together by 3 DPP steps.
 template <bool V4>
-__global__ __launch_bounds__(512) void evict_classify_kernel(const LongRows lr, const MarkArgs ma) {
-  constexpr int NW = 8, UL = 4, kLdsCand = 4096;
-  const int32_t r = blockIdx.x, lane = threadIdx.x & 63;
-  {  // the page marks, spread over the whole grid
-    const int64_t nthr = (int64_t)gridDim.x * gridDim.y * 512;
-    for (int64_t e = ((int64_t)blockIdx.y * gridDim.x + r) * 512 + threadIdx.x; e < ma.entries; e += nthr)
-      mark_entry(ma, e);
-  }
-  const int32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const float *row = lr.scores + (int64_t)r * lr.L;
-  const RowState st = lr.state[r];
-  uint32_t *bits = lr.bits + (int64_t)r * lr.words;
-  uint2 *cand = lr.cand + (int64_t)r * kRowCand;
-  __shared__ uint2 lcand[kLdsCand];
-  __shared__ uint32_t s_n, s_above, s_base;
-  if (threadIdx.x == 0) s_n = s_above = 0;
-  __syncthreads();
-  const int32_t nunits = lr.L / 256 + (lr.L % 256 != 0);
-  const int32_t per = (nunits + kClassifySplit - 1) / kClassifySplit;
-  const int32_t u_begin = blockIdx.y * per, u_end = min(nunits, u_begin + per);
-  const uint32_t sink_key = order_key(1e38f);
-  uint32_t above = 0;
-  for (int32_t u0 = u_begin + wave * UL; u0 < u_end; u0 += NW * UL) {
-    float4 v[UL];
+__global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongRows lr, const MarkArgs ma) {
+  constexpr int NT = kClsNT, NW = NT / 64, PER = kClsPer, SPER = kSample / NT;
+  const int32_t r = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int32_t L = lr.L;
+  const float *row = lr.scores + (int64_t)r * L;
+  __shared__ ClassifyLds sm;
+  auto sample_token = [&](int32_t i) {
+    const int32_t c = i / kSampleChunk;
+    return (int32_t)((int64_t)c * (L - kSampleChunk) / (kSampleChunks - 1)) + i % kSampleChunk;
+  };
+  // The sample, and this thread's first page-mark entry: its block-table
+  // load travels with the sample, the exchange is issued among the span's
+  // loads (a barrier would wait for it) and its result is checked at the
+  // end.
+  const int64_t nthr = (int64_t)gridDim.x * gridDim.y * NT;
+  const int64_t e0 = ((int64_t)s * gridDim.x + r) * NT + tid;
+  float sv[SPER];
 #pragma unroll
-    for (int u = 0; u < UL; ++u) {
-      if constexpr (V4) {
-        v[u] = *reinterpret_cast<const float4 *>(row + min((u0 + u) * 256 + 4 * lane, lr.L - 4));
-      } else {
-        const int32_t t = (u0 + u) * 256 + 4 * lane;
-        v[u] = make_float4(row[min(t, lr.L - 1)], row[min(t + 1, lr.L - 1)], row[min(t + 2, lr.L - 1)],
-                           row[min(t + 3, lr.L - 1)]);
+  for (int j = 0; j < SPER; ++j) sv[j] = row[sample_token(tid + j * NT)];
+  const int32_t mphys = mark_page(ma, e0);
+  const uint32_t sink_key = order_key(1e38f);
+#pragma unroll
+  for (int j = 0; j < SPER; ++j) {
+    const int32_t i = tid + j * NT;
+    sm.skeys[i] = sample_token(i) < lr.sinks ? sink_key : order_key(sv[j]);
+  }
+  // The span is read through a window of kClsWin loads per thread: the
+  // first ones fly during the bracket, and each later one is issued as a
+  // float4 is classified, so the data of all waves arrives interleaved with
+  // the classification instead of one wave's whole share after another's.
+  const int32_t t_span = s * kSpan;
+  auto load4 = [&](int j) __attribute__((always_inline)) {
+    const int32_t t = t_span + 4 * (j * NT + tid);
+    const float *p4 = row + min(t, L - 4);
+    if constexpr (V4) {
+      return *reinterpret_cast<const float4 *>(p4);
+    } else {
+      return make_float4(p4[0], p4[1], p4[2], p4[3]);
+    }
+  };
+  float4 v[kClsWin];
+#pragma unroll
+  for (int j = 0; j < kClsWin; ++j) v[j] = load4(j);
+  for (int i = tid; i < 256 * kRep; i += NT) (&sm.h1[0][0])[i] = 0;
+  for (int i = tid; i < 2 * 256; i += NT) (&sm.h2[0][0])[i] = 0;
+  if (tid == 0) sm.above = sm.ncand = 0;
+  __syncthreads();
+  const uint2 br = sample_bracket<NT>(lr, sm);
+  const uint32_t lo = br.x, hi = br.y;
+  uint32_t *bits = lr.bits + (int64_t)r * lr.words;
+  // Sink tokens count with the key of a 1e38 score and are never evicted.
+  const uint32_t sink_gt = sink_key > hi ? 0xFu : 0u, sink_in = sink_key >= lo && sink_key <= hi ? 0xFu : 0u;
+  // The scores are compared with the floats whose keys are lo and hi: x <
+  // flo implies key(x) < lo and x > fhi implies key(x) > hi, and a token
+  // the float compare cannot place (a NaN, -0 against a +0 bound, a NaN
+  // bound) becomes a candidate, which the resolve places exactly.
+  const float flo = __builtin_bit_cast(float, (lo & 0x80000000u) ? lo ^ 0x80000000u : ~lo);
+  const float fhi = __builtin_bit_cast(float, (hi & 0x80000000u) ? hi ^ 0x80000000u : ~hi);
+  const uint32_t sink_bits = __builtin_bit_cast(uint32_t, 1e38f);
+  uint32_t above = 0, ncand = 0;
+  unsigned long long mold;  // set by mark_swap where mphys >= 0
+  uint32_t wcnt = 0;     // this wave's list length (wave-uniform)
+  bool wlost = false;    // the wave's list overflowed (wave-uniform)
+  // One float4 of the span: plain = the wave's 256 tokens of this step are
+  // all inside the row and past the sinks (every step but the row's first
+  // and last), which drops the per-token masks.
+  auto step = [&](const float4 &v4, int32_t t0, int32_t word, auto plain) __attribute__((always_inline)) {
+    float x[4] = {v4.x, v4.y, v4.z, v4.w};
+    uint32_t in_row = 0xFu, sinkm = 0u;
+    if constexpr (!plain.value) {
+      // nibble masks of the lane's 4 tokens: inside the row, and sinks
+      in_row = 0xFu >> (4 - min(4, max(0, L - t0)));
+      sinkm = 0xFu >> (4 - min(4, max(0, lr.sinks - t0)));
+      if constexpr (!V4) {
+        // the slot holding the row's last token was loaded from L - 4:
+        // shift it down by d so that x[k] is token t0 + k again (k + d <= 3
+        // for every token of the row)
+        const int32_t d = min(3, max(0, t0 - (L - 4)));
+        if (d >= 1) x[0] = x[1], x[1] = x[2], x[2] = x[3];
+        if (d >= 2) x[0] = x[1], x[1] = x[2];
+        if (d >= 3) x[0] = x[1];
       }
     }
+    uint32_t lt = 0, gt = 0, raw[4];
 #pragma unroll
-    for (int u = 0; u < UL; ++u) {
-      const int32_t unit = u0 + u;
-      if (unit >= u_end) break;  // wave-uniform
-      const int32_t t0 = unit * 256 + 4 * lane;
-      const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-      uint32_t nib = 0, ncand = 0;
-      uint32_t ck[4];
+    for (int k = 0; k < 4; ++k) {
+      raw[k] = __builtin_bit_cast(uint32_t, x[k]);
+      lt |= x[k] < flo ? 1u << k : 0u;
+      gt |= x[k] > fhi ? 1u << k : 0u;
+    }
+    uint32_t cand = ~(lt | gt) & 0xFu, nib = lt;
+    if constexpr (!plain.value) {
+      gt = ((gt & ~sinkm) | (sink_gt & sinkm)) & in_row;
+      cand = ((cand & ~sinkm) | (sink_in & sinkm)) & in_row;
+      nib = lt & ~sinkm & in_row;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int32_t t = t0 + j;
-        const bool valid = t < lr.L;
-        const uint32_t key = t < lr.sinks ? sink_key : order_key(x[j]);
-        ck[j] = key;
-        nib |= (uint32_t)(valid && t >= lr.sinks && key < st.lo) << j;
-        above += (uint32_t)(valid && key > st.hi);
-        ncand += (uint32_t)(valid && key >= st.lo && key <= st.hi);
+      for (int k = 0; k < 4; ++k) raw[k] = (sinkm >> k) & 1 ? sink_bits : raw[k];
+    }
+    above += __builtin_popcount(gt);
+    const uint32_t nc = __builtin_popcount(cand);
+    ncand += nc;
+    {  // append the candidates (score bits, token) to the wave's list:
+       // offsets from a wave prefix of the lanes' counts (0..4, three bit
+       // planes)
+      uint32_t pre = 0, tot = 0;
+#pragma unroll
+      for (int b = 0; b < 3; ++b) {
+        const uint64_t bb = __ballot((nc >> b) & 1);
+        pre += __builtin_amdgcn_mbcnt_hi((uint32_t)(bb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bb, 0u)) << b;
+        tot += (uint32_t)__popcll(bb) << b;
       }
-      // bitmask word 8 unit + lane / 8: nibbles of the lane's group of 8
-      uint32_t w = nib << (4 * (lane & 7));
-      w |= __builtin_bit_cast(uint32_t, dpp_f32<0xB1>(__builtin_bit_cast(float, w)));   // quad_perm [1,0,3,2]
-      w |= __builtin_bit_cast(uint32_t, dpp_f32<0x4E>(__builtin_bit_cast(float, w)));   // quad_perm [2,3,0,1]
-      w |= __builtin_bit_cast(uint32_t, dpp_f32<0x141>(__builtin_bit_cast(float, w)));  // row_half_mirror
-      if ((lane & 7) == 0 && unit * 8 + (lane >> 3) < lr.words) bits[unit * 8 + (lane >> 3)] = w;
-      if (__ballot(ncand != 0)) {  // wave-uniform
-        // exclusive prefix of the lanes' candidate counts (0..4) over the wave
-        uint32_t pre = 0, tot = 0;
+      if (wcnt + tot <= (uint32_t)kWaveCand) {  // wave-uniform
+        uint32_t pos = wcnt + pre;
 #pragma unroll
-        for (int b = 0; b < 3; ++b) {
-          const uint64_t bb = __ballot((ncand >> b) & 1);
-          pre += (uint32_t)__popcll(bb & ((1ull << lane) - 1)) << b;
-          tot += (uint32_t)__popcll(bb) << b;
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t is = (cand >> k) & 1;
+          if (is) sm.wcand[wave][pos] = make_uint2(raw[k], (uint32_t)(t0 + k));
+          pos += is;
         }
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(&s_n, tot);
-        base = __builtin_amdgcn_readfirstlane(base) + pre;
+      } else {
+        wlost = true;
+      }
+      wcnt += tot;
+    }
+    uint32_t e = nib << (4 * (lane & 7));
+    e |= __builtin_bit_cast(uint32_t, dpp_f32<0xB1>(__builtin_bit_cast(float, e)));   // quad_perm [1,0,3,2]
+    e |= __builtin_bit_cast(uint32_t, dpp_f32<0x4E>(__builtin_bit_cast(float, e)));   // quad_perm [2,3,0,1]
+    e |= __builtin_bit_cast(uint32_t, dpp_f32<0x141>(__builtin_bit_cast(float, e)));  // row_half_mirror
+    if ((lane & 7) == 0 && word < lr.words) bits[word] = e;
+  };
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int32_t t = t0 + j;
-          if (t < lr.L && ck[j] >= st.lo && ck[j] <= st.hi) {
-            if (base < (uint32_t)kLdsCand) lcand[base] = make_uint2(ck[j], (uint32_t)t);
-            ++base;
+  for (int j = 0; j < PER; ++j) {
+    const int32_t t0 = t_span + 4 * (j * NT + tid);
+    const int32_t tw = t_span + 4 * j * NT + 256 * wave;  // the wave's first token of this step
+    const int32_t word = (t_span >> 5) + 8 * (j * NW + wave) + (lane >> 3);
+    const float4 cur = v[j % kClsWin];
+    if (j + kClsWin < PER) v[j % kClsWin] = load4(j + kClsWin);
+    if (j == 0) mark_swap(ma, e0, mphys, mold);
+    if (tw >= lr.sinks && tw + 256 <= L)  // wave-uniform
+      step(cur, t0, word, IntC<1>{});
+    else
+      step(cur, t0, word, IntC<0>{});
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    above += __shfl_xor(above, off, 64);
+    ncand += __shfl_xor(ncand, off, 64);
+  }
+  if (lane == 0) {
+    if (above) atomicAdd(&sm.above, above);
+    if (ncand) atomicAdd(&sm.ncand, ncand);
+    sm.wcount[wave] = wlost ? kWaveCand + 1u : wcnt;
+  }
+  // the page marks: this thread's first entry, then any further ones
+  mark_check(ma, mphys, mold);
+  for (int64_t e = e0 + nthr; e < ma.entries; e += nthr) mark_entry(ma, e);
+  __syncthreads();
+  // The wave lists, concatenated into the span's list.
+  uint32_t off = 0, lost = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const uint32_t c = sm.wcount[w];
+    off += w < wave ? c : 0u;
+    lost |= c > (uint32_t)kWaveCand ? kListLost : 0u;
+  }
+  uint2 *gl = lr.cand + ((int64_t)r * lr.spans + s) * kSpanCand;
+  if (!lost)
+    for (uint32_t i = lane; i < wcnt; i += 64) gl[off + i] = sm.wcand[wave][i];
+  if (tid == 0) lr.slot[(int64_t)r * lr.spans + s] = make_uint4(sm.above, sm.ncand | lost, lo, hi);
+}
+
+struct ResolveLds {
+  uint32_t lkey[kResCand], lpos[kResCand];
+  SelectShared<kResNT> sh;
+  uint32_t lbits[kLdsWords];
+  uint32_t above, ncand, lost;
+};
+
+// K2: one workgroup per row.
+__global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRows lr) {
+  constexpr int NT = kResNT, NW = NT / 64;
+  const int32_t r = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int32_t L = lr.L;
+  const float *row = lr.scores + (int64_t)r * L;
+  uint32_t *bits = lr.bits + (int64_t)r * lr.words;
+  const uint4 *slot = lr.slot + (int64_t)r * lr.spans;
+  __shared__ ResolveLds sm;
+  const uint32_t sink_key = order_key(1e38f);
+  if (tid == 0) sm.above = sm.ncand = sm.lost = 0;
+  __syncthreads();
+  {  // the spans' counts
+    uint32_t a = 0, c = 0, l = 0;
+    for (int32_t q = tid; q < lr.spans; q += NT) {
+      const uint4 sl = slot[q];
+      a += sl.x;
+      c += sl.y & ~kListLost;
+      l |= sl.y & kListLost;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      a += __shfl_xor(a, off, 64);
+      c += __shfl_xor(c, off, 64);
+      l |= __shfl_xor(l, off, 64);
+    }
+    if (lane == 0 && (a | c | l)) {
+      atomicAdd(&sm.above, a);
+      atomicAdd(&sm.ncand, c);
+      atomicOr(&sm.lost, l);
+    }
+  }
+  const uint4 s0 = slot[0];  // every span holds the row's bracket
+  const uint32_t lo = s0.z, hi = s0.w;
+  __syncthreads();
+  const uint32_t above = sm.above, nc = sm.ncand, keep = (uint32_t)lr.keep;
+  if (above < keep && above + nc >= keep && nc <= (uint32_t)kResCand && !sm.lost) {
+    // The spans' candidate lists, 8 entries per thread in flight.
+    uint32_t base = 0;
+    for (int32_t q = 0; q < lr.spans; ++q) {
+      const uint32_t cnt = slot[q].y;
+      const uint2 *gl = lr.cand + ((int64_t)r * lr.spans + q) * kSpanCand;
+      for (uint32_t i0 = 0; i0 < cnt; i0 += 8 * NT) {
+        uint2 c[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t i = i0 + k * NT + tid;
+          if (i < cnt) c[k] = gl[i];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t i = i0 + k * NT + tid;
+          if (i < cnt) {
+            sm.lkey[base + i] = order_key(__builtin_bit_cast(float, c[k].x));
+            sm.lpos[base + i] = c[k].y;
           }
         }
       }
+      base += cnt;
     }
-  }
-  // wave totals of the kept count
-  for (int off = 32; off >= 1; off >>= 1) above += __shfl_xor(above, off, 64);
-  if (lane == 0 && above) atomicAdd(&s_above, above);
-  __syncthreads();
-  const uint32_t n = s_n;
-  if (threadIdx.x == 0) {
-    if (s_above) atomicAdd(&lr.state[r].above, s_above);
-    s_base = n ? atomicAdd(&lr.state[r].ncand, n) : 0u;
-  }
-  __syncthreads();
-  if (n > (uint32_t)kLdsCand) {
-    // more candidates than the LDS list holds: mark the row's list as full
-    // (the resolve kernel then selects over the whole row)
-    if (threadIdx.x == 0) atomicAdd(&lr.state[r].ncand, (uint32_t)kRowCand + 1);
-    return;
-  }
-  const uint32_t base = s_base;
-  for (uint32_t i = threadIdx.x; i < n; i += 512)
-    if (base + i < (uint32_t)kRowCand) cand[base + i] = lcand[i];
-}
-
-// K3: resolve tau and finish the bitmask.
-__global__ __launch_bounds__(1024) void evict_resolve_kernel(const LongRows lr) {
-  constexpr int NT = 1024;
-  const int32_t r = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-  const float *row = lr.scores + (int64_t)r * lr.L;
-  __shared__ SelectShared<NT> sh;
-  const RowState st = lr.state[r];
-  uint32_t *bits = lr.bits + (int64_t)r * lr.words;
-  const uint2 *cand = lr.cand + (int64_t)r * kRowCand;
-  const uint32_t keep = (uint32_t)lr.keep;
-  if (st.above < keep && st.above + st.ncand >= keep && st.ncand <= (uint32_t)kRowCand) {
-    const uint32_t nc = st.ncand;
-    // the candidates are read four times for the select and once for the
-    // bitmask: from LDS when they fit
-    __shared__ uint32_t lkeys[kLdsKeys], lpos[kLdsKeys];
-    const bool in_lds = nc <= (uint32_t)kLdsKeys;
-    if (in_lds)
-      for (uint32_t i = tid; i < nc; i += NT) {
-        const uint2 c = cand[i];
-        lkeys[i] = c.x;
-        lpos[i] = c.y;
-      }
     __syncthreads();
-    // Candidates lie in [lo, hi]: the bytes lo and hi share are common to all.
-    const int fb = st.lo == st.hi ? 4 : __builtin_clz(st.lo ^ st.hi) / 8;
-    const uint32_t tau = in_lds ? radix_select<NT, true>(
-                                      [&](auto f) {
-                                        for (uint32_t i = tid; i < nc; i += NT) f(lkeys[i]);
-                                      },
-                                      keep - st.above, sh, st.lo, fb)
-                                : radix_select<NT, true>(
-                                      [&](auto f) {
-                                        for (uint32_t i = tid; i < nc; i += NT) f(cand[i].x);
-                                      },
-                                      keep - st.above, sh, st.lo, fb);
+  }
+  if (above < keep && above + nc >= keep && nc <= (uint32_t)kResCand && !sm.lost) {
+    // tau - lo = the (keep - above)-th largest of key - lo over the
+    // candidates (all in [lo, hi]): the leading zero bytes of hi - lo are
+    // common to all and skipped.
+    const uint32_t range = hi - lo;
+    const int fb = range == 0 ? 4 : __builtin_clz(range) / 8;
+    const uint32_t tau = lo + radix_select<NT, true>(
+                                  [&](auto f) {
+                                    for (uint32_t i = tid; i < nc; i += NT) f(sm.lkey[i] - lo);
+                                  },
+                                  keep - above, sm.sh, 0u, fb);
     // The evicted candidates' bits: OR-ed into an LDS copy of a range of
-    // kLdsWords bitmask words, which is then merged into the row's words
-    // with coalesced accesses (this workgroup alone owns the row's bitmask
-    // now), instead of one global atomic per candidate.
-    __shared__ uint32_t lbits[kLdsWords];
+    // kLdsWords bitmask words, then merged into the row's words.
     for (int32_t w0 = 0; w0 < lr.words; w0 += kLdsWords) {
-      for (int i = tid; i < kLdsWords; i += NT) lbits[i] = 0;
+      for (int i = tid; i < kLdsWords; i += NT) sm.lbits[i] = 0;
       __syncthreads();
       for (uint32_t i = tid; i < nc; i += NT) {
-        const uint2 c = in_lds ? make_uint2(lkeys[i], lpos[i]) : cand[i];
-        const int32_t w = (int32_t)(c.y >> 5) - w0;
-        if (c.x < tau && (int32_t)c.y >= lr.sinks && w >= 0 && w < kLdsWords) atomicOr(&lbits[w], 1u << (c.y & 31));
+        const int32_t t = (int32_t)sm.lpos[i], w = (t >> 5) - w0;
+        if (sm.lkey[i] < tau && t >= lr.sinks && w >= 0 && w < kLdsWords) atomicOr(&sm.lbits[w], 1u << (t & 31));
       }
       __syncthreads();
-      for (int i = tid; i < kLdsWords && w0 + i < lr.words; i += NT)
-        if (lbits[i]) bits[w0 + i] |= lbits[i];
+      constexpr int PW = kLdsWords / NT;
+      uint32_t lb[PW], gw[PW];
+#pragma unroll
+      for (int k = 0; k < PW; ++k) {
+        const int32_t i = k * NT + tid;
+        lb[k] = w0 + i < lr.words ? sm.lbits[i] : 0u;
+        gw[k] = lb[k] ? bits[w0 + i] : 0u;
+      }
+#pragma unroll
+      for (int k = 0; k < PW; ++k)
+        if (lb[k]) bits[w0 + k * NT + tid] = gw[k] | lb[k];
       __syncthreads();
     }
-    if (tid == 0) lr.state[r].tau = tau;
     return;
   }
-  // Bracket missed (or too many ties for the candidate list): exact select
-  // over the whole row, then every bitmask word rewritten.
+  // Bracket missed (or too many ties or candidates, or a list overflowed):
+  // exact select over the whole row, then every bitmask word rewritten.
   const uint32_t tau = radix_select<NT, true>(
       [&](auto f) {
-        for (int32_t t0 = 0; t0 < lr.L; t0 += 8 * NT) {
-          float v[8];
+        for (int32_t t0 = 0; t0 < L; t0 += 8 * NT) {
+          float x[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = row[min(t0 + tid + j * NT, lr.L - 1)];
+          for (int j = 0; j < 8; ++j) x[j] = row[min(t0 + tid + j * NT, L - 1)];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const int32_t t = t0 + tid + j * NT;
-            if (t < lr.L) f(t < lr.sinks ? order_key(1e38f) : order_key(v[j]));
+            if (t < L) f(t < lr.sinks ? sink_key : order_key(x[j]));
           }
         }
       },
-      keep, sh);
-  const int32_t nw64 = (lr.L + 63) / 64;
-  for (int32_t w = tid >> 6; w < nw64; w += NT / 64) {
+      keep, sm.sh);
+  const int32_t nw64 = (L + 63) / 64;
+  for (int32_t w = wave; w < nw64; w += NW) {
     const int32_t t = w * 64 + lane;
-    const bool e = t < lr.L && t >= lr.sinks && token_key(row, min(t, lr.L - 1), lr.sinks) < tau;
+    const bool e = t < L && t >= lr.sinks && token_key(row, min(t, L - 1), lr.sinks) < tau;
     const uint64_t b = __ballot(e);
     if (lane == 0) {
       bits[2 * w] = (uint32_t)b;
       bits[2 * w + 1] = (uint32_t)(b >> 32);
     }
   }
-  if (tid == 0) lr.state[r].tau = tau;
 }
 
-// K4: zero the evicted rows of logical blocks [lb_begin, lb_end) of row
+// K3: zero the evicted rows of logical blocks [lb_begin, lb_end) of row
 // (seq n, head h), then vote for the fully evicted ones (after this
 // workgroup's own zeroing, so the H-th vote, the unlink, follows every
 // head's reads of the block-table entry).
@@ -843,7 +993,7 @@ __global__ __launch_bounds__(256) void evict_apply_kernel(const LongRows lr, int
   }
 }
 
-// K4 for INT4 pools on the scale-line path (G <= 16, 16-byte aligned pool):
+// K3 for INT4 pools on the scale-line path (G <= 16, 16-byte aligned pool):
 // work items are (logical block, head) pairs of one sequence in page-major
 // order, so the H scale runs of a physical page (one per head, a block
 // apart) are rewritten together instead of one head's runs spread over the
@@ -1055,14 +1205,17 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
   const int32_t sinks = num_sink_tokens < 0 ? 0 : (num_sink_tokens > seq_len ? seq_len : num_sink_tokens);
   MEMOPT_REQUIRE(p.kv_format != MEMOPT_KV_INT4 || p.block_size == 16, MEMOPT_ERR_UNSUPPORTED,
                  "evict_tokens: INT4 page pools use 16-token pages");
-  MEMOPT_REQUIRE((int64_t)seq_len + 256 * kClassifySplit < (1LL << 31), MEMOPT_ERR_UNSUPPORTED,
+  MEMOPT_REQUIRE((int64_t)seq_len + kSpan < (1LL << 31), MEMOPT_ERR_UNSUPPORTED,
                  "evict_tokens: seq_len too large");
   const bool int4 = p.kv_format == MEMOPT_KV_INT4;
   const bool long_rows = seq_len > kShortRow;
   const int64_t rows = (int64_t)num_seqs * num_heads;
   const int32_t words = (seq_len + 63) / 64 * 2;
-  const int64_t ws_bytes =
-      long_rows ? rows * (int64_t)(sizeof(RowState) + words * sizeof(uint32_t) + kRowCand * sizeof(uint2)) : 0;
+  const int32_t spans = (seq_len + kSpan - 1) / kSpan;
+  // long-row workspace: slots [rows][spans], candidate lists [rows][spans][kSpanCand], bitmasks [rows][words]
+  const int64_t ws_bytes = long_rows ? rows * ((int64_t)spans * ((int64_t)sizeof(uint4) + kSpanCand * (int64_t)sizeof(uint2)) +
+                                              words * (int64_t)sizeof(uint32_t))
+                                     : 0;
   EvictScratch es;
   int rc = evict_scratch(int4 ? p.num_blocks : 0, ws_bytes, &es);
   if (rc != MEMOPT_OK) return rc;
@@ -1088,16 +1241,18 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
     lr.keep = keep;
     lr.sinks = sinks;
     lr.words = words;
-    lr.state = reinterpret_cast<RowState *>(es.ws);
-    lr.bits = reinterpret_cast<uint32_t *>(es.ws + rows * sizeof(RowState));
-    lr.cand = reinterpret_cast<uint2 *>(es.ws + rows * (int64_t)(sizeof(RowState) + words * sizeof(uint32_t)));
+    lr.spans = spans;
+    lr.slot = reinterpret_cast<uint4 *>(es.ws);
+    lr.cand = reinterpret_cast<uint2 *>(lr.slot + rows * spans);
+    lr.bits = reinterpret_cast<uint32_t *>(lr.cand + rows * spans * (int64_t)kSpanCand);
     MEMOPT_REQUIRE(rows < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "evict_tokens: too many (seq, head) rows");
-    hipLaunchKernelGGL(evict_bracket_kernel, dim3((unsigned)rows), dim3(512), 0, st, lr);
     if (seq_len % 4 == 0 && ((uintptr_t)attention_scores & 15) == 0)
-      hipLaunchKernelGGL(evict_classify_kernel<true>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr, ma);
+      hipLaunchKernelGGL(evict_classify_long_kernel<true>, dim3((unsigned)rows, (unsigned)spans), dim3(kClsNT), 0, st,
+                         lr, ma);
     else
-      hipLaunchKernelGGL(evict_classify_kernel<false>, dim3((unsigned)rows, kClassifySplit), dim3(512), 0, st, lr, ma);
-    hipLaunchKernelGGL(evict_resolve_kernel, dim3((unsigned)rows), dim3(1024), 0, st, lr);
+      hipLaunchKernelGGL(evict_classify_long_kernel<false>, dim3((unsigned)rows, (unsigned)spans), dim3(kClsNT), 0,
+                         st, lr, ma);
+    hipLaunchKernelGGL(evict_resolve_long_kernel, dim3((unsigned)rows), dim3(kResNT), 0, st, lr);
     const int32_t nlb = std::min((seq_len + p.block_size - 1) / p.block_size, max_blocks_per_seq);
     if (int4 && p.head_dim / 64 <= 16 && ((uintptr_t)p.key & 15) == 0) {
       const int32_t per = std::max(1, 256 / num_heads);

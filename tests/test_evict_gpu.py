@@ -22,10 +22,13 @@ def _pool_state(fmt):
 @pytest.mark.parametrize("N,H,L,bs,r,sinks", [
     (2, 4, 100, 16, 0.5, 4), (3, 2, 64, 16, 0.75, 0), (1, 8, 4096, 16, 0.75, 4),
     (2, 2, 8192, 16, 0.3, 4), (2, 3, 50, 8, 0.1, 2), (1, 2, 40, 16, 1.0, 4),
-    # 1024-thread kernel with keys in registers (L <= 32768), then the split
-    # kernels for long rows (sample bracket, classify, resolve, apply)
+    # 1024-thread kernel with keys in registers (L <= 32768), then the long-row
+    # kernels (one workgroup per 65536-token span: sample bracket, classify,
+    # resolve by the row's last span; then the apply): one span, two spans
+    # with a 1-token second span, an unaligned row (L % 4 == 3) over two spans
     (1, 2, 20000, 16, 0.75, 4), (1, 2, 40000, 16, 0.6, 4), (1, 1, 40001, 16, 0.5, 3),
-    (2, 3, 65536, 16, 0.75, 4), (1, 2, 33000, 32, 0.9, 0)])
+    (2, 3, 65536, 16, 0.75, 4), (1, 2, 33000, 32, 0.9, 0), (1, 2, 65537, 16, 0.75, 4),
+    (1, 1, 131071, 16, 0.6, 5)])
 def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
     if fmt == "int4" and bs != 16:
         pytest.skip("the INT4 page pool uses 16-token pages")
@@ -56,11 +59,12 @@ def test_evict_tokens_vs_oracle(fmt, N, H, L, bs, r, sinks):
     same_bits(ibf_d, ibf)
 
 
-@pytest.mark.parametrize("L", [40000, 40001])
+@pytest.mark.parametrize("L", [40000, 40001, 131072])
 def test_evict_tokens_long_rows_many_ties(L):
     """Long rows whose sample bracket holds far more tokens than the
-    candidate list (scores take 4 values): the resolve kernel falls back to
-    an exact select over the whole row and rewrites the bitmask."""
+    candidate lists (scores take 4 values): the row's resolving workgroup
+    falls back to an exact select over the whole row and rewrites the
+    bitmask (one span, and two spans)."""
     rng = np.random.default_rng(L)
     N, H, bs, D, r, sinks = 1, 2, 16, 64, 0.6, 4
     M = (L + bs - 1) // bs
@@ -127,12 +131,43 @@ def test_evict_tokens_long_rows_ordered_scores(order):
 
 
 def test_evict_tokens_longest_row():
-    """One row of 2^19 tokens (the longest the single-workgroup kernel of an
-    earlier design could not take): split kernels, INT4 pool."""
+    """One row of 2^19 tokens: 8 spans, and more bracket candidates (about
+    21K) than the resolving workgroup holds in LDS, so the select reads the
+    spans' candidate lists from memory. INT4 pool."""
     rng = np.random.default_rng(19)
     L = 1 << 19
     s = rng.lognormal(size=(1, 1, L)).astype(np.float32)
     _evict_case("int4", 1, 1, L, 64, 0.75, 4, s, extra_pages=1)
+
+
+def test_evict_tokens_long_rows_clustered_candidates():
+    """Candidates concentrated in the tokens one wave of the classify
+    kernel reads (positions p with p % 4096 < 256 hold scores within 1e-3
+    of 1, tau falls among them): that wave's candidate list overflows, and
+    the resolve selects over the whole row instead of the spans' lists."""
+    rng = np.random.default_rng(31)
+    N, H, L = 1, 2, 70000
+    s = np.empty((N, H, L), np.float32)
+    pos = np.arange(L)
+    cl = (pos % 4096) < 256
+    for h in range(H):
+        hi_mask = rng.random(L) < 0.5
+        s[0, h] = np.where(hi_mask, rng.uniform(2, 10, L), rng.uniform(0.01, 0.5, L))
+        s[0, h, cl] = 1.0 + rng.uniform(-1e-3, 1e-3, cl.sum())
+    n_hi = int(((s[0, 0] > 1.5) & ~cl).sum())
+    r = (n_hi + cl.sum() / 2 + 4) / L
+    _evict_case("int4", N, H, L, 64, float(r), 4, s)
+
+
+def test_evict_tokens_long_rows_span_counts():
+    """Back-to-back long-row calls with 4, 1 and 2 spans per row and several
+    rows: each row is resolved by whichever span finishes last, through
+    per-row arrival counters that every call must leave at zero for the
+    next one (a counter left behind would resolve a row early)."""
+    for i, (N, H, L) in enumerate([(1, 2, 200003), (2, 3, 50000), (3, 2, 131072), (1, 1, 65540)]):
+        rng = np.random.default_rng(100 + i)
+        s = rng.lognormal(size=(N, H, L)).astype(np.float32)
+        _evict_case("int4", N, H, L, 64, 0.75, 4, s, seed=i)
 
 
 @pytest.mark.parametrize("L", [300, 40000])
