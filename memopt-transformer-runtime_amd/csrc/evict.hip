@@ -130,20 +130,27 @@ __device__ __forceinline__ void zero_int4_scale_lines(uint8_t *pool, const Int4P
   for (int32_t lb0 = lb_begin + wave * bpw * UL; lb0 < nlb; lb0 += NW * bpw * UL) {
     uint32_t mm[UL];  // evicted tokens of the lane's block, 0 if none or unmapped
     int32_t ph[UL];
+    // All loads are unconditional, so that the steps' loads are in flight
+    // together: blocks past the end read the last block's entry, and a lane
+    // with nothing to clear reads the line of (page 0, head h), which every
+    // such lane shares, and stores nothing.
 #pragma unroll
-    for (int u = 0; u < UL; ++u) {  // bitmask and block-table loads are independent
+    for (int u = 0; u < UL; ++u) ph[u] = bt[min(lb0 + u * bpw + jb, nlb - 1)];
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
       const int32_t lb = lb0 + u * bpw + jb;
-      const bool in = jb < bpw && lb < nlb;
+      const bool in = jb < bpw && lb < nlb;  // 64 % lpb lanes idle when G is no power of 2
       mm[u] = in ? (evbits[lb >> 1] >> ((lb & 1) * 16)) & 0xFFFFu : 0u;
-      ph[u] = in ? bt[lb] : -1;
+      if (!in) ph[u] = -1;
     }
     uint4 v[UL];
     uint4 *w[UL];
+    const uint4 *idle = reinterpret_cast<const uint4 *>(pool + (int64_t)h * f.block + f.kscales) + q;
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
       if (!(ph[u] >= 0 && ph[u] < total_pool_blocks)) mm[u] = 0;
       w[u] = reinterpret_cast<uint4 *>(pool + ((int64_t)(mm[u] ? ph[u] : 0) * H + h) * f.block + f.kscales) + q;
-      if (mm[u] && !aliased) v[u] = *w[u];
+      v[u] = *(mm[u] && !aliased ? w[u] : idle);
     }
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
@@ -1018,30 +1025,61 @@ __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows l
   auto mask16 = [&](int32_t lb, int32_t h) { return (bits[(int64_t)h * lr.words + (lb >> 1)] >> ((lb & 1) * 16)) & 0xFFFFu; };
   const Int4Page f(z.D);
   uint8_t *pool = (uint8_t *)z.k;
-  const bool aliased = pages_aliased(z);
   // Same line rewrite as zero_int4_scale_lines: 4 G lanes per 16-token
   // block, one 16-byte chunk each, UL steps of 64 / (4 G) blocks in flight.
   const int32_t lpb = 4 * f.G, bpw = 64 / lpb, jb = lane / lpb, q = lane % lpb;
   const int32_t gmask = 16 * f.G - 1;
+  const int32_t full_end = min(lb_end, min(lr.L / 16, M));
+  // Fully evicted (block, head) items found during the rewrite, voted after
+  // one barrier: (logical block, page).
+  constexpr int kVotes = 256;
+  __shared__ int2 s_vote[kVotes];
+  __shared__ uint32_t s_nvote;
+  if (tid == 0) s_nvote = 0;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   for (int32_t i0 = wave * bpw * UL; i0 < items; i0 += NW * bpw * UL) {
     uint32_t mm[UL];
-    int32_t ph[UL], hh[UL];
+    int32_t ph[UL], hh[UL], ll[UL];
+    // All loads are unconditional, so that the steps' loads are in flight
+    // together: items past the end read the last item's mask and page, and
+    // a lane with nothing to clear reads the line of (page 0, head 0),
+    // which every such lane shares, and stores nothing.
+    uint32_t wd[UL];
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
-      const int32_t i = i0 + u * bpw + jb;
-      const bool in = jb < bpw && i < items;
-      const int32_t lb = lb_begin + i / H, h = i % H;
-      hh[u] = h;
-      mm[u] = in ? mask16(lb, h) : 0u;
-      ph[u] = in ? bt[lb] : -1;
+      const int32_t i = min(i0 + u * bpw + jb, items - 1);
+      ll[u] = lb_begin + i / H;
+      hh[u] = i % H;
+    }
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      wd[u] = bits[(int64_t)hh[u] * lr.words + (ll[u] >> 1)];
+      ph[u] = bt[ll[u]];
+    }
+    const bool aliased = pages_aliased(z);  // loaded with the masks and pages
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      const bool in = jb < bpw && i0 + u * bpw + jb < items;  // 64 % lpb lanes idle when G is no power of 2
+      mm[u] = in ? (wd[u] >> ((ll[u] & 1) * 16)) & 0xFFFFu : 0u;
+      if (!in) ph[u] = -1;
     }
     uint4 v[UL];
     uint4 *w[UL];
+    const uint4 *idle = reinterpret_cast<const uint4 *>(pool + f.kscales) + q;
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
       if (!(ph[u] >= 0 && ph[u] < total_pool_blocks)) mm[u] = 0;
       w[u] = reinterpret_cast<uint4 *>(pool + ((int64_t)(mm[u] ? ph[u] : 0) * H + hh[u]) * f.block + f.kscales) + q;
-      if (mm[u] && !aliased) v[u] = *w[u];
+      v[u] = *(mm[u] && !aliased ? w[u] : idle);
+    }
+#pragma unroll
+    for (int u = 0; u < UL; ++u) {
+      if (q == 0 && mm[u] == 0xFFFFu && ll[u] < full_end) {
+        const uint32_t slot = atomicAdd(&s_nvote, 1u);
+        if (slot < (uint32_t)kVotes) s_vote[slot] = make_int2(ll[u], ph[u]);
+      }
     }
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
@@ -1063,16 +1101,28 @@ __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows l
       }
     }
   }
-  __syncthreads();
-  const int32_t full_end = min(lb_end, min(lr.L / 16, M));
-  const int32_t vitems = max(0, full_end - lb_begin) * H;
-  for (int32_t i = tid; i < vitems; i += NT) {
-    const int32_t lb = lb_begin + i / H, h = i % H;
-    if (mask16(lb, h) != 0xFFFFu) continue;
-    const int32_t phys = bt[lb];
-    if (phys < 0 || phys >= total_pool_blocks) continue;
+  // Every wave's block-table reads are done (their values were used) once
+  // it reaches the barrier, so an unlink after it cannot hide an entry from
+  // a head of this call; the barrier does not wait for the stores.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  auto vote = [&](int32_t lb, int32_t phys) {
     const int prev = atomicAdd(&is_block_free[phys], 1);
     if (prev + 1 == H) block_tables[(int64_t)n * M + lb] = -1;
+  };
+  const uint32_t nv = s_nvote;
+  if (nv <= (uint32_t)kVotes) {
+    for (uint32_t i = tid; i < nv; i += NT) vote(s_vote[i].x, s_vote[i].y);
+  } else {  // more fully evicted items than the list holds: find them again
+    const int32_t vitems = max(0, full_end - lb_begin) * H;
+    for (int32_t i = tid; i < vitems; i += NT) {
+      const int32_t lb = lb_begin + i / H, h = i % H;
+      if (mask16(lb, h) != 0xFFFFu) continue;
+      const int32_t phys = bt[lb];
+      if (phys < 0 || phys >= total_pool_blocks) continue;
+      vote(lb, phys);
+    }
   }
 }
 
