@@ -495,7 +495,8 @@ __global__ __launch_bounds__(256) void mark_pages_kernel(const MarkArgs a) {
 //     kApplySplit workgroups per row, each over a range of logical blocks.
 // The result is the same exact top-k as the single-workgroup kernel.
 static constexpr int32_t kClsNT = 1024, kClsPer = 16;  // K1 threads per workgroup, float4 loads per thread
-static constexpr int32_t kClsWin = 6;  // K1 loads in flight per thread
+static constexpr int32_t kClsWin = 2;  // K1 loads in flight per thread (2 to 10 measured: 2 is fastest)
+static constexpr int32_t kClsPre = 2;  // of which issued before the bracket
 static constexpr int32_t kSpan = kClsNT * kClsPer * 4;  // tokens per K1 workgroup (65536)
 static constexpr int32_t kSampleChunks = 16, kSampleChunk = 512, kSample = kSampleChunks * kSampleChunk;
 static constexpr int32_t kResNT = 1024;     // K2 threads per workgroup
@@ -644,9 +645,11 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
     sm.skeys[i] = sample_token(i) < lr.sinks ? sink_key : order_key(sv[j]);
   }
   // The span is read through a window of kClsWin loads per thread: the
-  // first ones fly during the bracket, and each later one is issued as a
+  // first kClsPre fly during the bracket, and each later one is issued as a
   // float4 is classified, so the data of all waves arrives interleaved with
   // the classification instead of one wave's whole share after another's.
+  // With all 16 loads issued up front K1 took 29 us on config 5, with a
+  // window of 6 25.4-27.4 us, of 2 23.5 us.
   const int32_t t_span = s * kSpan;
   auto load4 = [&](int j) __attribute__((always_inline)) {
     const int32_t t = t_span + 4 * (j * NT + tid);
@@ -659,13 +662,15 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   };
   float4 v[kClsWin];
 #pragma unroll
-  for (int j = 0; j < kClsWin; ++j) v[j] = load4(j);
+  for (int j = 0; j < kClsPre; ++j) v[j] = load4(j);
   for (int i = tid; i < 256 * kRep; i += NT) (&sm.h1[0][0])[i] = 0;
   for (int i = tid; i < 2 * 256; i += NT) (&sm.h2[0][0])[i] = 0;
   if (tid == 0) sm.above = sm.ncand = 0;
   __syncthreads();
   const uint2 br = sample_bracket<NT>(lr, sm);
   const uint32_t lo = br.x, hi = br.y;
+#pragma unroll
+  for (int j = kClsPre; j < kClsWin; ++j) v[j] = load4(j);
   uint32_t *bits = lr.bits + (int64_t)r * lr.words;
   // Sink tokens count with the key of a 1e38 score and are never evicted.
   const uint32_t sink_gt = sink_key > hi ? 0xFu : 0u, sink_in = sink_key >= lo && sink_key <= hi ? 0xFu : 0u;
