@@ -315,12 +315,14 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
 
   // All loads are issued first (index clamped into the row), then turned
   // into keys: a load placed under the sink test would be waited on before
-  // the next one is issued.
+  // the next one is issued. They are non-temporal (the scores are read
+  // once; the INT4 scale runs the zeroing rewrites stay cached instead:
+  // config 3 28.6 against 29.9 us).
   uint32_t kreg[R];
   {
     float v[R];
 #pragma unroll
-    for (int j = 0; j < R; ++j) v[j] = row[min(tid + j * NT, L - 1)];
+    for (int j = 0; j < R; ++j) v[j] = __builtin_nontemporal_load(&row[min(tid + j * NT, L - 1)]);
 #pragma unroll
     for (int j = 0; j < R; ++j) kreg[j] = tid + j * NT < sinks ? order_key(1e38f) : order_key(v[j]);
   }
@@ -649,15 +651,21 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   // float4 is classified, so the data of all waves arrives interleaved with
   // the classification instead of one wave's whole share after another's.
   // With all 16 loads issued up front K1 took 29 us on config 5, with a
-  // window of 6 25.4-27.4 us, of 2 23.5 us.
+  // window of 6 25.4-27.4 us, of 2 23.5 us. The loads are non-temporal: the
+  // scores are read once, and kept out of the caches they leave the INT4
+  // scale runs there for the apply launch (config 5 apply 50.3 -> 44.7 us
+  // over repeated calls).
   const int32_t t_span = s * kSpan;
   auto load4 = [&](int j) __attribute__((always_inline)) {
     const int32_t t = t_span + 4 * (j * NT + tid);
     const float *p4 = row + min(t, L - 4);
     if constexpr (V4) {
-      return *reinterpret_cast<const float4 *>(p4);
+      typedef float f4v __attribute__((ext_vector_type(4)));
+      const f4v x = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p4));
+      return make_float4(x.x, x.y, x.z, x.w);
     } else {
-      return make_float4(p4[0], p4[1], p4[2], p4[3]);
+      return make_float4(__builtin_nontemporal_load(p4), __builtin_nontemporal_load(p4 + 1),
+                         __builtin_nontemporal_load(p4 + 2), __builtin_nontemporal_load(p4 + 3));
     }
   };
   float4 v[kClsWin];
@@ -1015,10 +1023,16 @@ __global__ __launch_bounds__(256) void evict_apply_kernel(const LongRows lr, int
 // heads; per * H is about 256 items, one pass of its 4 waves. The votes
 // follow the workgroup's own zeroing; a page's H votes of this sequence all
 // come from this workgroup, and the unlink writes only this sequence's entry.
+// i / H for 0 <= i < 2^24 and 1 <= H < 2^16 as (i * hm) >> 40 with
+// hm = ceil(2^40 / H): hm = 2^40 / H + e (0 <= e < 1) adds i e / 2^40 <
+// 2^-16 <= 1 / H to the exact quotient, which never reaches the next
+// integer.
+__device__ __forceinline__ int32_t div_h(int32_t i, uint64_t hm) { return (int32_t)(((uint64_t)(uint32_t)i * hm) >> 40); }
+
 __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows lr, int32_t *__restrict__ block_tables,
                                                                 int32_t *__restrict__ is_block_free, int32_t M,
                                                                 int64_t total_pool_blocks, RowZero z, int32_t nlb,
-                                                                int32_t per) {
+                                                                int32_t per, uint64_t hm) {
   constexpr int NT = 256, NW = NT / 64, UL = 8;
   const int32_t n = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const int32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1036,14 +1050,12 @@ __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows l
   const int32_t gmask = 16 * f.G - 1;
   const int32_t full_end = min(lb_end, min(lr.L / 16, M));
   // Fully evicted (block, head) items found during the rewrite, voted after
-  // one barrier: (logical block, page).
-  constexpr int kVotes = 256;
-  __shared__ int2 s_vote[kVotes];
-  __shared__ uint32_t s_nvote;
-  if (tid == 0) s_nvote = 0;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  // one barrier: (logical block, page), a list per wave (each wave clears
+  // its own count, so no barrier is needed before the rewrite).
+  constexpr int kVotes = 64;
+  __shared__ int2 s_vote[NW][kVotes];
+  __shared__ uint32_t s_nvote[NW];
+  if (lane == 0) s_nvote[wave] = 0;
   for (int32_t i0 = wave * bpw * UL; i0 < items; i0 += NW * bpw * UL) {
     uint32_t mm[UL];
     int32_t ph[UL], hh[UL], ll[UL];
@@ -1054,9 +1066,9 @@ __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows l
     uint32_t wd[UL];
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
-      const int32_t i = min(i0 + u * bpw + jb, items - 1);
-      ll[u] = lb_begin + i / H;
-      hh[u] = i % H;
+      const int32_t i = min(i0 + u * bpw + jb, items - 1), q = div_h(i, hm);
+      ll[u] = lb_begin + q;
+      hh[u] = i - q * H;
     }
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
@@ -1082,8 +1094,8 @@ __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows l
 #pragma unroll
     for (int u = 0; u < UL; ++u) {
       if (q == 0 && mm[u] == 0xFFFFu && ll[u] < full_end) {
-        const uint32_t slot = atomicAdd(&s_nvote, 1u);
-        if (slot < (uint32_t)kVotes) s_vote[slot] = make_int2(ll[u], ph[u]);
+        const uint32_t slot = atomicAdd(&s_nvote[wave], 1u);
+        if (slot < (uint32_t)kVotes) s_vote[wave][slot] = make_int2(ll[u], ph[u]);
       }
     }
 #pragma unroll
@@ -1116,13 +1128,15 @@ __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows l
     const int prev = atomicAdd(&is_block_free[phys], 1);
     if (prev + 1 == H) block_tables[(int64_t)n * M + lb] = -1;
   };
-  const uint32_t nv = s_nvote;
-  if (nv <= (uint32_t)kVotes) {
-    for (uint32_t i = tid; i < nv; i += NT) vote(s_vote[i].x, s_vote[i].y);
-  } else {  // more fully evicted items than the list holds: find them again
+  bool over = false;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) over = over || s_nvote[w] > (uint32_t)kVotes;
+  if (!over) {
+    for (uint32_t i = lane; i < s_nvote[wave]; i += 64) vote(s_vote[wave][i].x, s_vote[wave][i].y);
+  } else {  // more fully evicted items than a list holds: find them again
     const int32_t vitems = max(0, full_end - lb_begin) * H;
     for (int32_t i = tid; i < vitems; i += NT) {
-      const int32_t lb = lb_begin + i / H, h = i % H;
+      const int32_t q = div_h(i, hm), lb = lb_begin + q, h = i - q * H;
       if (mask16(lb, h) != 0xFFFFu) continue;
       const int32_t phys = bt[lb];
       if (phys < 0 || phys >= total_pool_blocks) continue;
@@ -1309,11 +1323,12 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
                          st, lr, ma);
     hipLaunchKernelGGL(evict_resolve_long_kernel, dim3((unsigned)rows), dim3(kResNT), 0, st, lr);
     const int32_t nlb = std::min((seq_len + p.block_size - 1) / p.block_size, max_blocks_per_seq);
-    if (int4 && p.head_dim / 64 <= 16 && ((uintptr_t)p.key & 15) == 0) {
+    if (int4 && p.head_dim / 64 <= 16 && ((uintptr_t)p.key & 15) == 0 && num_heads < 65536) {
       const int32_t per = std::max(1, 256 / num_heads);
+      const uint64_t hm = ((1ULL << 40) + (uint64_t)num_heads - 1) / (uint64_t)num_heads;
       hipLaunchKernelGGL(evict_apply_pages_kernel, dim3((unsigned)num_seqs, (unsigned)((nlb + per - 1) / per)),
                          dim3(256), 0, st, lr, block_tables, is_block_free, max_blocks_per_seq, total_pool_blocks, z,
-                         nlb, per);
+                         nlb, per, hm);
     } else {
       hipLaunchKernelGGL(evict_apply_kernel, dim3((unsigned)rows, kApplySplit), dim3(256), 0, st, lr, block_tables,
                          is_block_free, max_blocks_per_seq, total_pool_blocks, z);
