@@ -26,9 +26,11 @@ struct IntC {
 };
 
 // Order-preserving uint32 key of a float: negative values have every bit
-// flipped, others the sign bit set.
+// flipped, others the sign bit set; -0 takes the key of +0 (f + 0 turns -0
+// into +0 and leaves every other value as it is), since the two compare
+// equal: a -0 score ties with a +0 tau, as in float compares.
 __device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint32_t u = __builtin_bit_cast(uint32_t, f + 0.0f);
   return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
 
@@ -806,6 +808,7 @@ struct ResolveLds {
   SelectShared<kResNT> sh;
   uint32_t lbits[kLdsWords];
   uint32_t above, ncand, lost;
+  uint32_t xabove, xin;  // listed keys above hi, resp. inside [lo, hi]
 };
 
 // K2: one workgroup per row.
@@ -819,7 +822,7 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   const uint4 *slot = lr.slot + (int64_t)r * lr.spans;
   __shared__ ResolveLds sm;
   const uint32_t sink_key = order_key(1e38f);
-  if (tid == 0) sm.above = sm.ncand = sm.lost = 0;
+  if (tid == 0) sm.above = sm.ncand = sm.lost = sm.xabove = sm.xin = 0;
   __syncthreads();
   {  // the spans' counts
     uint32_t a = 0, c = 0, l = 0;
@@ -846,42 +849,61 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   __syncthreads();
   const uint32_t above = sm.above, nc = sm.ncand, keep = (uint32_t)lr.keep;
   if (above < keep && above + nc >= keep && nc <= (uint32_t)kResCand && !sm.lost) {
-    // The spans' candidate lists, 8 entries per thread in flight.
-    uint32_t base = 0;
+    // The spans' candidate lists, 8 entries per thread in flight. The
+    // classify launch places a token by float compares with the floats of
+    // lo and hi; a score the compares cannot place (a NaN) is listed
+    // whatever its key: listed keys above hi count as kept, keys below lo
+    // are evicted, and the select runs over the keys in [lo, hi].
+    uint32_t base = 0, xa = 0, xi = 0;
     for (int32_t q = 0; q < lr.spans; ++q) {
       const uint32_t cnt = slot[q].y;
       const uint2 *gl = lr.cand + ((int64_t)r * lr.spans + q) * kSpanCand;
       for (uint32_t i0 = 0; i0 < cnt; i0 += 8 * NT) {
-        uint2 c[8];
+        uint2 c[8];  // unconditional loads (index clamped into the list), all in flight
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t i = i0 + k * NT + tid;
-          if (i < cnt) c[k] = gl[i];
-        }
+        for (int k = 0; k < 8; ++k) c[k] = gl[min(i0 + k * NT + tid, cnt - 1)];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const uint32_t i = i0 + k * NT + tid;
           if (i < cnt) {
-            sm.lkey[base + i] = order_key(__builtin_bit_cast(float, c[k].x));
+            const uint32_t key = order_key(__builtin_bit_cast(float, c[k].x));
+            sm.lkey[base + i] = key;
             sm.lpos[base + i] = c[k].y;
+            xa += key > hi;
+            xi += key >= lo && key <= hi;
           }
         }
       }
       base += cnt;
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      xa += __shfl_xor(xa, off, 64);
+      xi += __shfl_xor(xi, off, 64);
+    }
+    if (lane == 0 && (xa | xi)) {
+      atomicAdd(&sm.xabove, xa);
+      atomicAdd(&sm.xin, xi);
+    }
     __syncthreads();
   }
-  if (above < keep && above + nc >= keep && nc <= (uint32_t)kResCand && !sm.lost) {
-    // tau - lo = the (keep - above)-th largest of key - lo over the
-    // candidates (all in [lo, hi]): the leading zero bytes of hi - lo are
-    // common to all and skipped.
+  const uint32_t above_all = above + sm.xabove;
+  const bool listed = above < keep && above + nc >= keep && nc <= (uint32_t)kResCand && !sm.lost &&
+                      above_all < keep && above_all + sm.xin >= keep;
+  if (listed) {
+    // tau - lo = the (keep - above_all)-th largest of key - lo over the
+    // candidates in [lo, hi]: the leading zero bytes of hi - lo are common
+    // to all and skipped.
     const uint32_t range = hi - lo;
     const int fb = range == 0 ? 4 : __builtin_clz(range) / 8;
     const uint32_t tau = lo + radix_select<NT, true>(
                                   [&](auto f) {
-                                    for (uint32_t i = tid; i < nc; i += NT) f(sm.lkey[i] - lo);
+                                    for (uint32_t i = tid; i < nc; i += NT) {
+                                      const uint32_t k = sm.lkey[i];
+                                      if (k >= lo && k <= hi) f(k - lo);
+                                    }
                                   },
-                                  keep - above, sm.sh, 0u, fb);
+                                  keep - above_all, sm.sh, 0u, fb);
     // The evicted candidates' bits: OR-ed into an LDS copy of a range of
     // kLdsWords bitmask words, then merged into the row's words.
     for (int32_t w0 = 0; w0 < lr.words; w0 += kLdsWords) {

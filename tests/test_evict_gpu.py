@@ -159,6 +159,23 @@ def test_evict_tokens_long_rows_clustered_candidates():
     _evict_case("int4", N, H, L, 64, float(r), 4, s)
 
 
+@pytest.mark.parametrize("L", [8192, 70000])
+def test_evict_tokens_signed_zero_ties(L):
+    """Scores of +0 and -0 (6 % of each row, random signs) between
+    negative and positive scores, keep = half the row: tau is a zero, and
+    +0 and -0 tie as in float compares (neither is evicted, the negative
+    scores are). Short rows (one workgroup) and long rows (the bracket
+    lands on the zeros: candidate lists and the resolve)."""
+    rng = np.random.default_rng(L + 3)
+    N, H = 1, 2
+    s = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    neg = rng.random((N, H, L)) < 0.48
+    s[neg] = -s[neg]
+    zero = rng.random((N, H, L)) < 0.06
+    s[zero] = np.where(rng.random(int(zero.sum())) < 0.5, np.float32(0.0), np.float32(-0.0))
+    _evict_case("int4", N, H, L, 64, 0.5, 4, s)
+
+
 def test_evict_tokens_long_rows_span_counts():
     """Back-to-back long-row calls with 4, 1 and 2 spans per row and several
     rows: each row is resolved by whichever span finishes last, through
