@@ -803,13 +803,70 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   if (tid == 0) lr.slot[(int64_t)r * lr.spans + s] = make_uint4(sm.above, sm.ncand | lost, lo, hi);
 }
 
+static constexpr int32_t kSpanLds = 64;  // spans whose list offsets K2 keeps in LDS
+
 struct ResolveLds {
   uint32_t lkey[kResCand], lpos[kResCand];
   SelectShared<kResNT> sh;
+  uint32_t hist12[4096], wsum[kResNT / 64], pick[2];  // select12
   uint32_t lbits[kLdsWords];
+  uint32_t cpre[kSpanLds + 1];  // list offsets of the spans (spans <= kSpanLds)
   uint32_t above, ncand, lost;
   uint32_t xabove, xin;  // listed keys above hi, resp. inside [lo, hi]
 };
+
+// d of the k-th largest (1 <= k <= number of values) of the values d in
+// [0, range] handed out by visit(f) (every thread of the workgroup calls
+// it): 12-bit radix passes from the top bit of range (two passes for
+// range < 2^24) over one 4096-bin LDS histogram. Thread t owns bins
+// 4t .. 4t + 3 of the suffix scan (NT = 1024).
+template <int NT, typename Visit>
+__device__ uint32_t select12(Visit visit, uint32_t k, uint32_t range, ResolveLds &sm) {
+  static_assert(NT * 4 == 4096, "select12 takes 1024 threads");
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nbits = range ? 32 - __builtin_clz(range) : 1;
+  uint32_t prefix = 0, pmask = 0;
+  for (int shift = max(nbits - 12, 0);; shift = max(shift - 12, 0)) {
+    for (int i = tid; i < 4096; i += NT) sm.hist12[i] = 0;
+    __syncthreads();
+    visit([&](uint32_t d) {
+      if ((d & pmask) == prefix) atomicAdd(&sm.hist12[(d >> shift) & 0xFFFu], 1u);
+    });
+    __syncthreads();
+    uint32_t c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = sm.hist12[4 * tid + j];
+    const uint32_t tot = c[0] + c[1] + c[2] + c[3];
+    uint32_t inc = tot;  // sum of tot over lanes >= lane of the wave
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_down(inc, off, 64);
+      if (lane + off < 64) inc += o;
+    }
+    if (lane == 0) sm.wsum[wave] = inc;
+    __syncthreads();
+    uint32_t above = inc - tot;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) above += w > wave ? sm.wsum[w] : 0u;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      const uint32_t upto = above + c[j];  // values with digit >= 4 tid + j
+      if (upto >= k && above < k) {
+        sm.pick[0] = 4 * tid + j;
+        sm.pick[1] = k - above;
+      }
+      above = upto;
+    }
+    __syncthreads();
+    prefix |= sm.pick[0] << shift;
+    pmask |= 0xFFFu << shift;
+    k = sm.pick[1];
+    if (shift == 0) break;
+  }
+  return prefix;
+}
 
 // K2: one workgroup per row.
 __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRows lr) {
@@ -822,26 +879,34 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   const uint4 *slot = lr.slot + (int64_t)r * lr.spans;
   __shared__ ResolveLds sm;
   const uint32_t sink_key = order_key(1e38f);
-  if (tid == 0) sm.above = sm.ncand = sm.lost = sm.xabove = sm.xin = 0;
-  __syncthreads();
-  {  // the spans' counts
-    uint32_t a = 0, c = 0, l = 0;
-    for (int32_t q = tid; q < lr.spans; q += NT) {
-      const uint4 sl = slot[q];
-      a += sl.x;
-      c += sl.y & ~kListLost;
-      l |= sl.y & kListLost;
+  if (tid == 0) sm.xabove = sm.xin = 0;
+  if (wave == 0) {  // the spans' counts, and their lists' offsets, 64 spans per step
+    uint32_t a = 0, off = 0, l = 0;
+    for (int32_t q0 = 0; q0 < lr.spans; q0 += 64) {
+      const int32_t q = q0 + lane;
+      const uint4 sl = slot[min(q, lr.spans - 1)];
+      const uint32_t c = q < lr.spans ? sl.y & ~kListLost : 0u;
+      a += q < lr.spans ? sl.x : 0u;
+      l |= q < lr.spans ? sl.y & kListLost : 0u;
+      uint32_t inc = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+      }
+      if (q < kSpanLds) sm.cpre[q] = off + inc - c;
+      off += __shfl(inc, 63, 64);
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      a += __shfl_xor(a, off, 64);
-      c += __shfl_xor(c, off, 64);
-      l |= __shfl_xor(l, off, 64);
+    for (int o = 32; o >= 1; o >>= 1) {
+      a += __shfl_xor(a, o, 64);
+      l |= __shfl_xor(l, o, 64);
     }
-    if (lane == 0 && (a | c | l)) {
-      atomicAdd(&sm.above, a);
-      atomicAdd(&sm.ncand, c);
-      atomicOr(&sm.lost, l);
+    if (lane == 0) {
+      sm.above = a;
+      sm.ncand = off;
+      sm.lost = l;
+      if (lr.spans <= kSpanLds) sm.cpre[lr.spans] = off;
     }
   }
   const uint4 s0 = slot[0];  // every span holds the row's bracket
@@ -854,27 +919,46 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
     // lo and hi; a score the compares cannot place (a NaN) is listed
     // whatever its key: listed keys above hi count as kept, keys below lo
     // are evicted, and the select runs over the keys in [lo, hi].
-    uint32_t base = 0, xa = 0, xi = 0;
-    for (int32_t q = 0; q < lr.spans; ++q) {
-      const uint32_t cnt = slot[q].y;
-      const uint2 *gl = lr.cand + ((int64_t)r * lr.spans + q) * kSpanCand;
-      for (uint32_t i0 = 0; i0 < cnt; i0 += 8 * NT) {
-        uint2 c[8];  // unconditional loads (index clamped into the list), all in flight
-#pragma unroll
-        for (int k = 0; k < 8; ++k) c[k] = gl[min(i0 + k * NT + tid, cnt - 1)];
+    uint32_t xa = 0, xi = 0;
+    auto take = [&](uint32_t e, uint2 c) {
+      const uint32_t key = order_key(__builtin_bit_cast(float, c.x));
+      sm.lkey[e] = key;
+      sm.lpos[e] = c.y;
+      xa += key > hi;
+      xi += key >= lo && key <= hi;
+    };
+    const uint2 *gl0 = lr.cand + (int64_t)r * lr.spans * kSpanCand;
+    if (lr.spans <= kSpanLds) {
+      // all spans' entries as one sequence e = cpre[q] + i: unconditional
+      // loads (index clamped), all in flight together
+      for (uint32_t e0 = 0; e0 < nc; e0 += 8 * NT) {
+        uint2 c[8];
+        int32_t q = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const uint32_t i = i0 + k * NT + tid;
-          if (i < cnt) {
-            const uint32_t key = order_key(__builtin_bit_cast(float, c[k].x));
-            sm.lkey[base + i] = key;
-            sm.lpos[base + i] = c[k].y;
-            xa += key > hi;
-            xi += key >= lo && key <= hi;
-          }
+          const uint32_t e = min(e0 + k * NT + tid, nc - 1);
+          while (q + 1 < lr.spans && sm.cpre[q + 1] <= e) ++q;  // e grows with k
+          c[k] = gl0[(int64_t)q * kSpanCand + (e - sm.cpre[q])];
         }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (e0 + k * NT + tid < nc) take(e0 + k * NT + tid, c[k]);
       }
-      base += cnt;
+    } else {
+      uint32_t base = 0;
+      for (int32_t q = 0; q < lr.spans; ++q) {
+        const uint32_t cnt = slot[q].y;
+        const uint2 *gl = gl0 + (int64_t)q * kSpanCand;
+        for (uint32_t i0 = 0; i0 < cnt; i0 += 8 * NT) {
+          uint2 c[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) c[k] = gl[min(i0 + k * NT + tid, cnt - 1)];
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (i0 + k * NT + tid < cnt) take(base + i0 + k * NT + tid, c[k]);
+        }
+        base += cnt;
+      }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -892,18 +976,15 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
                       above_all < keep && above_all + sm.xin >= keep;
   if (listed) {
     // tau - lo = the (keep - above_all)-th largest of key - lo over the
-    // candidates in [lo, hi]: the leading zero bytes of hi - lo are common
-    // to all and skipped.
-    const uint32_t range = hi - lo;
-    const int fb = range == 0 ? 4 : __builtin_clz(range) / 8;
-    const uint32_t tau = lo + radix_select<NT, true>(
+    // candidates in [lo, hi].
+    const uint32_t tau = lo + select12<NT>(
                                   [&](auto f) {
                                     for (uint32_t i = tid; i < nc; i += NT) {
                                       const uint32_t k = sm.lkey[i];
                                       if (k >= lo && k <= hi) f(k - lo);
                                     }
                                   },
-                                  keep - above_all, sm.sh, 0u, fb);
+                                  keep - above_all, hi - lo, sm);
     // The evicted candidates' bits: OR-ed into an LDS copy of a range of
     // kLdsWords bitmask words, then merged into the row's words.
     for (int32_t w0 = 0; w0 < lr.words; w0 += kLdsWords) {
