@@ -818,8 +818,9 @@ struct ResolveLds {
 // d of the k-th largest (1 <= k <= number of values) of the values d in
 // [0, range] handed out by visit(f) (every thread of the workgroup calls
 // it): 12-bit radix passes from the top bit of range (two passes for
-// range < 2^24) over one 4096-bin LDS histogram. Thread t owns bins
-// 4t .. 4t + 3 of the suffix scan (NT = 1024).
+// range < 2^24) over one 4096-bin LDS histogram, which must be zero (and
+// visible to all threads) on entry. Thread t owns bins 4t .. 4t + 3 of
+// the suffix scan (NT = 1024).
 template <int NT, typename Visit>
 __device__ uint32_t select12(Visit visit, uint32_t k, uint32_t range, ResolveLds &sm) {
   static_assert(NT * 4 == 4096, "select12 takes 1024 threads");
@@ -828,9 +829,13 @@ __device__ uint32_t select12(Visit visit, uint32_t k, uint32_t range, ResolveLds
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nbits = range ? 32 - __builtin_clz(range) : 1;
   uint32_t prefix = 0, pmask = 0;
+  bool first = true;
   for (int shift = max(nbits - 12, 0);; shift = max(shift - 12, 0)) {
-    for (int i = tid; i < 4096; i += NT) sm.hist12[i] = 0;
-    __syncthreads();
+    if (!first) {  // the first pass's histogram is cleared by the caller
+      for (int i = tid; i < 4096; i += NT) sm.hist12[i] = 0;
+      __syncthreads();
+    }
+    first = false;
     visit([&](uint32_t d) {
       if ((d & pmask) == prefix) atomicAdd(&sm.hist12[(d >> shift) & 0xFFFu], 1u);
     });
@@ -880,6 +885,15 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   __shared__ ResolveLds sm;
   const uint32_t sink_key = order_key(1e38f);
   if (tid == 0) sm.xabove = sm.xin = 0;
+  // The row's first kLdsWords bitmask words (written by the classify
+  // launch) are read now, for the merge at the end, and the merge's LDS
+  // copy and the first select pass's histogram are cleared now.
+  constexpr int PW = kLdsWords / NT;
+  uint32_t bw[PW];
+#pragma unroll
+  for (int k = 0; k < PW; ++k) bw[k] = bits[min(k * NT + tid, lr.words - 1)];
+  for (int i = tid; i < kLdsWords; i += NT) sm.lbits[i] = 0;
+  for (int i = tid; i < 4096; i += NT) sm.hist12[i] = 0;
   if (wave == 0) {  // the spans' counts, and their lists' offsets, 64 spans per step
     uint32_t a = 0, off = 0, l = 0;
     for (int32_t q0 = 0; q0 < lr.spans; q0 += 64) {
@@ -986,22 +1000,24 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
                                   },
                                   keep - above_all, hi - lo, sm);
     // The evicted candidates' bits: OR-ed into an LDS copy of a range of
-    // kLdsWords bitmask words, then merged into the row's words.
+    // kLdsWords bitmask words, then merged into the row's words (the first
+    // range's words were read at the start).
     for (int32_t w0 = 0; w0 < lr.words; w0 += kLdsWords) {
-      for (int i = tid; i < kLdsWords; i += NT) sm.lbits[i] = 0;
-      __syncthreads();
+      if (w0 > 0) {
+        for (int i = tid; i < kLdsWords; i += NT) sm.lbits[i] = 0;
+        __syncthreads();
+      }
       for (uint32_t i = tid; i < nc; i += NT) {
         const int32_t t = (int32_t)sm.lpos[i], w = (t >> 5) - w0;
         if (sm.lkey[i] < tau && t >= lr.sinks && w >= 0 && w < kLdsWords) atomicOr(&sm.lbits[w], 1u << (t & 31));
       }
       __syncthreads();
-      constexpr int PW = kLdsWords / NT;
       uint32_t lb[PW], gw[PW];
 #pragma unroll
       for (int k = 0; k < PW; ++k) {
         const int32_t i = k * NT + tid;
         lb[k] = w0 + i < lr.words ? sm.lbits[i] : 0u;
-        gw[k] = lb[k] ? bits[w0 + i] : 0u;
+        gw[k] = w0 == 0 ? bw[k] : lb[k] ? bits[w0 + i] : 0u;
       }
 #pragma unroll
       for (int k = 0; k < PW; ++k)
