@@ -837,7 +837,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   float16_t o[NDB];
 #pragma unroll
   for (int i = 0; i < NDB; ++i) o[i] = (float16_t){};
-  float m = -INFINITY, lsum = 0.0f;
+  // Row sums of the probabilities, one per 32-key block: two independent
+  // chains of 8 dependent v_dot2 per tile instead of one chain of 16.
+  float m = -INFINITY, lsum = 0.0f, lsum1 = 0.0f;
   float16_t mtile = (float16_t){};
 
   const int32_t qlast = min(q0 + 32 * NW, p.Lq) - 1;
@@ -968,6 +970,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       const float alpha = (mn == m) ? 1.0f : fast_exp2((m - mn) * cs);
       const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
       lsum *= alpha;
+      lsum1 *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1095,7 +1098,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       if (k_ahead) load_k(it + 3, IntC<K3>{}, 0, NKL / 2);
       // Seg 3: PV(i) block 0 | probabilities of S(i) block 1
       pv_block(vt, 0, pa);
-      probs(sc[1], pb, lsum);
+      probs(sc[1], pb, lsum1);
       PIPE_SGB(0x100, 4, 0);
 #pragma unroll
       for (int c = 0; c < 2 * NDB; ++c) {
@@ -1138,7 +1141,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   }
   __builtin_amdgcn_s_waitcnt(0);
 
-  const float l = half_sum(lsum);
+  const float l = half_sum(lsum + lsum1);
   if (!q_ok) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   half_t *orow = p.out + (((int64_t)b * p.Lq + qi) * p.H + h) * D;
