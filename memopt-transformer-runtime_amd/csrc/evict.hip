@@ -440,11 +440,16 @@ struct MarkArgs {
   uint32_t epoch;
 };
 
-// mark_entry in three steps, so that its two dependent memory round trips
-// overlap other work: the page of entry e (or -1) ...
-__device__ __forceinline__ int32_t mark_page(const MarkArgs &a, int64_t e) {
+// mark_entry in four steps, so that its two dependent memory round trips
+// overlap other work: the block-table value of entry e, loaded whatever e
+// (index clamped, so the load needs no branch and nothing waits for it
+// until the value is used) ...
+__device__ __forceinline__ int32_t mark_load(const MarkArgs &a, int64_t e) {
+  return a.entries > 0 ? a.bt[min(e, a.entries - 1)] : -1;
+}
+// ... the page of entry e (or -1) from that value ...
+__device__ __forceinline__ int32_t mark_page(const MarkArgs &a, int64_t e, int32_t phys) {
   if (e >= a.entries || (int32_t)(e % a.M) >= a.nlb) return -1;
-  const int32_t phys = a.bt[e];
   return phys >= 0 && phys < a.total_pool_blocks ? phys : -1;
 }
 // ... the exchange (its result, only read by mark_check and only where
@@ -454,6 +459,10 @@ __device__ __forceinline__ void mark_swap(const MarkArgs &a, int64_t e, int32_t 
 }
 // ... and the alias check.
 __device__ __forceinline__ void mark_check(const MarkArgs &a, int32_t phys, unsigned long long old) {
+  // Both halves of the exchange's result stay live until here: the return
+  // writes both, so a register reused for the unread low half would make
+  // the code wait for the exchange where the reuse begins.
+  asm volatile("" ::"v"(old));
   if (phys >= 0 && (uint32_t)(old >> 32) == a.epoch) atomicMax(a.flag, a.epoch);
 }
 
@@ -476,12 +485,11 @@ __global__ __launch_bounds__(256) void mark_pages_kernel(const MarkArgs a) {
 // ---------------------------------------------------------------------------
 // A row is cut into spans of kSpan tokens and takes three kernels:
 //  K1 evict_classify_long_kernel, one workgroup per span: it loads a
-//     16 x 512-key sample spread over the row and, once the sample is in,
-//     issues the loads of its whole span (32 float4 per thread, kept in
-//     registers). While those are in flight it computes a bracket [lo, hi]
-//     around the row's keep-th largest key from the sample (every span of
-//     a row derives the same bracket from the same sample). Each token is
-//     then kept (key > hi, counted), evicted (key < lo, a bit of the row's
+//     16 x 512-key sample spread over the row and computes a bracket
+//     [lo, hi] around the row's keep-th largest key from it (every span of
+//     a row derives the same bracket from the same sample), then streams
+//     its span through a window of loads per thread. Each token is then
+//     kept (key > hi, counted), evicted (key < lo, a bit of the row's
 //     bitmask) or a candidate ((score, token) appended to its wave's list
 //     in LDS; the lists are copied to the span's list at the end). The
 //     same launch marks the block-table entries (alias check, INT4 pools)
@@ -524,6 +532,14 @@ struct LongRows {
 // list is incomplete, and the resolve selects over the whole row instead.
 static constexpr uint32_t kListLost = 0x80000000u;
 
+// Workgroup barrier that orders LDS accesses only: it does not wait for the
+// caller's outstanding global loads and stores.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 struct ClassifyLds {
   uint32_t skeys[kSample];
   uint32_t h1[256][kRep];  // first-byte histogram, lane l adds to copy l % kRep
@@ -545,7 +561,8 @@ struct ClassifyLds {
 // hold most of a wave's keys, and same-address LDS atomics serialize), so
 // each first-byte bin has kRep copies, lane l adding to copy l % kRep.
 // Returns (lo, hi) to every thread. sm.h1 and sm.h2 must be zero and
-// sm.skeys complete (after a barrier) on entry; ends with a barrier.
+// sm.skeys complete (after a barrier) on entry; ends with a barrier. Its
+// barriers order LDS only: the caller's span loads stay in flight.
 template <int NT>
 __device__ __forceinline__ uint2 sample_bracket(const LongRows &lr, ClassifyLds &sm) {
   constexpr int PER = kSample / NT;
@@ -582,17 +599,17 @@ __device__ __forceinline__ uint2 sample_bracket(const LongRows &lr, ClassifyLds 
   };
 #pragma unroll
   for (int j = 0; j < PER; ++j) atomicAdd(&sm.h1[sm.skeys[tid + j * NT] >> 24][lane % kRep], 1u);
-  __syncthreads();
+  lds_barrier();
   if (tid < 256) {
     uint32_t t = 0;
 #pragma unroll
     for (int i = 0; i < kRep; ++i) t += sm.h1[tid][(i + tid) % kRep];
     sm.tot[tid] = t;
   }
-  __syncthreads();
+  lds_barrier();
   for (int which = 0; which < 2; ++which)
     if (want[which] >= 1 && want[which] <= kSample) pick(sm.tot, which, (uint32_t)want[which]);
-  __syncthreads();
+  lds_barrier();
   const uint32_t d1[2] = {sm.pick[0][0], sm.pick[1][0]};
   const uint32_t k1[2] = {sm.pick[0][1], sm.pick[1][1]};
 #pragma unroll
@@ -602,22 +619,21 @@ __device__ __forceinline__ uint2 sample_bracket(const LongRows &lr, ClassifyLds 
     for (int which = 0; which < 2; ++which)
       if ((key >> 24) == d1[which]) atomicAdd(&sm.h2[which][(key >> 16) & 0xFF], 1u);
   }
-  __syncthreads();
+  lds_barrier();
   for (int which = 0; which < 2; ++which)
     if (want[which] >= 1 && want[which] <= kSample) pick(sm.h2[which], which, k1[which]);
-  __syncthreads();
+  lds_barrier();
   const uint32_t hi = r_hi < 1 ? 0xFFFFFFFFu : (((d1[0] << 8) | sm.pick[0][0]) << 16) | 0xFFFFu;
   const uint32_t lo = r_lo > kSample ? 0u : ((d1[1] << 8) | sm.pick[1][0]) << 16;
   return make_uint2(lo, hi);
 }
 
 // K1, workgroup (r, s): span s of row r. The sample is loaded and the
-// bracket computed first; then the span's loads are issued (all of them:
-// a wave stalls at issue once the memory pipeline is full, so loads
-// issued before the bracket would hold it back) and each float4 is
-// classified as it arrives. V4: the row base is 16-byte aligned and
-// L % 4 == 0, so a lane's 4 tokens are one float4; otherwise four scalar
-// loads. Lane l of wave w holds tokens t_span + 4096 j + 256 w + 4 l .. + 3
+// bracket computed first, with the first kClsPre span loads per thread in
+// flight; the rest of the span streams through a window of kClsWin loads
+// per thread, each float4 classified as it arrives. V4: the row base is
+// 16-byte aligned and L % 4 == 0, so a lane's 4 tokens are one float4;
+// otherwise four scalar loads. Lane l of wave w holds tokens t_span + 4096 j + 256 w + 4 l .. + 3
 // for j < kClsPer; bitmask word t / 32 gets the nibbles of lanes 8g .. 8g
 // + 7, OR-ed together by 3 DPP steps.
 template <bool V4>
@@ -641,22 +657,19 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   float sv[SPER];
 #pragma unroll
   for (int j = 0; j < SPER; ++j) sv[j] = row[sample_token(tid + j * NT)];
-  const int32_t mphys = mark_page(ma, e0);
-  const uint32_t sink_key = order_key(1e38f);
-#pragma unroll
-  for (int j = 0; j < SPER; ++j) {
-    const int32_t i = tid + j * NT;
-    sm.skeys[i] = sample_token(i) < lr.sinks ? sink_key : order_key(sv[j]);
-  }
+  const int32_t mraw = mark_load(ma, e0);
   // The span is read through a window of kClsWin loads per thread: the
-  // first kClsPre fly during the bracket, and each later one is issued as a
-  // float4 is classified, so the data of all waves arrives interleaved with
-  // the classification instead of one wave's whole share after another's.
-  // With all 16 loads issued up front K1 took 29 us on config 5, with a
-  // window of 6 25.4-27.4 us, of 2 23.5 us. The loads are non-temporal: the
-  // scores are read once, and kept out of the caches they leave the INT4
-  // scale runs there for the apply launch (config 5 apply 50.3 -> 44.7 us
-  // over repeated calls).
+  // first kClsPre are issued right behind the sample (before anything
+  // waits for it) and fly during the bracket, whose barriers do not wait
+  // for them, and each later one is issued as a float4 is classified, so
+  // the data of all waves arrives interleaved with the classification
+  // instead of one wave's whole share after another's. With all 16 loads
+  // issued before the bracket K1 took 29 us on config 5, with a window of 6
+  // 25.4-27.4 us, of 2 23.5 us: a wave stalls at issue while the memory
+  // pipeline is full, which holds back the bracket. The loads are
+  // non-temporal: the scores are read once, and kept out of the caches they
+  // leave the INT4 scale runs there for the apply launch (config 5 apply
+  // 50.3 -> 44.7 us over repeated calls).
   const int32_t t_span = s * kSpan;
   auto load4 = [&](int j) __attribute__((always_inline)) {
     const int32_t t = t_span + 4 * (j * NT + tid);
@@ -673,15 +686,26 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   float4 v[kClsWin];
 #pragma unroll
   for (int j = 0; j < kClsPre; ++j) v[j] = load4(j);
+  // keeps the loads above in front of the first wait for the sample
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t sink_key = order_key(1e38f);
+#pragma unroll
+  for (int j = 0; j < SPER; ++j) {
+    const int32_t i = tid + j * NT;
+    const uint32_t k = order_key(sv[j]);
+    sm.skeys[i] = sample_token(i) < lr.sinks ? sink_key : k;
+  }
+  const int32_t mphys = mark_page(ma, e0, mraw);
   for (int i = tid; i < 256 * kRep; i += NT) (&sm.h1[0][0])[i] = 0;
   for (int i = tid; i < 2 * 256; i += NT) (&sm.h2[0][0])[i] = 0;
   if (tid == 0) sm.above = sm.ncand = 0;
-  __syncthreads();
+  lds_barrier();
   const uint2 br = sample_bracket<NT>(lr, sm);
   const uint32_t lo = br.x, hi = br.y;
 #pragma unroll
   for (int j = kClsPre; j < kClsWin; ++j) v[j] = load4(j);
   uint32_t *bits = lr.bits + (int64_t)r * lr.words;
+  const __amdgpu_buffer_rsrc_t brow = __builtin_amdgcn_make_buffer_rsrc(bits, (short)0, lr.words * 4, 0x00020000);
   // Sink tokens count with the key of a 1e38 score and are never evicted.
   const uint32_t sink_gt = sink_key > hi ? 0xFu : 0u, sink_in = sink_key >= lo && sink_key <= hi ? 0xFu : 0u;
   // The scores are compared with the floats whose keys are lo and hi: x <
@@ -760,7 +784,13 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
     e |= __builtin_bit_cast(uint32_t, dpp_f32<0xB1>(__builtin_bit_cast(float, e)));   // quad_perm [1,0,3,2]
     e |= __builtin_bit_cast(uint32_t, dpp_f32<0x4E>(__builtin_bit_cast(float, e)));   // quad_perm [2,3,0,1]
     e |= __builtin_bit_cast(uint32_t, dpp_f32<0x141>(__builtin_bit_cast(float, e)));  // row_half_mirror
-    if ((lane & 7) == 0 && word < lr.words) bits[word] = e;
+    // Every lane of the group of 8 holds the group's word, and all 8 store
+    // it (one write per address) through a buffer resource bounded by the
+    // row's words, which drops the words past the row: with no lane mask,
+    // every step issues exactly one store, so the compiler can count the
+    // window's loads exactly (a store under a lane mask may be skipped, and
+    // it would then wait for the newer load of the window as well).
+    __builtin_amdgcn_raw_buffer_store_b32(e, brow, word * 4, 0, 0);
   };
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -788,7 +818,8 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   // the page marks: this thread's first entry, then any further ones
   mark_check(ma, mphys, mold);
   for (int64_t e = e0 + nthr; e < ma.entries; e += nthr) mark_entry(ma, e);
-  __syncthreads();
+  // (the bitmask stores need not be complete for the list copy)
+  lds_barrier();
   // The wave lists, concatenated into the span's list.
   uint32_t off = 0, lost = 0;
 #pragma unroll
@@ -803,12 +834,14 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   if (tid == 0) lr.slot[(int64_t)r * lr.spans + s] = make_uint4(sm.above, sm.ncand | lost, lo, hi);
 }
 
-static constexpr int32_t kSpanLds = 64;  // spans whose list offsets K2 keeps in LDS
+static constexpr int32_t kSpanLds = 64;   // spans whose list offsets K2 keeps in LDS
+static constexpr int32_t kSpecSpans = 8;  // spans whose lists K2 loads before their counts
 
 struct ResolveLds {
   uint32_t lkey[kResCand], lpos[kResCand];
   SelectShared<kResNT> sh;
-  uint32_t hist12[4096], wsum[kResNT / 64], pick[2];  // select12
+  uint32_t hist12[4096], wsum[kResNT / 64], pick[3];  // select12: digit, rank left, bin count
+  uint32_t small[64], nsmall;                         // select12: the values of a small bin
   uint32_t lbits[kLdsWords];
   uint32_t cpre[kSpanLds + 1];  // list offsets of the spans (spans <= kSpanLds)
   uint32_t above, ncand, lost;
@@ -817,10 +850,13 @@ struct ResolveLds {
 
 // d of the k-th largest (1 <= k <= number of values) of the values d in
 // [0, range] handed out by visit(f) (every thread of the workgroup calls
-// it): 12-bit radix passes from the top bit of range (two passes for
-// range < 2^24) over one 4096-bin LDS histogram, which must be zero (and
-// visible to all threads) on entry. Thread t owns bins 4t .. 4t + 3 of
-// the suffix scan (NT = 1024).
+// it): 12-bit radix passes from the top bit of range. The first pass's
+// histogram (bin (d >> shift) for shift = max(bits(range) - 12, 0)) is
+// built by the caller in sm.hist12 and visible to all threads on entry.
+// When the bin a pass picks holds at most 64 values, they are gathered and
+// one wave ranks them (the k-th largest among them is the result) instead
+// of a further pass. sm.nsmall must be zero on entry. Thread t owns bins
+// 4t .. 4t + 3 of the suffix scan (NT = 1024).
 template <int NT, typename Visit>
 __device__ uint32_t select12(Visit visit, uint32_t k, uint32_t range, ResolveLds &sm) {
   static_assert(NT * 4 == 4096, "select12 takes 1024 threads");
@@ -829,17 +865,36 @@ __device__ uint32_t select12(Visit visit, uint32_t k, uint32_t range, ResolveLds
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nbits = range ? 32 - __builtin_clz(range) : 1;
   uint32_t prefix = 0, pmask = 0;
-  bool first = true;
-  for (int shift = max(nbits - 12, 0);; shift = max(shift - 12, 0)) {
-    if (!first) {  // the first pass's histogram is cleared by the caller
+  for (int shift = max(nbits - 12, 0), first = 1;; shift = max(shift - 12, 0), first = 0) {
+    if (!first) {
+      if (sm.pick[2] <= 64u) {
+        // the picked bin's values (d & pmask == prefix), ranked by wave 0
+        visit([&](uint32_t d) {
+          if ((d & pmask) == prefix) sm.small[atomicAdd(&sm.nsmall, 1u)] = d;
+        });
+        __syncthreads();
+        if (wave == 0) {
+          const uint32_t c = sm.pick[2];
+          const uint32_t mine = (uint32_t)lane < c ? sm.small[lane] : 0u;
+          uint32_t gt = 0, ge = 0;  // values above, resp. at or above, this lane's
+          for (uint32_t j = 0; j < c; ++j) {
+            const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)mine, (int)j);
+            gt += o > mine;
+            ge += o >= mine;
+          }
+          const uint64_t b = __ballot((uint32_t)lane < c && gt < k && k <= ge);
+          if (lane == 0) sm.pick[0] = (uint32_t)__builtin_amdgcn_readlane((int)mine, (int)__builtin_ctzll(b));
+        }
+        __syncthreads();
+        return sm.pick[0];
+      }
       for (int i = tid; i < 4096; i += NT) sm.hist12[i] = 0;
       __syncthreads();
+      visit([&](uint32_t d) {
+        if ((d & pmask) == prefix) atomicAdd(&sm.hist12[(d >> shift) & 0xFFFu], 1u);
+      });
+      __syncthreads();
     }
-    first = false;
-    visit([&](uint32_t d) {
-      if ((d & pmask) == prefix) atomicAdd(&sm.hist12[(d >> shift) & 0xFFFu], 1u);
-    });
-    __syncthreads();
     uint32_t c[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) c[j] = sm.hist12[4 * tid + j];
@@ -861,6 +916,7 @@ __device__ uint32_t select12(Visit visit, uint32_t k, uint32_t range, ResolveLds
       if (upto >= k && above < k) {
         sm.pick[0] = 4 * tid + j;
         sm.pick[1] = k - above;
+        sm.pick[2] = c[j];
       }
       above = upto;
     }
@@ -884,7 +940,10 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   const uint4 *slot = lr.slot + (int64_t)r * lr.spans;
   __shared__ ResolveLds sm;
   const uint32_t sink_key = order_key(1e38f);
-  if (tid == 0) sm.xabove = sm.xin = 0;
+  if (tid == 0) sm.xabove = sm.xin = sm.nsmall = 0;
+  // The first 64 spans' slots, loaded first (wave 0 scans them as soon as
+  // they arrive; a later load would have it wait for the ones below too).
+  const uint4 sl0 = slot[min(lane, lr.spans - 1)];
   // The row's first kLdsWords bitmask words (written by the classify
   // launch) are read now, for the merge at the end, and the merge's LDS
   // copy and the first select pass's histogram are cleared now.
@@ -892,13 +951,29 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   uint32_t bw[PW];
 #pragma unroll
   for (int k = 0; k < PW; ++k) bw[k] = bits[min(k * NT + tid, lr.words - 1)];
+  // With up to kSpecSpans spans, the first nq = kResCand / spans entries of
+  // every span's list are loaded now, with the counts (entries past a
+  // span's count are dropped), so the gather does not wait for the counts
+  // first. Entry v = k NT + tid of that sequence is entry v % nq of span
+  // v / nq.
+  const uint2 *gl0 = lr.cand + (int64_t)r * lr.spans * kSpanCand;
+  constexpr int KS = kResCand / NT;
+  const bool spec = lr.spans <= kSpecSpans;
+  const uint32_t nq = spec ? (uint32_t)(kResCand / lr.spans) : 1u;
+  // (loaded whatever spans is, in bounds, so that no branch joins them)
+  uint2 sc[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    const uint32_t v = k * NT + tid, q = min(v / nq, (uint32_t)lr.spans - 1);
+    sc[k] = gl0[(int64_t)q * kSpanCand + min(v - q * nq, (uint32_t)kSpanCand - 1)];
+  }
   for (int i = tid; i < kLdsWords; i += NT) sm.lbits[i] = 0;
   for (int i = tid; i < 4096; i += NT) sm.hist12[i] = 0;
   if (wave == 0) {  // the spans' counts, and their lists' offsets, 64 spans per step
     uint32_t a = 0, off = 0, l = 0;
     for (int32_t q0 = 0; q0 < lr.spans; q0 += 64) {
       const int32_t q = q0 + lane;
-      const uint4 sl = slot[min(q, lr.spans - 1)];
+      const uint4 sl = q0 == 0 ? sl0 : slot[min(q, lr.spans - 1)];
       const uint32_t c = q < lr.spans ? sl.y & ~kListLost : 0u;
       a += q < lr.spans ? sl.x : 0u;
       l |= q < lr.spans ? sl.y & kListLost : 0u;
@@ -925,24 +1000,42 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   }
   const uint4 s0 = slot[0];  // every span holds the row's bracket
   const uint32_t lo = s0.z, hi = s0.w;
-  __syncthreads();
+  lds_barrier();
   const uint32_t above = sm.above, nc = sm.ncand, keep = (uint32_t)lr.keep;
+  // first select pass: bins of (key - lo) >> shift1
+  const uint32_t range = hi - lo;
+  const int shift1 = max((range ? 32 - __builtin_clz(range) : 1) - 12, 0);
   if (above < keep && above + nc >= keep && nc <= (uint32_t)kResCand && !sm.lost) {
-    // The spans' candidate lists, 8 entries per thread in flight. The
-    // classify launch places a token by float compares with the floats of
-    // lo and hi; a score the compares cannot place (a NaN) is listed
-    // whatever its key: listed keys above hi count as kept, keys below lo
-    // are evicted, and the select runs over the keys in [lo, hi].
+    // The spans' candidate lists. The classify launch places a token by
+    // float compares with the floats of lo and hi; a score the compares
+    // cannot place (a NaN) is listed whatever its key: listed keys above
+    // hi count as kept, keys below lo are evicted, and the select runs over
+    // the keys in [lo, hi], whose first-pass histogram is built here.
     uint32_t xa = 0, xi = 0;
     auto take = [&](uint32_t e, uint2 c) {
       const uint32_t key = order_key(__builtin_bit_cast(float, c.x));
       sm.lkey[e] = key;
       sm.lpos[e] = c.y;
       xa += key > hi;
-      xi += key >= lo && key <= hi;
+      const bool in = key >= lo && key <= hi;
+      xi += in;
+      if (in) atomicAdd(&sm.hist12[(key - lo) >> shift1], 1u);
     };
-    const uint2 *gl0 = lr.cand + (int64_t)r * lr.spans * kSpanCand;
-    if (lr.spans <= kSpanLds) {
+    if (spec) {
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        // (keeps the key computation here, after the barrier: hoisted to
+        // the loads, it would make the code wait for them there)
+        asm volatile("" : "+v"(sc[k]));
+        const uint32_t v = k * NT + tid, q = v / nq, i = v - q * nq;
+        if (q < (uint32_t)lr.spans && i < sm.cpre[q + 1] - sm.cpre[q]) take(sm.cpre[q] + i, sc[k]);
+      }
+      // a span with more than nq candidates: the rest of its list
+      for (int32_t q = 0; q < lr.spans; ++q) {
+        const uint32_t cnt = sm.cpre[q + 1] - sm.cpre[q];
+        for (uint32_t i = nq + tid; i < cnt; i += NT) take(sm.cpre[q] + i, gl0[(int64_t)q * kSpanCand + i]);
+      }
+    } else if (lr.spans <= kSpanLds) {
       // all spans' entries as one sequence e = cpre[q] + i: unconditional
       // loads (index clamped), all in flight together
       for (uint32_t e0 = 0; e0 < nc; e0 += 8 * NT) {
