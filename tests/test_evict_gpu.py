@@ -176,6 +176,35 @@ def test_evict_tokens_signed_zero_ties(L):
     _evict_case("int4", N, H, L, 64, 0.5, 4, s)
 
 
+@pytest.mark.parametrize("kind", ["wide", "cluster", "wide_cluster"])
+def test_evict_tokens_long_rows_select_passes(kind):
+    """The resolve's exact select over the candidates in [lo, hi], a 12-bit
+    radix pass over key - lo, then either a pass over the picked bin or,
+    when that bin holds at most 64 keys, a ranking by one wave. wide: scores
+    spread log-uniformly over 200 octaves, so the bracket spans about 2^26
+    keys (bins of 2^15 keys, then the ranking). cluster: 300 tokens share
+    the score at the keep-th rank, so the picked bin holds more than 64 keys
+    and takes a second radix pass (a tie at tau: all 300 are kept).
+    wide_cluster: the wide row with 300 distinct scores within 1e-3 of the
+    keep-th one (a crowded first bin, a second pass, then the ranking)."""
+    rng = np.random.default_rng({"wide": 41, "cluster": 43, "wide_cluster": 47}[kind])
+    N, H, L, r = 1, 2, 70000, 0.75
+    if kind.startswith("wide"):
+        s = np.exp2(rng.uniform(-100, 100, size=(N, H, L))).astype(np.float32)
+    else:
+        s = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    if kind != "wide":
+        keep = int(np.ceil(np.float32(r) * np.float32(L)))
+        for h in range(H):
+            tau = np.sort(s[0, h])[::-1][keep - 1]
+            pos = rng.choice(np.arange(8, L), 300, replace=False)
+            if kind == "cluster":
+                s[0, h, pos] = tau
+            else:
+                s[0, h, pos] = (tau * (1 + rng.uniform(-1e-3, 1e-3, 300))).astype(np.float32)
+    _evict_case("int4", N, H, L, 64, r, 4, s)
+
+
 def test_evict_tokens_long_rows_span_counts():
     """Back-to-back long-row calls with 4, 1 and 2 spans per row and several
     rows: each row is resolved by whichever span finishes last, through
