@@ -757,6 +757,10 @@ __device__ __forceinline__ void buffer_load_lds16_m0(__amdgpu_buffer_rsrc_t r, u
                : "memory");
 }
 
+__device__ __forceinline__ half8_t lds_read16(uint32_t a) {
+  return *(const __attribute__((address_space(3))) half8_t *)a;
+}
+
 __device__ __forceinline__ uint32_t lds_u32(const void *p) {
   return __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p);
@@ -774,8 +778,8 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p) {
 //  * S^T = K Q^T and O^T += V^T P^T run on v_mfma_f32_32x32x16_f16. The S^T
 //    accumulator layout is the PV B-operand layout (the staged V^T columns
 //    are in that key order), so probabilities go from exp2 straight into
-//    the PV MFMAs. The running max enters the S chains as their initial
-//    accumulator (-m), so the MFMA returns score - m.
+//    the PV MFMAs. The S chains start from zero; the running max enters
+//    each exp2 argument as one fma, cs s - cs m.
 //  * Iteration i holds S(i) (computed by iteration i - 1) and interleaves
 //      QK(i+1) block 0 MFMAs  with the running max of S(i),
 //      QK(i+1) block 1 MFMAs  with exp2 / packing of S(i) block 0,
@@ -839,8 +843,11 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   for (int i = 0; i < NDB; ++i) o[i] = (float16_t){};
   // Row sums of the probabilities, one per 32-key block: two independent
   // chains of 8 dependent v_dot2 per tile instead of one chain of 16.
-  float m = -INFINITY, lsum = 0.0f, lsum1 = 0.0f;
-  float16_t mtile = (float16_t){};
+  // The S accumulators hold raw scores q.k; the running max m enters each
+  // exp2 argument through one fma, cs s + ncm with ncm = -cs m (0 while m is
+  // -inf), so raising m touches no held score and no registers carry a -m
+  // splat for the MFMA chains to start from.
+  float m = -INFINITY, ncm = 0.0f, lsum = 0.0f, lsum1 = 0.0f;
 
   const int32_t qlast = min(q0 + 32 * NW, p.Lq) - 1;
   const int32_t pos_lo = ctx - p.Lq + q0, pos_hi = ctx - p.Lq + qlast;
@@ -924,9 +931,19 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   int32_t ka[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) ka[c] = (lane & 31) * KRB + 16 * ((2 * c + hl) ^ kswz(lane & 31));
-  int32_t va[4];
+  // LDS byte addresses of this lane's V^T fragments in each V buffer, held
+  // in registers (the empty asm hides their values from the compiler). The
+  // second buffer lies above the 16-bit ds_read offset range: without a
+  // register base per fragment the compiler rebuilds each address with a
+  // v_or and the reads of that buffer lose their four-deep prefetch.
+  uint32_t vb[2][4];
 #pragma unroll
-  for (int kc = 0; kc < 4; ++kc) va[kc] = (lane & 31) * VRB + 16 * ((2 * kc + hl) ^ (((lane & 31) >> 1) & 7));
+  for (int kc = 0; kc < 4; ++kc) {
+    const uint32_t va = (uint32_t)((lane & 31) * VRB + 16 * ((2 * kc + hl) ^ (((lane & 31) >> 1) & 7)));
+    vb[0][kc] = lds_u32(lds_v0) + va;
+    vb[1][kc] = lds_u32(lds_v1) + va;
+    asm volatile("" : "+v"(vb[0][kc]), "+v"(vb[1][kc]));
+  }
 
   // Hidden (key, query) slots of S(i) become -inf. Slot r of block blk of
   // this lane holds key tb + 32 blk + 16(r/8) + 4((r/4)%2) + (r/2)%2 + 8(r%2) + 2 hl.
@@ -959,37 +976,20 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   };
   // Lazy running max (raw score units): rescale only when cs (score - m)
   // exceeds 8, i.e. a probability would exceed 2^8; the first visible key
-  // always raises. S values held in
-  // `s` and in the nblk_next blocks of `nx` (scores of the next tile already
-  // computed against the old m) are moved to the new m.
-  auto raise_max = [&](float tmax, float16_t (&s)[2], float16_t (&nx)[2], int nblk_next) __attribute__((always_inline)) {
-    const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : (tmax * cs > 8.0f);
+  // always raises.
+  auto raise_max = [&](float tmax) __attribute__((always_inline)) {
+    const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : ((tmax - m) * cs > 8.0f);
     if (__any(raise)) {
-      const float base = (m == -INFINITY) ? 0.0f : m;
-      const float mn = fmaxf(m, base + tmax);
+      const float mn = fmaxf(m, tmax);
       const float alpha = (mn == m) ? 1.0f : fast_exp2((m - mn) * cs);
-      const float delta = (mn == -INFINITY) ? 0.0f : mn - base;
       lsum *= alpha;
       lsum1 *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[0][r] -= delta;
-        s[1][r] -= delta;
-      }
-      if (nblk_next > 0)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) nx[0][r] -= delta;
-      if (nblk_next > 1)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) nx[1][r] -= delta;
       m = mn;
-      const float nb = (mn == -INFINITY) ? 0.0f : -mn;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mtile[r] = nb;
+      ncm = (mn == -INFINITY) ? 0.0f : -mn * cs;
     }
   };
   const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
@@ -1000,25 +1000,37 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     uint32_t w[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      w[i] = as_u32(half2_t{(half_t)fast_exp2(s[2 * i] * cs), (half_t)fast_exp2(s[2 * i + 1] * cs)});
+      w[i] = as_u32(half2_t{(half_t)fast_exp2(fmaf(s[2 * i], cs, ncm)),
+                            (half_t)fast_exp2(fmaf(s[2 * i + 1], cs, ncm))});
 #pragma unroll
     for (int i = 0; i < 8; ++i) ls = __builtin_amdgcn_fdot2(as_half2(w[i]), ones, ls, false);
     pb[0] = __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
     pb[1] = __builtin_bit_cast(half8_t, make_uint4(w[4], w[5], w[6], w[7]));
   };
-  auto qk_block = [&](const uint8_t *kt, int blk, float16_t &acc) __attribute__((always_inline)) {
+  // Operand fragments: K chunk c of a 32-key block; V^T fragment i of a
+  // 32-key block in PV order (dim block i / 2, 16-key half i % 2).
+  auto kfrag = [&](const uint8_t *kt, int blk, int c) __attribute__((always_inline)) {
+    return *reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]);
+  };
+  auto vfrag = [&](auto vbufc, int blk, int i) __attribute__((always_inline)) {
+    return lds_read16(vb[decltype(vbufc)::value][2 * blk + (i & 1)] + 32 * (i >> 1) * VRB);
+  };
+  // A segment's first four fragments come from `pre` when the previous
+  // segment read them (PRE = 1) during its last MFMAs, so the copies and
+  // bookkeeping between segments overlap their LDS latency.
+  auto qk_block = [&](const uint8_t *kt, int blk, float16_t &acc, auto prec, const half8_t (&pre)[4])
+                      __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8_t *>(kt + 32 * blk * KRB + ka[c]),
-                                                   qf[c], c == 0 ? mtile : acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16((decltype(prec)::value && c < 4) ? pre[c] : kfrag(kt, blk, c),
+                                                   qf[c], c == 0 ? (float16_t){} : acc, 0, 0, 0);
   };
-  auto pv_block = [&](const uint8_t *vt, int blk, const half8_t (&pb)[2]) __attribute__((always_inline)) {
+  auto pv_block = [&](auto vbufc, int blk, const half8_t (&pb)[2], const half8_t (&pre)[4])
+                      __attribute__((always_inline)) {
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int g2 = 0; g2 < 2; ++g2)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            *reinterpret_cast<const half8_t *>(vt + 32 * db * VRB + va[2 * blk + g2]), pb[g2], o[db], 0, 0, 0);
+    for (int i = 0; i < 2 * NDB; ++i)
+      o[i >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(i < 4 ? pre[i] : vfrag(vbufc, blk, i), pb[i & 1], o[i >> 1],
+                                                         0, 0, 0);
   };
 
   float16_t sx[2], sy[2];
@@ -1034,8 +1046,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     } else {
       fl_cur = publish(0, IntC<0>{});
     }
-    qk_block(lds_k0, 0, sx[0]);
-    qk_block(lds_k0, 1, sx[1]);
+    const half8_t none[4] = {};
+    qk_block(lds_k0, 0, sx[0], IntC<0>{}, none);
+    qk_block(lds_k0, 1, sx[1], IntC<0>{}, none);
     __syncthreads();  // K(0)'s buffer is refilled by the first iteration
   }
 
@@ -1048,7 +1061,6 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     constexpr int K3 = decltype(k3c)::value, V2 = decltype(v2c)::value;
     constexpr int KR = (K3 + 1) % 3;
     const uint8_t *const kt = KR == 0 ? lds_k0 : KR == 1 ? lds_k1 : lds_k2;
-    const uint8_t *const vt = V2 ? lds_v1 : lds_v0;
     const int32_t tb = tile_base(it);
     const bool v_ahead = it + 1 < n_tiles, k_ahead = it + 3 < n_tiles;
     if (v_ahead) load_v(it + 1, IntC<V2 ^ 1>{}, 0, NVL / 2);
@@ -1065,28 +1077,35 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       // wait at the normal one, so of the two waves sharing a SIMD the one
       // with MFMAs to issue wins the arbitration (measured ~0.7 % faster).
       __builtin_amdgcn_s_setprio(1);
-      qk_block(kt, 0, sn[0]);
+      const half8_t none[4] = {};
+      half8_t pre_k[4], pre_a[4], pre_b[4];
+      qk_block(kt, 0, sn[0], IntC<0>{}, none);
       const float tmax = row_max(sc);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) pre_k[c] = kfrag(kt, 1, c);
+      // Each MFMA is followed by one read: this block's last four
+      // fragments, then the next segment's first four.
       PIPE_SGB(0x100, 4, 0);
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         PIPE_SGB(0x008, 1, 0);
-        if (c + 4 < NCH) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x100, 1, 0);
         PIPE_SGB(0x002, 2, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      raise_max(tmax, sc, sn, 1);
+      raise_max(tmax);
       if (v_ahead) load_v(it + 1, IntC<V2 ^ 1>{}, NVL / 2, NVL);
       // Seg 2: QK(i+1) block 1 | probabilities of S(i) block 0
       half8_t pa[2], pb[2];
-      qk_block(kt, 1, sn[1]);
+      qk_block(kt, 1, sn[1], IntC<1>{}, pre_k);
       probs(sc[0], pa, lsum);
-      PIPE_SGB(0x100, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pre_a[i] = vfrag(IntC<V2>{}, 0, i);
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         PIPE_SGB(0x008, 1, 0);
-        if (c + 4 < NCH) PIPE_SGB(0x100, 1, 0);
-        PIPE_SGB(0x002, 32 / NCH, 0);  // per exp2: a scale multiply, half a pack, half a row-sum dot
+        PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x002, 32 / NCH, 0);  // per exp2: a scale fma, half a pack, half a row-sum dot
         PIPE_SGB(0x400, 16 / NCH, 0);
       }
       // The probabilities must be complete here: without this use the
@@ -1097,13 +1116,14 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       // K copies go last: the end-of-tile wait leaves the newest NKL in flight.
       if (k_ahead) load_k(it + 3, IntC<K3>{}, 0, NKL / 2);
       // Seg 3: PV(i) block 0 | probabilities of S(i) block 1
-      pv_block(vt, 0, pa);
+      pv_block(IntC<V2>{}, 0, pa, pre_a);
       probs(sc[1], pb, lsum1);
-      PIPE_SGB(0x100, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pre_b[i] = vfrag(IntC<V2>{}, 1, i);
 #pragma unroll
       for (int c = 0; c < 2 * NDB; ++c) {
         PIPE_SGB(0x008, 1, 0);
-        if (c + 4 < 2 * NDB) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x100, 1, 0);
         PIPE_SGB(0x002, 32 / (2 * NDB), 0);
         PIPE_SGB(0x400, 16 / (2 * NDB), 0);
       }
@@ -1111,12 +1131,11 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       __builtin_amdgcn_sched_barrier(0);
       if (k_ahead) load_k(it + 3, IntC<K3>{}, NKL / 2, NKL);
       // Seg 4: PV(i) block 1
-      pv_block(vt, 1, pb);
-      PIPE_SGB(0x100, 4, 0);
+      pv_block(IntC<V2>{}, 1, pb, pre_b);
 #pragma unroll
       for (int c = 0; c < 2 * NDB; ++c) {
         PIPE_SGB(0x008, 1, 0);
-        if (c + 4 < 2 * NDB) PIPE_SGB(0x100, 1, 0);
+        if (c < 4) PIPE_SGB(0x100, 1, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(0);
