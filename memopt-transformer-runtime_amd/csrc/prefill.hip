@@ -848,6 +848,10 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   // -inf), so raising m touches no held score and no registers carry a -m
   // splat for the MFMA chains to start from.
   float m = -INFINITY, ncm = 0.0f, lsum = 0.0f, lsum1 = 0.0f;
+  // Raise threshold in raw score units, m + 8 / cs (-inf until the first
+  // visible key), so the per-tile test is one compare.
+  const float thr_off = 8.0f / cs;
+  float thr = -INFINITY;
 
   const int32_t qlast = min(q0 + 32 * NW, p.Lq) - 1;
   const int32_t pos_lo = ctx - p.Lq + q0, pos_hi = ctx - p.Lq + qlast;
@@ -978,8 +982,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   // exceeds 8, i.e. a probability would exceed 2^8; the first visible key
   // always raises.
   auto raise_max = [&](float tmax) __attribute__((always_inline)) {
-    const bool raise = (m == -INFINITY) ? (tmax != -INFINITY) : ((tmax - m) * cs > 8.0f);
-    if (__any(raise)) {
+    if (__any(tmax > thr)) {
       const float mn = fmaxf(m, tmax);
       const float alpha = (mn == m) ? 1.0f : fast_exp2((m - mn) * cs);
       lsum *= alpha;
@@ -990,6 +993,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
       m = mn;
       ncm = (mn == -INFINITY) ? 0.0f : -mn * cs;
+      thr = mn + thr_off;
     }
   };
   const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
