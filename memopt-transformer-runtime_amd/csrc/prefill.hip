@@ -872,9 +872,6 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   // each tile pays two compares instead of re-deriving it.
   const int32_t full_lo = causal ? wpos_hi - p.W + 1 : ctx - p.W;
   const int32_t full_hi = wq_last != qw0 + 31 ? INT32_MIN : min(kv_lim - TK, causal ? wpos_lo - TK + 1 : INT32_MAX);
-  auto tile_full = [&](int32_t tb, int4 fl) {
-    return (fl.x & fl.y & fl.z & fl.w) != 0 && tb >= full_lo && tb <= full_hi;
-  };
 
   const int32_t *vrow = reinterpret_cast<const int32_t *>(ws + (int64_t)units * L::kBlock) + (int64_t)b * MC;
   const StageMap sm = stage_map(ctx, p.M * p.bs, p.Lq, p.W, p.sinks, causal);
@@ -884,6 +881,29 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   // every copy and flag load of every tile).
   const int32_t slot_w = n_tiles > sink_tiles ? sm.slot(4 * t_first) - 4 * sink_tiles : 0;
   auto tile_slot = [&](int32_t it) { return (uint32_t)(4 * it + (it < sink_tiles ? 0 : slot_w)); };
+  // A tile skips the mask when all its (key, query) slots are visible and
+  // its four chunks are linked. The fully visible tiles of this wave form
+  // one run of iterations (tile bases grow with the iteration),
+  // [it_full, it_full + n_full), found once here; links are checked once
+  // for every chunk the workgroup visits. In a workgroup with an unlinked
+  // chunk every tile takes the mask, which loads the link flags itself, so
+  // the common path carries no flag loads.
+  int32_t it_full = 0, n_full = 0;
+  {
+    bool first = true;
+    for (int32_t base = 0; base < n_tiles; base += 64) {
+      const int32_t it = base + lane, tb = tile_base(it);
+      const uint64_t fm = __ballot(it < n_tiles && tb >= full_lo && tb <= full_hi);
+      if (fm != 0) {
+        if (first) it_full = base + __builtin_ctzll(fm);
+        first = false;
+        n_full = base + 63 - __builtin_clzll(fm) + 1 - it_full;
+      }
+    }
+    int unlinked = 0;
+    for (int32_t i = lane; i < 4 * n_tiles; i += 64) unlinked |= vrow[tile_slot(i >> 2) + (i & 3)] == 0;
+    if (__any(unlinked)) n_full = 0;
+  }
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(ws + ((int64_t)b * p.H + h) * MC * L::kBlock), (short)0, (int)(MC * CS), 0x00020000);
   uint32_t kvoff, vvoff;
@@ -915,21 +935,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       buffer_load_lds16_m0(rs, (buf ? mv1 : mv0) + cl * NT * 16, vvoff, cb + cl * NT * 4);
   };
   // End of a tile: wait for this thread's tile copies except the newest
-  // `keep` (the K prefetch, which has another tile of time), and for its LDS
-  // reads; fetch the linked flags of the next tile's four chunks with one
-  // scalar load inside the same wait (the value is complete when the asm
-  // returns); then the barrier publishes the copies of all threads.
-  auto publish = [&](int32_t next_it, auto keepc) __attribute__((always_inline)) {
-    constexpr int keep = decltype(keepc)::value;
-    const int32_t *fp = vrow + (next_it < n_tiles ? tile_slot(next_it) : 0);
-    int4 f;
-    if constexpr (keep == 0)
-      asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt vmcnt(0) lgkmcnt(0)" : "=s"(f) : "s"(fp) : "memory");
-    else
-      asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt vmcnt(%2) lgkmcnt(0)"
-                   : "=s"(f) : "s"(fp), "n"(keep) : "memory");
+  // `keep` (the K prefetch, which has another tile of time) and for its LDS
+  // reads (the next copies overwrite buffers read in this tile); then the
+  // barrier publishes the copies of all threads.
+  auto publish = [&](auto keepc) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(decltype(keepc)::value) : "memory");
     __syncthreads();
-    return f;
   };
 
   int32_t ka[NCH];
@@ -951,7 +962,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
 
   // Hidden (key, query) slots of S(i) become -inf. Slot r of block blk of
   // this lane holds key tb + 32 blk + 16(r/8) + 4((r/4)%2) + (r/2)%2 + 8(r%2) + 2 hl.
-  auto apply_mask = [&](float16_t (&s)[2], int32_t tb, int4 fl) __attribute__((always_inline)) {
+  auto apply_mask = [&](float16_t (&s)[2], int32_t tb, int32_t it) __attribute__((always_inline)) {
+    int4 fl;  // link flags of the four chunks (a scalar load: the address is uniform)
+    asm volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(fl) : "s"(vrow + tile_slot(it)) : "memory");
     const int32_t kb = tb + 2 * hl;
     const int32_t rl = vis_lo - kb, rsk = p.sinks - kb;
 #pragma unroll
@@ -1038,7 +1051,6 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   };
 
   float16_t sx[2], sy[2];
-  int4 fl_cur = {};
   if (n_tiles > 0) {
     // K(0), V(0), K(1), K(2) in that order; K(2) may stay in flight.
     load_k(0, IntC<0>{}, 0, NKL);
@@ -1046,9 +1058,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     if (n_tiles > 1) load_k(1, IntC<1>{}, 0, NKL);
     if (n_tiles > 2) {
       load_k(2, IntC<2>{}, 0, NKL);
-      fl_cur = publish(0, IntC<NKL>{});
+      publish(IntC<NKL>{});
     } else {
-      fl_cur = publish(0, IntC<0>{});
+      publish(IntC<0>{});
     }
     const half8_t none[4] = {};
     qk_block(lds_k0, 0, sx[0], IntC<0>{}, none);
@@ -1072,7 +1084,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     // covers tiles this wave sees nothing of (all slots -inf: P = 0, O and
     // the row sum unchanged). S(i+1) of the last iteration is computed from
     // stale LDS and never read.
-    if (!tile_full(tb, fl_cur)) apply_mask(sc, tb, fl_cur);
+    if ((uint32_t)(it - it_full) >= (uint32_t)n_full) apply_mask(sc, tb, it);
     {
       // Operand fragments stream 4 ahead of the MFMA that uses them (the
       // scheduling groups below keep at most 4 in flight).
@@ -1144,8 +1156,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(0);
     }
-    if (k_ahead) fl_cur = publish(it + 1, IntC<NKL>{});
-    else fl_cur = publish(it + 1, IntC<0>{});
+    if (k_ahead) publish(IntC<NKL>{});
+    else publish(IntC<0>{});
   };
   // Unrolled by six: buffer indices (mod 3 for K, mod 2 for V and the
   // score registers) stay compile-time constants.
