@@ -65,6 +65,39 @@ def test_prefill_int4_pages_vs_composition_oracle(case):
     assert_close(got, want, what=str(case))
 
 
+@pytest.mark.parametrize("D,int4", [(64, False), (128, False), (128, True)])
+def test_prefill_running_max_raised_every_tile(D, int4):
+    """Keys that grow along a common direction make every query's scores
+    climb about 9.6 log2 units per 64 keys, so the lazy running max (raised
+    only when a score passes it by more than 8 log2 units) rises in every
+    tile and the rescale of the held output and row sums runs tile after
+    tile; the first keys' weights fall to zero in fp16 along the way."""
+    B, H, bs, ctx = 1, 2, 16, 640
+    rng = np.random.default_rng(31)
+    u = np.ones(D) / np.sqrt(D)
+    t = np.arange(ctx)
+    # q . k_t = 30 * 25 * t / ctx raw; 0.1275 log2 units per raw unit at D = 128
+    k_rows = (25.0 * t / ctx)[:, None] * u[None, :] + 0.05 * rng.standard_normal((ctx, D))
+    nb = ctx // bs + 2
+    kp = np.zeros((nb, bs, H, D), np.float16)
+    vp = rng.standard_normal((nb, bs, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:ctx // bs].reshape(1, -1).astype(np.int32)
+    for j in range(ctx // bs):
+        kp[bt[0, j]] = k_rows[j * bs:(j + 1) * bs, None, :].astype(np.float16)
+    q = (30.0 * u[None, None, None, :] + 0.05 * rng.standard_normal((B, ctx, H, D))).astype(np.float16)
+    cl = np.array([ctx], np.int32)
+    if int4:
+        pages = O.to_int4_pages(kp, vp)
+        want = O.paged_attention_int4(q, pages, bt, cl, ctx, ctx, num_sink_tokens=4, causal=True)
+        kc = vc = to_dev(pages)
+    else:
+        want = O.paged_attention(q, kp, vp, bt, cl, ctx, ctx, num_sink_tokens=4, causal=True)
+        kc, vc = to_dev(kp), to_dev(vp)
+    got = memopt_C.dynamic_sparse_attention(to_dev(q), kc, vc, to_dev(bt), to_dev(cl), ctx, ctx,
+                                            num_sink_tokens=4, causal=True)
+    assert_close(got, want, what=f"climbing scores D={D} int4={int4}")
+
+
 def test_prefill_out_of_pool_pages_are_skipped():
     """Block-table entries >= num_blocks contribute no keys, like entries < 0."""
     B, H, D, bs, ctx, Lq = 1, 2, 64, 16, [96], 96
