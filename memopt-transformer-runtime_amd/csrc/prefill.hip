@@ -749,16 +749,47 @@ struct IntC {
 // read; nothing is clobbered behind its back. The s_nop is the one wait
 // state the hardware needs between an SALU write of m0 and an LDS DMA that
 // reads it.
-__device__ __forceinline__ void buffer_load_lds16_m0(__amdgpu_buffer_rsrc_t r, uint32_t m0v, uint32_t voff,
-                                                     uint32_t soff) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voff), "s"(r), "s"(soff), "{m0}"(m0v)
-               : "memory");
+//
+// lds_dma<C0, N> issues copies C0 .. C0 + N - 1 (N = 1 or 2) of one group
+// that shares m0 and the scalar offset: copy c carries the immediate offset
+// c * 1024, which the hardware adds to both the global and the LDS address
+// (measured on MI355X), and the lane offset vo[c] holds the rest of its
+// global address minus that immediate. So a group of copies needs one m0
+// write and one wait state instead of one of each per copy.
+template <int C0, int N>
+__device__ __forceinline__ void lds_dma(__amdgpu_buffer_rsrc_t r, uint32_t m0v, const uint32_t *vo, uint32_t soff) {
+  static_assert(N == 1 || N == 2, "one or two copies per group");
+  static_assert((C0 + N) * 1024 <= 4096, "immediate offsets are 12 bits");
+  if constexpr (N == 1) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen offset:%4 lds"
+                 :
+                 : "v"(vo[C0]), "s"(r), "s"(soff), "{m0}"(m0v), "i"(C0 * 1024)
+                 : "memory");
+  } else {
+    asm volatile(
+        "s_nop 0\n\tbuffer_load_dwordx4 %0, %2, %3 offen offset:%5 lds\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen offset:%6 lds"
+        :
+        : "v"(vo[C0]), "v"(vo[C0 + 1]), "s"(r), "s"(soff), "{m0}"(m0v), "i"(C0 * 1024), "i"(C0 * 1024 + 1024)
+        : "memory");
+  }
 }
 
+// Copies [C0, C1) of a group, two per m0 write.
+template <int C0, int C1>
+__device__ __forceinline__ void lds_dma_range(__amdgpu_buffer_rsrc_t r, uint32_t m0v, const uint32_t *vo,
+                                              uint32_t soff) {
+  if constexpr (C1 - C0 == 1) {
+    lds_dma<C0, 1>(r, m0v, vo, soff);
+  } else if constexpr (C1 - C0 >= 2) {
+    lds_dma<C0, 2>(r, m0v, vo, soff);
+    lds_dma_range<C0 + 2, C1>(r, m0v, vo, soff);
+  }
+}
+
+// ds_read_b128 at LDS byte address a.
 __device__ __forceinline__ half8_t lds_read16(uint32_t a) {
-  return *(const __attribute__((address_space(3))) half8_t *)a;
+  return *(const __attribute__((address_space(3))) half8_t *)(uintptr_t)a;
 }
 
 __device__ __forceinline__ uint32_t lds_u32(const void *p) {
@@ -803,7 +834,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   using L = StageLayout<D>;
   constexpr uint32_t CS = (uint32_t)L::kBlock;  // bytes per staged chunk
   // Three K buffers and two V buffers: 160 KiB for the two workgroups of a CU at D = 128.
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k0[KBUF], lds_k1[KBUF], lds_k2[KBUF];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k0[KBUF], lds_k1[KBUF];
   __shared__ __attribute__((aligned(16))) uint8_t lds_v0[VBUF], lds_v1[VBUF];
 
   auto kswz = [](int R) { return KC == 16 ? (R & 15) : ((R >> 1) & 7); };
@@ -904,35 +935,70 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     for (int32_t i = lane; i < 4 * n_tiles; i += 64) unlinked |= vrow[tile_slot(i >> 2) + (i & 3)] == 0;
     if (__any(unlinked)) n_full = 0;
   }
+  // Tiles this wave computes: the sink tiles (when it has a query) and the
+  // window iterations [it_v0, it_v1) holding keys of its queries' windows.
+  // The workgroup visits the union over its four waves; a wave skips the
+  // MFMAs and softmax of the tiles it sees nothing of (it still copies and
+  // meets the barriers), and computes no S for the iteration after its last.
+  const bool any_q = qw0 < p.Lq;
+  int32_t it_v0 = sink_tiles, it_v1 = sink_tiles;
+  bool win_in_tile0 = false;
+  {
+    const int32_t klo = max(0, causal ? wpos_lo - p.W + 1 : ctx - p.W);
+    const int32_t khi = causal ? min(wpos_hi, kv_lim - 1) : kv_lim - 1;
+    if (any_q && khi >= klo) {
+      it_v1 = min(n_tiles, sink_tiles + max(0, khi / TK - t_first + 1));
+      it_v0 = min(it_v1, sink_tiles + max(0, klo / TK - t_first));
+      win_in_tile0 = klo < TK;
+    }
+  }
+  // A sink tile whose visible keys all lie in its first 32 (16) keys: only
+  // its first S block (and its first 16-key half of the PV contraction).
+  const bool sink_half = any_q && sink_tiles == 1 && sink_end <= 32 && !win_in_tile0;
+  const bool sink_quarter = sink_half && sink_end <= 16;
+  auto wave_vis = [&](int32_t it) { return it < sink_tiles ? any_q : (it >= it_v0 && it < it_v1); };
+  // Iterations [c0, c1) take the pipelined body: S(i) and S(i+1) both
+  // visible, not the half sink tile. The rest (the wave's first and last
+  // tiles, tiles it skips) take a plain body.
+  int32_t c0 = 0, c1 = 0;
+  if (any_q) {
+    c0 = it_v0 == sink_tiles ? (sink_half ? 1 : 0) : it_v0;
+    c1 = max(c0, it_v1 - 1);
+  }
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(ws + ((int64_t)b * p.H + h) * MC * L::kBlock), (short)0, (int)(MC * CS), 0x00020000);
-  uint32_t kvoff, vvoff;
-  {
-    const int r = (tid / KC) & 15, j = (tid % KC) ^ kswz(tid / KC);
-    kvoff = (uint32_t)(r * KRB + 16 * j);
-    const int jv = (tid & 7) ^ ((tid >> 4) & 7);
-    vvoff = (uint32_t)(jv >> 1) * CS + (uint32_t)((tid >> 3) * 32 + 16 * (jv & 1));
+  // Tile copies: wave w fills NKL contiguous KiB of a K buffer (the K-tile
+  // rows of chunk w) and NVL contiguous KiB of a V^T buffer (rows
+  // [8 NVL w, 8 NVL (w + 1))), 1 KiB per copy, lane i writing LDS bytes
+  // 16 i .. 16 i + 15 of it. Copy c of a tile reads the tile's first chunk
+  // (scalar offset) + c * 1024 (immediate, also applied to the LDS address)
+  // + kvo[c] / vvo[c]: the lane's row, swizzled 16-byte piece and chunk.
+  constexpr int RPC = 1024 / KRB;  // K-tile rows per copy
+  uint32_t kvo[NKL], vvo[NVL];
+#pragma unroll
+  for (int c = 0; c < NKL; ++c) {
+    const int R = wave * NKL * RPC + c * RPC + lane / KC, j = (lane % KC) ^ kswz(R);
+    kvo[c] = (uint32_t)((R / 16) * (int)CS + (R % 16) * KRB + 16 * j - c * 1024);
   }
-  const uint32_t wofs = (uint32_t)wave * 64 * 16;
-  const uint32_t mk0 = lds_u32(lds_k0) + wofs, mk1 = lds_u32(lds_k1) + wofs, mk2 = lds_u32(lds_k2) + wofs;
-  const uint32_t mv0 = lds_u32(lds_v0) + wofs, mv1 = lds_u32(lds_v1) + wofs;
-  // Copies cl in [c0, c1) of a tile's K (V) part; a tile is split over the
+#pragma unroll
+  for (int c = 0; c < NVL; ++c) {
+    const int d = wave * NVL * 8 + c * 8 + lane / 8, jv = (lane & 7) ^ ((d >> 1) & 7);
+    vvo[c] = (uint32_t)((jv >> 1) * (int)CS + (int)L::kVPart + d * 32 + 16 * (jv & 1) - c * 1024);
+  }
+  const uint32_t wk = (uint32_t)wave * NKL * 1024, wv = (uint32_t)wave * NVL * 1024;
+  const uint32_t mk0 = lds_u32(lds_k0) + wk, mk1 = lds_u32(lds_k1) + wk;
+  const uint32_t mv0 = lds_u32(lds_v0) + wv, mv1 = lds_u32(lds_v1) + wv;
+  // Copies [C0, C1) of a tile's K (V) part; a tile is split over the
   // segments of an iteration so the copies are not issued in one burst.
-  auto load_k = [&](int32_t it, auto bufc, int c0, int c1) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    const uint32_t cb = tile_slot(it) * CS;
-#pragma unroll
-    for (int cl = c0; cl < c1; ++cl) {
-      const uint32_t k = (uint32_t)(cl * NT + wave * 64) / (16 * KC);
-      buffer_load_lds16_m0(rs, (buf == 2 ? mk2 : buf ? mk1 : mk0) + cl * NT * 16, kvoff, cb + k * CS);
-    }
+  auto load_k = [&](int32_t it, auto bufc, auto c0c, auto c1c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value, C0 = decltype(c0c)::value, C1 = decltype(c1c)::value;
+    const uint32_t m0v = buf ? mk1 : mk0, soff = tile_slot(it) * CS;
+    lds_dma_range<C0, C1>(rs, m0v, kvo, soff);
   };
-  auto load_v = [&](int32_t it, auto bufc, int c0, int c1) __attribute__((always_inline)) {
-    constexpr int buf = decltype(bufc)::value;
-    const uint32_t cb = tile_slot(it) * CS + (uint32_t)L::kVPart;
-#pragma unroll
-    for (int cl = c0; cl < c1; ++cl)
-      buffer_load_lds16_m0(rs, (buf ? mv1 : mv0) + cl * NT * 16, vvoff, cb + cl * NT * 4);
+  auto load_v = [&](int32_t it, auto bufc, auto c0c, auto c1c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value, C0 = decltype(c0c)::value, C1 = decltype(c1c)::value;
+    const uint32_t m0v = buf ? mv1 : mv0, soff = tile_slot(it) * CS;
+    lds_dma_range<C0, C1>(rs, m0v, vvo, soff);
   };
   // End of a tile: wait for this thread's tile copies except the newest
   // `keep` (the K prefetch, which has another tile of time) and for its LDS
@@ -1052,38 +1118,31 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
 
   float16_t sx[2], sy[2];
   if (n_tiles > 0) {
-    // K(0), V(0), K(1), K(2) in that order; K(2) may stay in flight.
-    load_k(0, IntC<0>{}, 0, NKL);
-    load_v(0, IntC<0>{}, 0, NVL);
-    if (n_tiles > 1) load_k(1, IntC<1>{}, 0, NKL);
-    if (n_tiles > 2) {
-      load_k(2, IntC<2>{}, 0, NKL);
-      publish(IntC<NKL>{});
-    } else {
-      publish(IntC<0>{});
-    }
+    load_k(0, IntC<0>{}, IntC<0>{}, IntC<NKL>{});
+    load_v(0, IntC<0>{}, IntC<0>{}, IntC<NVL>{});
+    if (n_tiles > 1) load_k(1, IntC<1>{}, IntC<0>{}, IntC<NKL>{});
+    publish(IntC<0>{});
     const half8_t none[4] = {};
-    qk_block(lds_k0, 0, sx[0], IntC<0>{}, none);
-    qk_block(lds_k0, 1, sx[1], IntC<0>{}, none);
+    sx[1] = (float16_t){};
+    if (wave_vis(0)) {
+      qk_block(lds_k0, 0, sx[0], IntC<0>{}, none);
+      if (!sink_half) qk_block(lds_k0, 1, sx[1], IntC<0>{}, none);
+    }
     __syncthreads();  // K(0)'s buffer is refilled by the first iteration
   }
 
-  // Iteration `it` with S(it) in `sc` and S(it + 1) computed into `sn`.
-  // K(it+1) is read from buffer (it+1) % 3 and K(it+3) loaded into buffer
-  // it % 3 (last read for QK(it) in iteration it - 1); V(it) is read from
-  // buffer it % 2 and V(it+1) loaded into buffer (it+1) % 2.
-  auto iter = [&](int32_t it, float16_t (&sc)[2], float16_t (&sn)[2], auto k3c, auto v2c)
-                  __attribute__((always_inline)) {
-    constexpr int K3 = decltype(k3c)::value, V2 = decltype(v2c)::value;
-    constexpr int KR = (K3 + 1) % 3;
-    const uint8_t *const kt = KR == 0 ? lds_k0 : KR == 1 ? lds_k1 : lds_k2;
+  // Iteration `it` (parity P) with S(it) in `sc` and S(it + 1) computed into
+  // `sn`. K(it+1) is read from buffer P ^ 1 and K(it+2) loaded into buffer
+  // P (it held K(it), last read for QK(it) in iteration it - 1); V(it) is
+  // read from buffer P and V(it+1) loaded into buffer P ^ 1. Every copy an
+  // iteration issues completes before its closing barrier.
+  auto iter = [&](int32_t it, float16_t (&sc)[2], float16_t (&sn)[2], auto pc) __attribute__((always_inline)) {
+    constexpr int P = decltype(pc)::value;
+    const uint8_t *const kt = P ? lds_k0 : lds_k1;
     const int32_t tb = tile_base(it);
-    const bool v_ahead = it + 1 < n_tiles, k_ahead = it + 3 < n_tiles;
-    if (v_ahead) load_v(it + 1, IntC<V2 ^ 1>{}, 0, NVL / 2);
-    // Tiles that are not fully visible go through the mask, which also
-    // covers tiles this wave sees nothing of (all slots -inf: P = 0, O and
-    // the row sum unchanged). S(i+1) of the last iteration is computed from
-    // stale LDS and never read.
+    const bool v_ahead = it + 1 < n_tiles, k_ahead = it + 2 < n_tiles;
+    if (k_ahead) load_k(it + 2, IntC<P>{}, IntC<0>{}, IntC<NKL / 2>{});
+    // Tiles that are not fully visible go through the mask.
     if ((uint32_t)(it - it_full) >= (uint32_t)n_full) apply_mask(sc, tb, it);
     {
       // Operand fragments stream 4 ahead of the MFMA that uses them (the
@@ -1110,13 +1169,13 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       raise_max(tmax);
-      if (v_ahead) load_v(it + 1, IntC<V2 ^ 1>{}, NVL / 2, NVL);
+      if (k_ahead) load_k(it + 2, IntC<P>{}, IntC<NKL / 2>{}, IntC<NKL>{});
       // Seg 2: QK(i+1) block 1 | probabilities of S(i) block 0
       half8_t pa[2], pb[2];
       qk_block(kt, 1, sn[1], IntC<1>{}, pre_k);
       probs(sc[0], pa, lsum);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pre_a[i] = vfrag(IntC<V2>{}, 0, i);
+      for (int i = 0; i < 4; ++i) pre_a[i] = vfrag(IntC<P>{}, 0, i);
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         PIPE_SGB(0x008, 1, 0);
@@ -1129,13 +1188,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       // segment 3, ahead of the PV MFMAs that need them.
       asm volatile("" ::"v"(pa[0]), "v"(pa[1]));
       __builtin_amdgcn_sched_barrier(0);
-      // K copies go last: the end-of-tile wait leaves the newest NKL in flight.
-      if (k_ahead) load_k(it + 3, IntC<K3>{}, 0, NKL / 2);
+      if (v_ahead) load_v(it + 1, IntC<P ^ 1>{}, IntC<0>{}, IntC<NVL / 2>{});
       // Seg 3: PV(i) block 0 | probabilities of S(i) block 1
-      pv_block(IntC<V2>{}, 0, pa, pre_a);
+      pv_block(IntC<P>{}, 0, pa, pre_a);
       probs(sc[1], pb, lsum1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pre_b[i] = vfrag(IntC<V2>{}, 1, i);
+      for (int i = 0; i < 4; ++i) pre_b[i] = vfrag(IntC<P>{}, 1, i);
 #pragma unroll
       for (int c = 0; c < 2 * NDB; ++c) {
         PIPE_SGB(0x008, 1, 0);
@@ -1145,9 +1203,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       }
       asm volatile("" ::"v"(pb[0]), "v"(pb[1]));
       __builtin_amdgcn_sched_barrier(0);
-      if (k_ahead) load_k(it + 3, IntC<K3>{}, NKL / 2, NKL);
+      if (v_ahead) load_v(it + 1, IntC<P ^ 1>{}, IntC<NVL / 2>{}, IntC<NVL>{});
       // Seg 4: PV(i) block 1
-      pv_block(IntC<V2>{}, 1, pb, pre_b);
+      pv_block(IntC<P>{}, 1, pb, pre_b);
 #pragma unroll
       for (int c = 0; c < 2 * NDB; ++c) {
         PIPE_SGB(0x008, 1, 0);
@@ -1156,23 +1214,96 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(0);
     }
-    if (k_ahead) publish(IntC<NKL>{});
-    else publish(IntC<0>{});
+    publish(IntC<0>{});
   };
-  // Unrolled by six: buffer indices (mod 3 for K, mod 2 for V and the
-  // score registers) stay compile-time constants.
-  for (int32_t it = 0; it < n_tiles; it += 6) {
-    iter(it, sx, sy, IntC<0>{}, IntC<0>{});
+  // The same iteration without the pipeline, for iterations outside
+  // [c0, c1): QK(i+1) only when tile i+1 is visible to this wave, the
+  // softmax and PV of S(i) only when tile i is, one S block (and one 16-key
+  // half of the PV contraction) for a sink tile that needs no more. The
+  // copies and the end-of-tile barrier are those of the pipelined body.
+  auto iter_edge = [&](int32_t it, float16_t (&sc)[2], float16_t (&sn)[2], auto pc) __attribute__((always_inline)) {
+    constexpr int P = decltype(pc)::value;
+    const uint8_t *const kt = P ? lds_k0 : lds_k1;
+    const int32_t tb = tile_base(it);
+    const bool v_ahead = it + 1 < n_tiles, k_ahead = it + 2 < n_tiles;
+    const bool cur = wave_vis(it), nxt = v_ahead && wave_vis(it + 1);
+    if (k_ahead) load_k(it + 2, IntC<P>{}, IntC<0>{}, IntC<NKL>{});
+    if (v_ahead) load_v(it + 1, IntC<P ^ 1>{}, IntC<0>{}, IntC<NVL>{});
+    if (cur) {
+      const bool one = it == 0 && sink_half;  // wave-uniform
+      if ((uint32_t)(it - it_full) >= (uint32_t)n_full) apply_mask(sc, tb, it);
+      float tmax;
+      if (one) {
+        tmax = sc[0][0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, sc[0][r]);
+        tmax = half_max(tmax);
+      } else {
+        tmax = row_max(sc);
+      }
+      raise_max(tmax);
+      half8_t pa[2], pre[4];
+      probs(sc[0], pa, lsum);
+      if (one && sink_quarter) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vfrag(IntC<P>{}, 0, 2 * db), pa[0], o[db], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pre[i] = vfrag(IntC<P>{}, 0, i);
+        pv_block(IntC<P>{}, 0, pa, pre);
+      }
+      if (!one) {
+        half8_t pb[2];
+        probs(sc[1], pb, lsum1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pre[i] = vfrag(IntC<P>{}, 1, i);
+        pv_block(IntC<P>{}, 1, pb, pre);
+      }
+    }
+    // S(i+1) after S(i) is used, so the two are never live together here
+    // (a skipped S(i+1) is zeroed: it is never read).
+    const half8_t none[4] = {};
+    if (nxt) {
+      qk_block(kt, 0, sn[0], IntC<0>{}, none);
+      qk_block(kt, 1, sn[1], IntC<0>{}, none);
+    } else {
+      sn[0] = (float16_t){};
+      sn[1] = (float16_t){};
+    }
+    publish(IntC<0>{});
+  };
+  // Iterations [0, m0) and [m1, n_tiles) run the plain body, [m0, m1) the
+  // pipelined one, m0 = c0 rounded up to even. Each loop takes two
+  // iterations per trip, so buffer indices and score registers stay
+  // compile-time constants (a parity branch per iteration instead made the
+  // compiler spill).
+  const int32_t m0 = min(n_tiles, c0 + (c0 & 1)), m1 = max(m0, c1);
+  int32_t it = 0;
+  for (; it < m0; it += 2) {
+    iter_edge(it, sx, sy, IntC<0>{});
+    if (it + 1 >= m0) {
+      ++it;
+      break;
+    }
+    iter_edge(it + 1, sy, sx, IntC<1>{});
+  }
+  for (; it < m1; it += 2) {
+    iter(it, sx, sy, IntC<0>{});
+    if (it + 1 >= m1) {
+      ++it;
+      break;
+    }
+    iter(it + 1, sy, sx, IntC<1>{});
+  }
+  if (it < n_tiles && (it & 1)) {
+    iter_edge(it, sy, sx, IntC<1>{});
+    ++it;
+  }
+  for (; it < n_tiles; it += 2) {
+    iter_edge(it, sx, sy, IntC<0>{});
     if (it + 1 >= n_tiles) break;
-    iter(it + 1, sy, sx, IntC<1>{}, IntC<1>{});
-    if (it + 2 >= n_tiles) break;
-    iter(it + 2, sx, sy, IntC<2>{}, IntC<0>{});
-    if (it + 3 >= n_tiles) break;
-    iter(it + 3, sy, sx, IntC<0>{}, IntC<1>{});
-    if (it + 4 >= n_tiles) break;
-    iter(it + 4, sx, sy, IntC<1>{}, IntC<0>{});
-    if (it + 5 >= n_tiles) break;
-    iter(it + 5, sy, sx, IntC<2>{}, IntC<1>{});
+    iter_edge(it + 1, sy, sx, IntC<1>{});
   }
   __builtin_amdgcn_s_waitcnt(0);
 
