@@ -135,17 +135,28 @@ int memopt_evict_cache(const float *attention_scores, int64_t num_blocks,
  * dequantizes to zeros). A logical block with all block_size positions
  * evicted votes is_block_free[phys] += 1; the vote reaching H unlinks
  * block_tables[seq, lb] = -1. No seq_len cap (rows longer than 32768
- * tokens run as several workgroups per row). A physical page listed more
- * than once in block_tables (shared between sequences) receives the union
- * of their evictions: INT4 pools detect it and clear that call's scales
- * atomically. The library keeps per-device scratch for this (page marks
- * sized to the pool, the long-row workspace), allocated on first use and
- * grown as needed; calls on one device must not overlap. */
+ * tokens run as several workgroups per row). A physical page named by more
+ * than one live entry of block_tables (shared between sequences) receives
+ * the union of their evictions and no votes: it is never unlinked or
+ * counted free by this call.
+ * `workspace` is device scratch of at least memopt_evict_workspace_size
+ * bytes, 16-byte aligned, of any content; nothing in it is kept between
+ * calls. The call allocates no device memory. Calls sharing a workspace
+ * must not overlap (nor may calls on one pool: they mutate it). */
 int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs,
                         int32_t num_heads, int32_t seq_len, int32_t *block_tables,
                         int32_t max_blocks_per_seq, int32_t *is_block_free,
                         int64_t total_pool_blocks, float retain_ratio,
-                        int32_t num_sink_tokens, void *stream);
+                        int32_t num_sink_tokens, void *workspace,
+                        int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes memopt_evict_tokens needs for these sizes: page marks for
+ * total_pool_blocks pages plus, for seq_len > 32768, the long-row
+ * selection state. No counterpart in the reference, whose kernels keep this
+ * state in shared memory (it caps seq_len at 4096). */
+int memopt_evict_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t seq_len,
+                                int32_t max_blocks_per_seq, int64_t total_pool_blocks,
+                                int64_t *bytes);
 
 /* ------------------------------------------------------------------------ */
 /* Quantization (surface, whole-tensor)                                     */
@@ -232,8 +243,10 @@ typedef struct memopt_attn_desc {
 } memopt_attn_desc;
 
 int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes);
-/* A call whose workspace pointer is NULL with workspace_bytes 0 (for instance
- * through memopt_dynamic_sparse_attention) runs its decode unsplit. */
+/* `workspace` must hold at least memopt_attention_workspace_size bytes;
+ * a smaller one is an error (MEMOPT_ERR_INVALID). Only
+ * memopt_dynamic_sparse_attention, whose reference signature has no
+ * workspace, runs a decode that would split unsplit instead. */
 int memopt_paged_attention(const memopt_attn_desc *desc, void *stream);
 
 /* Bytes of the per-GPU static scratch of memopt_paged_attention_noalloc. */

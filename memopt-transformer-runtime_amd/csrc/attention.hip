@@ -199,12 +199,14 @@ static int decode_workspace(const memopt_attn_desc &d, int32_t *splits, int64_t 
 }
 
 // Split count and partials buffer of a decode call: the caller's workspace
-// when the shape splits; a call that passes no workspace at all (the
-// reference signature, memopt_dynamic_sparse_attention) runs unsplit.
-static int decode_plan(const memopt_attn_desc &d, int32_t *splits) {
+// when the shape splits. `unsplit_ok`: the entry point has no workspace
+// argument (the reference signature, memopt_dynamic_sparse_attention), so a
+// call that passes none runs unsplit; memopt_paged_attention callers must
+// pass the workspace memopt_attention_workspace_size asks for.
+static int decode_plan(const memopt_attn_desc &d, bool unsplit_ok, int32_t *splits) {
   int64_t need;
   decode_workspace(d, splits, &need);
-  if (need > 0 && d.workspace == nullptr && d.workspace_bytes == 0) {
+  if (need > 0 && unsplit_ok && d.workspace == nullptr && d.workspace_bytes == 0) {
     *splits = 1;
     return MEMOPT_OK;
   }
@@ -268,9 +270,11 @@ int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes
   return MEMOPT_OK;
 }
 
-int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
-  MEMOPT_REQUIRE(desc, MEMOPT_ERR_INVALID, "paged_attention: null descriptor");
-  const memopt_attn_desc &d = *desc;
+}  // extern "C"
+
+namespace memopt {
+
+static int paged_attention(const memopt_attn_desc &d, bool unsplit_ok, void *stream) {
   int rc = validate(d);
   if (rc != MEMOPT_OK) return rc;
   if (d.batch == 0 || d.q_len == 0 || d.num_heads == 0 || d.head_dim == 0) return MEMOPT_OK;
@@ -283,7 +287,7 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
 
   if (use_decode_int4(d)) {
     int32_t splits;
-    rc = decode_plan(d, &splits);
+    rc = decode_plan(d, unsplit_ok, &splits);
     if (rc != MEMOPT_OK) return rc;
     DecodeParams p;
     p.q = (const half_t *)d.query;
@@ -332,7 +336,7 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
 
   if (use_decode_fp16(d)) {
     int32_t splits;
-    rc = decode_plan(d, &splits);
+    rc = decode_plan(d, unsplit_ok, &splits);
     if (rc != MEMOPT_OK) return rc;
     DecodeParams p;
     p.q = (const half_t *)d.query;
@@ -396,6 +400,15 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
   return check_launch("paged_attention(generic)");
 }
 
+}  // namespace memopt
+
+extern "C" {
+
+int memopt_paged_attention(const memopt_attn_desc *desc, void *stream) {
+  MEMOPT_REQUIRE(desc, MEMOPT_ERR_INVALID, "paged_attention: null descriptor");
+  return paged_attention(*desc, false, stream);
+}
+
 int memopt_paged_attention_noalloc(const memopt_attn_desc *desc, void *stream) {
   MEMOPT_REQUIRE(desc, MEMOPT_ERR_INVALID, "paged_attention_noalloc: null descriptor");
   memopt_attn_desc d = *desc;
@@ -450,7 +463,7 @@ int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_
   d.context_lens = context_lens;
   d.max_seq_len = max_seq_len;
   d.window_size = window_size;
-  return memopt_paged_attention(&d, stream);
+  return paged_attention(d, true, stream);
 }
 
 }  // extern "C"

@@ -12,7 +12,7 @@
 //   * no seq_len cap (the reference rejects seq_len > 4096).
 // evict_cache: src/csrc/kv_cache.cu:379-483 (per (block, head) selection).
 #include <algorithm>
-#include <mutex>
+#include <atomic>
 #include <string>
 
 #include "common.hpp"
@@ -34,18 +34,34 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
 
+// Set in a page mark when two or more live block-table entries of one call
+// name the page.
+static constexpr uint32_t kMarkShared = 0x80000000u;
+
 struct RowZero {
   int32_t kv_format, H, D, bs;
   void *k, *v, *ks, *vs;
-  // INT4 pools: *alias_flag == epoch when some physical page appears more
-  // than once in this call's block tables (set by mark_pages_kernel).
+  // *alias_flag == tag (this call's id) when some physical page appears
+  // more than once in this call's block tables, and marks[page] then tells
+  // which (set by mark_pages_kernel or the long-row classify launch).
   const uint32_t *alias_flag;
-  uint32_t epoch;
+  const uint32_t *marks;
+  uint32_t tag;
 };
 
 // Whether this call's block tables alias a physical page (wave-uniform).
 __device__ __forceinline__ bool pages_aliased(const RowZero &z) {
-  return z.alias_flag != nullptr && *z.alias_flag == z.epoch;
+  return z.alias_flag != nullptr && *z.alias_flag == z.tag;
+}
+
+// A page named by more than one live block-table entry of this call is
+// shared between sequences (prefix sharing): it receives the union of their
+// evictions but never a free vote, so no sequence unlinks it and the free
+// sweep never returns a page that another table still maps. Per-(sequence,
+// head) votes from two sequences would otherwise add up to H while heads
+// still hold live rows.
+__device__ __forceinline__ bool page_shared(const RowZero &z, int32_t phys) {
+  return pages_aliased(z) && (z.marks[phys] & kMarkShared) != 0;
 }
 
 // Zero (page, pos, head) in both K and V. fp16: D halves. INT4 pages: the
@@ -416,34 +432,43 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
     for (int j = 0; j < z.bs && all; ++j) all = ev(lb * z.bs + j);
     if (!all) continue;
     const int32_t phys = bt[lb];
-    if (phys < 0 || phys >= total_pool_blocks) continue;
+    if (phys < 0 || phys >= total_pool_blocks || page_shared(z, phys)) continue;
     const int prev = atomicAdd(&is_block_free[phys], 1);
     if (prev + 1 == H) block_tables[(int64_t)n * M + lb] = -1;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Aliased physical pages (INT4 pools)
+// Aliased physical pages
 // ---------------------------------------------------------------------------
-// marks[phys] = (epoch << 32) | (entry + 1) of the last block-table entry of
-// this call that names page phys; a second entry naming it within the same
-// call (same epoch) sets *flag = epoch. The epoch changes every call, so the
-// marks never need clearing. Only logical blocks that hold tokens of the row
-// count (lb < nlb).
+// Each live block-table entry e (logical block lb < nlb of its row, a page
+// inside the pool) exchanges marks[phys] for e + 1. The value it takes out
+// is the previous entry that marked the page: in this call, or left from an
+// earlier call or any earlier content of the memory. The page is shared in
+// this call exactly when some exchange takes out an entry e' != e that is a
+// live entry naming the same page in the current block tables: with k >= 2
+// live entries on a page, every exchange after the first takes out one of
+// them; with k = 1, a live entry e' naming the page would be a second one.
+// So stale or arbitrary marks are harmless and nothing is cleared between
+// calls. The detecting entry ORs kMarkShared into the mark (the last
+// exchange of a shared page detects and ORs after it, so the final mark
+// carries the bit exactly when k >= 2) and sets *flag = tag, this call's id
+// (a stale flag only selects the atomic scale rewrite, which gives the same
+// result as the plain one). Block tables do not change during the mark pass.
 struct MarkArgs {
   const int32_t *bt;
   int64_t entries;  // num_seqs * max_blocks_per_seq (0: nothing to mark)
   int32_t M, nlb;
   int64_t total_pool_blocks;
-  unsigned long long *marks;
+  uint32_t *marks;
   uint32_t *flag;
-  uint32_t epoch;
+  uint32_t tag;
 };
 
-// mark_entry in four steps, so that its two dependent memory round trips
-// overlap other work: the block-table value of entry e, loaded whatever e
-// (index clamped, so the load needs no branch and nothing waits for it
-// until the value is used) ...
+// mark_entry in steps, so that its dependent memory round trips overlap
+// other work: the block-table value of entry e, loaded whatever e (index
+// clamped, so the load needs no branch and nothing waits for it until the
+// value is used) ...
 __device__ __forceinline__ int32_t mark_load(const MarkArgs &a, int64_t e) {
   return a.entries > 0 ? a.bt[min(e, a.entries - 1)] : -1;
 }
@@ -454,25 +479,23 @@ __device__ __forceinline__ int32_t mark_page(const MarkArgs &a, int64_t e, int32
 }
 // ... the exchange (its result, only read by mark_check and only where
 // phys >= 0, is left unset elsewhere, so that nothing waits for it) ...
-__device__ __forceinline__ void mark_swap(const MarkArgs &a, int64_t e, int32_t phys, unsigned long long &old) {
-  if (phys >= 0) old = atomicExch(&a.marks[phys], ((unsigned long long)a.epoch << 32) | (uint32_t)(e + 1));
+__device__ __forceinline__ void mark_swap(const MarkArgs &a, int64_t e, int32_t phys, uint32_t &old) {
+  if (phys >= 0) old = atomicExch(&a.marks[phys], (uint32_t)(e + 1));
 }
-// ... and the alias check.
-__device__ __forceinline__ void mark_check(const MarkArgs &a, int32_t phys, unsigned long long old) {
-  // Both halves of the exchange's result stay live until here: the return
-  // writes both, so a register reused for the unread low half would make
-  // the code wait for the exchange where the reuse begins.
-  asm volatile("" ::"v"(old));
-  if (phys >= 0 && (uint32_t)(old >> 32) == a.epoch) atomicMax(a.flag, a.epoch);
+// ... and the alias check: the entry taken out must still name the page.
+__device__ __forceinline__ void mark_check(const MarkArgs &a, int64_t e, int32_t phys, uint32_t old) {
+  const int64_t o = (int64_t)(old & ~kMarkShared) - 1;
+  if (phys < 0 || o < 0 || o == e || o >= a.entries || (int32_t)(o % a.M) >= a.nlb) return;
+  if (a.bt[o] != phys) return;
+  atomicOr(&a.marks[phys], kMarkShared);
+  atomicExch(a.flag, a.tag);
 }
 
 __device__ __forceinline__ void mark_entry(const MarkArgs &a, int64_t e) {
-  if ((int32_t)(e % a.M) >= a.nlb) return;
-  const int32_t phys = a.bt[e];
-  if (phys < 0 || phys >= a.total_pool_blocks) return;
-  const unsigned long long mine = ((unsigned long long)a.epoch << 32) | (uint32_t)(e + 1);
-  const unsigned long long old = atomicExch(&a.marks[phys], mine);
-  if ((uint32_t)(old >> 32) == a.epoch) atomicMax(a.flag, a.epoch);
+  const int32_t phys = mark_page(a, e, a.bt[e]);
+  uint32_t old = 0;
+  mark_swap(a, e, phys, old);
+  mark_check(a, e, phys, old);
 }
 
 __global__ __launch_bounds__(256) void mark_pages_kernel(const MarkArgs a) {
@@ -716,7 +739,7 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
   const float fhi = __builtin_bit_cast(float, (hi & 0x80000000u) ? hi ^ 0x80000000u : ~hi);
   const uint32_t sink_bits = __builtin_bit_cast(uint32_t, 1e38f);
   uint32_t above = 0, ncand = 0;
-  unsigned long long mold;  // set by mark_swap where mphys >= 0
+  uint32_t mold;  // set by mark_swap where mphys >= 0
   uint32_t wcnt = 0;     // this wave's list length (wave-uniform)
   bool wlost = false;    // the wave's list overflowed (wave-uniform)
   // One float4 of the span: plain = the wave's 256 tokens of this step are
@@ -816,7 +839,7 @@ __global__ __launch_bounds__(kClsNT) void evict_classify_long_kernel(const LongR
     sm.wcount[wave] = wlost ? kWaveCand + 1u : wcnt;
   }
   // the page marks: this thread's first entry, then any further ones
-  mark_check(ma, mphys, mold);
+  mark_check(ma, e0, mphys, mold);
   for (int64_t e = e0 + nthr; e < ma.entries; e += nthr) mark_entry(ma, e);
   // (the bitmask stores need not be complete for the list copy)
   lds_barrier();
@@ -1219,7 +1242,7 @@ __global__ __launch_bounds__(256) void evict_apply_kernel(const LongRows lr, int
     for (int j = 0; j < z.bs && all; ++j) all = ev(lb * z.bs + j);
     if (!all) continue;
     const int32_t phys = bt[lb];
-    if (phys < 0 || phys >= total_pool_blocks) continue;
+    if (phys < 0 || phys >= total_pool_blocks || page_shared(z, phys)) continue;
     const int prev = atomicAdd(&is_block_free[phys], 1);
     if (prev + 1 == lr.H) block_tables[(int64_t)n * M + lb] = -1;
   }
@@ -1337,6 +1360,7 @@ __global__ __launch_bounds__(256) void evict_apply_pages_kernel(const LongRows l
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   auto vote = [&](int32_t lb, int32_t phys) {
+    if (page_shared(z, phys)) return;
     const int prev = atomicAdd(&is_block_free[phys], 1);
     if (prev + 1 == H) block_tables[(int64_t)n * M + lb] = -1;
   };
@@ -1399,65 +1423,35 @@ __global__ __launch_bounds__(256) void evict_cache_kernel(const float *__restric
 }
 
 // ---------------------------------------------------------------------------
-// Library-owned device state of evict_tokens (per device): the page marks
-// and alias flag, and the long-row workspace. Allocated on first use and
-// grown when a larger pool or batch needs more; calls on one device must
-// not overlap (they mutate the same pool anyway).
+// evict_tokens workspace (allocated by the caller, see
+// memopt_evict_workspace_size; any content, nothing persists between calls):
+//   [0, 256)                 alias flag (u32);
+//   [256, 256 + marks)       page marks, one u32 per pool block;
+//   then (256-aligned)       long-row state: span slots, candidate lists and
+//                            row bitmasks (rows longer than kShortRow only).
 // ---------------------------------------------------------------------------
-struct EvictScratch {
-  unsigned long long *marks = nullptr;
-  int64_t nmarks = 0;
-  uint32_t *flag = nullptr;
-  uint8_t *ws = nullptr;
-  int64_t ws_bytes = 0;
-  uint32_t epoch = 0;
-};
+static constexpr int64_t kEvictHeader = 256;
 
-static constexpr int kEvictMaxDevices = 64;
-static std::mutex g_evict_mu;
-static EvictScratch g_evict[kEvictMaxDevices];
+static int64_t evict_marks_bytes(int64_t total_pool_blocks) {
+  return (4 * total_pool_blocks + 255) / 256 * 256;
+}
 
-static int evict_scratch(int64_t nmarks, int64_t ws_bytes, EvictScratch *out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kEvictMaxDevices) {
-    (void)hipGetLastError();
-    set_error("evict_tokens: no usable current device");
-    return MEMOPT_ERR_HIP;
-  }
-  std::lock_guard<std::mutex> lock(g_evict_mu);
-  EvictScratch &es = g_evict[dev];
-  auto fail = [](const char *what, hipError_t e) {
-    (void)hipGetLastError();
-    set_error(std::string("evict_tokens: ") + what + ": " + hipGetErrorString(e));
-    return MEMOPT_ERR_HIP;
-  };
-  if (es.flag == nullptr) {
-    hipError_t e = hipMalloc((void **)&es.flag, 256);
-    if (e != hipSuccess) return fail("hipMalloc(flag)", e);
-    e = hipMemset(es.flag, 0, 256);
-    if (e != hipSuccess) return fail("hipMemset(flag)", e);
-  }
-  if (nmarks > es.nmarks) {
-    if (es.marks) (void)hipFree(es.marks);
-    es.marks = nullptr;
-    es.nmarks = 0;
-    hipError_t e = hipMalloc((void **)&es.marks, nmarks * sizeof(unsigned long long));
-    if (e != hipSuccess) return fail("hipMalloc(marks)", e);
-    e = hipMemset(es.marks, 0, nmarks * sizeof(unsigned long long));  // epoch 0 is never used
-    if (e != hipSuccess) return fail("hipMemset(marks)", e);
-    es.nmarks = nmarks;
-  }
-  if (ws_bytes > es.ws_bytes) {
-    if (es.ws) (void)hipFree(es.ws);
-    es.ws = nullptr;
-    es.ws_bytes = 0;
-    const hipError_t e = hipMalloc((void **)&es.ws, ws_bytes);
-    if (e != hipSuccess) return fail("hipMalloc(workspace)", e);
-    es.ws_bytes = ws_bytes;
-  }
-  if (++es.epoch == 0) es.epoch = 1;
-  *out = es;
-  return MEMOPT_OK;
+static int64_t evict_long_bytes(int64_t num_seqs, int32_t num_heads, int32_t seq_len) {
+  if (seq_len <= kShortRow) return 0;
+  const int64_t rows = num_seqs * num_heads;
+  const int64_t words = ((int64_t)seq_len + 63) / 64 * 2;
+  const int64_t spans = ((int64_t)seq_len + kSpan - 1) / kSpan;
+  return rows * (spans * ((int64_t)sizeof(uint4) + kSpanCand * (int64_t)sizeof(uint2)) +
+                 words * (int64_t)sizeof(uint32_t));
+}
+
+// Call ids for the alias flag: distinct for 2^32 - 1 consecutive calls.
+static std::atomic<uint32_t> g_evict_calls{0};
+
+static uint32_t evict_tag() {
+  uint32_t t = g_evict_calls.fetch_add(1, std::memory_order_relaxed) + 1;
+  while (t == 0) t = g_evict_calls.fetch_add(1, std::memory_order_relaxed) + 1;
+  return t;
 }
 
 }  // namespace memopt
@@ -1466,9 +1460,20 @@ using namespace memopt;
 
 extern "C" {
 
+int memopt_evict_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t seq_len,
+                                int32_t max_blocks_per_seq, int64_t total_pool_blocks, int64_t *bytes) {
+  (void)max_blocks_per_seq;
+  MEMOPT_REQUIRE(bytes, MEMOPT_ERR_INVALID, "evict_workspace_size: null output");
+  MEMOPT_REQUIRE(num_seqs >= 0 && num_heads >= 0 && seq_len >= 0 && total_pool_blocks >= 0, MEMOPT_ERR_INVALID,
+                 "evict_workspace_size: negative size");
+  *bytes = kEvictHeader + evict_marks_bytes(total_pool_blocks) + evict_long_bytes(num_seqs, num_heads, seq_len);
+  return MEMOPT_OK;
+}
+
 int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t num_heads, int32_t seq_len,
                         int32_t *block_tables, int32_t max_blocks_per_seq, int32_t *is_block_free,
-                        int64_t total_pool_blocks, float retain_ratio, int32_t num_sink_tokens, void *stream) {
+                        int64_t total_pool_blocks, float retain_ratio, int32_t num_sink_tokens, void *workspace,
+                        int64_t workspace_bytes, void *stream) {
   const PoolView p = pool_snapshot();
   MEMOPT_REQUIRE(p.initialized, MEMOPT_ERR_STATE, "evict_tokens: pool not initialized");
   MEMOPT_REQUIRE(retain_ratio > 0.f && retain_ratio <= 1.f, MEMOPT_ERR_INVALID,
@@ -1480,6 +1485,15 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
   if (num_seqs == 0 || seq_len == 0) return MEMOPT_OK;
   MEMOPT_REQUIRE(attention_scores && block_tables && is_block_free, MEMOPT_ERR_INVALID,
                  "evict_tokens: null pointer");
+  int64_t need = 0;
+  (void)memopt_evict_workspace_size(num_seqs, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, &need);
+  MEMOPT_REQUIRE(workspace && workspace_bytes >= need, MEMOPT_ERR_INVALID,
+                 "evict_tokens: workspace too small (memopt_evict_workspace_size gives " + std::to_string(need) +
+                     " bytes)");
+  MEMOPT_REQUIRE(((uintptr_t)workspace & 15) == 0, MEMOPT_ERR_INVALID,
+                 "evict_tokens: workspace must be 16-byte aligned");
+  MEMOPT_REQUIRE((int64_t)num_seqs * max_blocks_per_seq < (1LL << 31), MEMOPT_ERR_UNSUPPORTED,
+                 "evict_tokens: block tables too large");
   // keep = clamp((int)ceilf(r * L), 1, L), in fp32 as src/csrc/kv_cache.cu:754-755.
   int keep = (int)ceilf(retain_ratio * (float)seq_len);
   keep = keep < 1 ? 1 : (keep > seq_len ? seq_len : keep);
@@ -1493,22 +1507,21 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
   const int64_t rows = (int64_t)num_seqs * num_heads;
   const int32_t words = (seq_len + 63) / 64 * 2;
   const int32_t spans = (seq_len + kSpan - 1) / kSpan;
-  // long-row workspace: slots [rows][spans], candidate lists [rows][spans][kSpanCand], bitmasks [rows][words]
-  const int64_t ws_bytes = long_rows ? rows * ((int64_t)spans * ((int64_t)sizeof(uint4) + kSpanCand * (int64_t)sizeof(uint2)) +
-                                              words * (int64_t)sizeof(uint32_t))
-                                     : 0;
-  EvictScratch es;
-  int rc = evict_scratch(int4 ? p.num_blocks : 0, ws_bytes, &es);
-  if (rc != MEMOPT_OK) return rc;
-  RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key,     p.value,
-            p.key_scales, p.value_scales, int4 ? es.flag : nullptr, es.epoch};
   hipStream_t st = (hipStream_t)stream;
-  // INT4 pools: pages listed twice in the block tables switch the scale
-  // rewrite to atomics.
+  const uint32_t tag = evict_tag();
+  uint8_t *ws = (uint8_t *)workspace;
+  uint32_t *flag = (uint32_t *)ws;
+  uint32_t *marks = (uint32_t *)(ws + kEvictHeader);
+  uint8_t *long_ws = ws + kEvictHeader + evict_marks_bytes(total_pool_blocks);
+  RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key, p.value, p.key_scales, p.value_scales,
+            flag, marks, tag};
+  // Pages listed more than once in the block tables: INT4 pools switch the
+  // scale rewrite to atomics, and no format votes for them.
   MarkArgs ma{block_tables, 0, max_blocks_per_seq,
-              (int32_t)std::min<int64_t>((seq_len + 15) / 16, max_blocks_per_seq), total_pool_blocks,
-              es.marks, es.flag, es.epoch};
-  if (int4 && ma.nlb > 0) ma.entries = (int64_t)num_seqs * max_blocks_per_seq;
+              (int32_t)std::min<int64_t>(((int64_t)seq_len + p.block_size - 1) / p.block_size, max_blocks_per_seq),
+              total_pool_blocks, marks, flag, tag};
+  if (ma.nlb > 0) ma.entries = (int64_t)num_seqs * max_blocks_per_seq;
+  int rc = MEMOPT_OK;
   if (!long_rows && ma.entries > 0) {
     hipLaunchKernelGGL(mark_pages_kernel, dim3((unsigned)((ma.entries + 255) / 256)), dim3(256), 0, st, ma);
     rc = check_launch("evict_tokens(mark_pages)");
@@ -1523,7 +1536,7 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
     lr.sinks = sinks;
     lr.words = words;
     lr.spans = spans;
-    lr.slot = reinterpret_cast<uint4 *>(es.ws);
+    lr.slot = reinterpret_cast<uint4 *>(long_ws);
     lr.cand = reinterpret_cast<uint2 *>(lr.slot + rows * spans);
     lr.bits = reinterpret_cast<uint32_t *>(lr.cand + rows * spans * (int64_t)kSpanCand);
     MEMOPT_REQUIRE(rows < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "evict_tokens: too many (seq, head) rows");
@@ -1575,7 +1588,7 @@ int memopt_evict_cache(const float *attention_scores, int64_t num_blocks, float 
   int keep = (int)(retain_ratio * (float)p.block_size);  // truncation, src/csrc/kv_cache.cu:426
   keep = keep < 1 ? 1 : (keep > p.block_size ? p.block_size : keep);
   RowZero z{p.kv_format, p.num_heads, p.head_dim, p.block_size, p.key, p.value, p.key_scales, p.value_scales,
-            nullptr, 0};
+            nullptr, nullptr, 0};
   MEMOPT_REQUIRE(num_blocks < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "evict_cache: too many blocks");
   hipLaunchKernelGGL(evict_cache_kernel, dim3((unsigned)num_blocks, p.num_heads), dim3(256),
                      (size_t)p.block_size * sizeof(float), (hipStream_t)stream, attention_scores, p.block_size,

@@ -94,7 +94,9 @@ _c_free = _sig("memopt_free_block", [_i64])
 _c_free_count = _sig("memopt_free_blocks_count", [ctypes.POINTER(_i64)])
 _c_write = _sig("memopt_write_cache", [_vp, _vp, _i64, _i32, _i32, _vp, _vp])
 _c_evict_cache = _sig("memopt_evict_cache", [_vp, _i64, _f32, _i32, _vp])
-_c_evict_tokens = _sig("memopt_evict_tokens", [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _i64, _f32, _i32, _vp])
+_c_evict_tokens = _sig("memopt_evict_tokens",
+                       [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _i64, _f32, _i32, _vp, _i64, _vp])
+_c_evict_ws = _sig("memopt_evict_workspace_size", [_i32, _i32, _i32, _i32, _i64, ctypes.POINTER(_i64)])
 _c_quant = _sig("memopt_quantize_kv_cache_int4", [_vp, _i64, _i64, _i32, _vp, _vp, _vp])
 _c_dequant = _sig("memopt_dequantize_kv_cache_int4", [_vp, _i64, _vp, _i64, _i32, _vp, _vp])
 _c_dsa = _sig("memopt_dynamic_sparse_attention",
@@ -420,10 +422,16 @@ def evict_tokens(attention_scores: torch.Tensor, block_tables: torch.Tensor, is_
     if N == 0 or L == 0:
         return
     scores = attention_scores.contiguous()
+    M, nb = block_tables.shape[1], is_block_free.shape[0]
+    need = _i64(0)
+    _check(_c_evict_ws(N, H, L, M, nb, ctypes.byref(need)))
     with torch.cuda.device(scores.device):
-        _check(_c_evict_tokens(scores.data_ptr(), N, H, L, block_tables.data_ptr(), block_tables.shape[1],
-                               is_block_free.data_ptr(), is_block_free.shape[0], float(retain_ratio),
-                               int(num_sink_tokens), _stream(scores)))
+        # scratch from torch's caching allocator on the current stream (page
+        # marks and long-row selection state; nothing is kept between calls)
+        ws = torch.empty(need.value, dtype=torch.uint8, device=scores.device)
+        _check(_c_evict_tokens(scores.data_ptr(), N, H, L, block_tables.data_ptr(), M,
+                               is_block_free.data_ptr(), nb, float(retain_ratio),
+                               int(num_sink_tokens), ws.data_ptr(), need.value, _stream(scores)))
 
 
 def free_evicted_blocks(is_block_free: torch.Tensor) -> List[int]:

@@ -447,6 +447,11 @@ def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
     {"format": "int4", "pages", "D"}. A logical block whose block_size positions are all
     evicted in this head votes is_block_free[phys] += 1; the vote that
     reaches H sets block_tables[seq, lb] = -1 (:993-1014).
+    A physical page named by two or more live entries (lb < ceil(L / bs),
+    page inside the pool) is shared between sequences, a case the reference
+    never meets: it gets the union of the rows' evictions and no votes, so
+    it is never unlinked or counted free (per-(seq, head) votes from two
+    sequences could otherwise reach H while heads still hold live rows).
     Mutates block_tables, is_block_free and pools in place; returns the
     evicted mask [N, H, L].
     """
@@ -461,6 +466,10 @@ def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
     M = block_tables.shape[1]
     nlb = (L + block_size - 1) // block_size
     bt0 = block_tables.copy()
+    live = bt0[:, :min(nlb, M)].ravel()
+    live = live[(live >= 0) & (live < is_block_free.shape[0])]
+    pages, counts = np.unique(live, return_counts=True)
+    shared = set(int(x) for x in pages[counts > 1])
     votes = []
     for n in range(N):
         for h in range(H):
@@ -475,7 +484,7 @@ def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
                 t0, t1 = lb * block_size, min(L, (lb + 1) * block_size)
                 if t1 - t0 == block_size and evicted[n, h, t0:t1].all():
                     p = int(bt0[n, lb])
-                    if 0 <= p < is_block_free.shape[0]:
+                    if 0 <= p < is_block_free.shape[0] and p not in shared:
                         votes.append((n, lb, p))
     for n, lb, p in votes:
         is_block_free[p] += 1

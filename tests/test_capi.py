@@ -112,3 +112,52 @@ def test_quantize_argument_guards(lib):
     assert f(None, 100, 2, 64, None, None, None) == ERR_INVALID        # numel % 64 != 0
     assert f(None, 192, 3, 64, None, None, None) == ERR_INVALID        # odd last dim
     assert f(None, 0, 128, 64, None, None, None) == OK                 # empty is a no-op
+
+
+def test_evict_workspace_size_and_guard(lib):
+    """memopt_evict_workspace_size: a 256-byte header, 4 bytes of page mark per
+    pool block (rounded to 256), plus long-row state only past 32768 tokens;
+    memopt_evict_tokens refuses a smaller workspace before launching anything."""
+    size = lib.memopt_evict_workspace_size
+    size.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
+                     ctypes.POINTER(ctypes.c_int64)]
+    out = ctypes.c_int64()
+    assert size(2, 8, 4096, 256, 1000, ctypes.byref(out)) == OK
+    assert out.value == 256 + 4096  # 4000 bytes of marks, rounded up to 256
+    assert size(2, 8, 32768, 2048, 1000, ctypes.byref(out)) == OK and out.value == 256 + 4096
+    assert size(2, 8, 32769, 2049, 1000, ctypes.byref(out)) == OK and out.value > 256 + 4096
+    short = out.value
+    assert size(2, 8, 200000, 12500, 1000, ctypes.byref(out)) == OK and out.value > short
+    assert _init(lib, 64, 16, 8, 64, 1) == OK
+    ev = lib.memopt_evict_tokens
+    ev.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                   ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64,
+                   ctypes.c_void_p]
+    dummy = ctypes.c_void_p(256)
+    assert size(1, 8, 64, 4, 64, ctypes.byref(out)) == OK
+    rc = ev(dummy, 1, 8, 64, dummy, 4, dummy, 64, 0.5, 4, dummy, out.value - 1, None)
+    assert rc == ERR_INVALID and b"workspace too small" in lib.memopt_last_error()
+    rc = ev(dummy, 1, 8, 64, dummy, 4, dummy, 64, 0.5, 4, None, 0, None)
+    assert rc == ERR_INVALID and b"workspace too small" in lib.memopt_last_error()
+    lib.memopt_reset_pool()
+
+
+def test_paged_attention_requires_its_workspace(lib):
+    """A decode that splits needs the workspace memopt_attention_workspace_size
+    reports: memopt_paged_attention refuses a call without it (no silent
+    unsplit fallback) before launching anything."""
+    import memopt_C
+    d = memopt_C.AttnDesc()
+    p = 256
+    d.query = d.out = d.key_cache = d.block_tables = d.context_lens = p
+    d.batch, d.q_len, d.num_heads, d.head_dim = 1, 1, 1, 128
+    d.kv_format, d.block_size, d.num_kv_blocks = 1, 16, 4096
+    d.max_blocks_per_seq, d.max_seq_len, d.window_size = 4096, 65536, 65536
+    need = ctypes.c_int64()
+    ws = lib.memopt_attention_workspace_size
+    ws.argtypes = [ctypes.POINTER(memopt_C.AttnDesc), ctypes.POINTER(ctypes.c_int64)]
+    assert ws(ctypes.byref(d), ctypes.byref(need)) == OK and need.value > 0
+    attn = lib.memopt_paged_attention
+    attn.argtypes = [ctypes.POINTER(memopt_C.AttnDesc), ctypes.c_void_p]
+    assert attn(ctypes.byref(d), None) == ERR_INVALID
+    assert b"workspace too small" in lib.memopt_last_error()

@@ -207,9 +207,9 @@ def test_evict_tokens_long_rows_select_passes(kind):
 
 def test_evict_tokens_long_rows_span_counts():
     """Back-to-back long-row calls with 4, 1 and 2 spans per row and several
-    rows: each row is resolved by whichever span finishes last, through
-    per-row arrival counters that every call must leave at zero for the
-    next one (a counter left behind would resolve a row early)."""
+    rows, each with a workspace sized for its own span count: a call must
+    not depend on what an earlier call left in the span slots, candidate
+    lists or bitmasks."""
     for i, (N, H, L) in enumerate([(1, 2, 200003), (2, 3, 50000), (3, 2, 131072), (1, 1, 65540)]):
         rng = np.random.default_rng(100 + i)
         s = rng.lognormal(size=(N, H, L)).astype(np.float32)
@@ -231,6 +231,40 @@ def test_evict_tokens_aliased_pages(L):
     _evict_case("int4", N, H, L, D, 0.6, 4, s, bt=bt, seed=L + 1)
     # the fp16 pool's zero stores need no atomics and give the same union
     _evict_case("fp16", N, H, L, D, 0.6, 4, s, bt=bt, seed=L + 1)
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int4"])
+@pytest.mark.parametrize("L", [64, 40000])
+@pytest.mark.parametrize("heads_b", [(0, 1), (2, 3), (0, 1, 2, 3)])
+def test_evict_tokens_shared_page_votes(fmt, L, heads_b):
+    """Two sequences name one page (prefix sharing) and both fully evict it:
+    sequence 0 in heads 0 and 1, sequence 1 in `heads_b` (overlapping,
+    disjoint, all). A shared page gets the union of the evictions and no
+    votes, so it stays linked in both tables (votes per (sequence, head)
+    would reach H = 4 while heads still hold live rows); every other page
+    fully evicted in all heads is unlinked. Short rows and long rows."""
+    rng = np.random.default_rng(L + len(heads_b))
+    N, H, D, bs = 2, 4, 64, 16
+    M = (L + bs - 1) // bs
+    bt = rng.permutation(N * M + 2)[:N * M].reshape(N, M).astype(np.int32)
+    bt[1, 2] = bt[0, 2]  # logical block 2 of both sequences: one page
+    s = rng.lognormal(size=(N, H, L)).astype(np.float32)
+    low = lambda n: (1e-6 * (1 + rng.random(n))).astype(np.float32)  # distinct, below every lognormal draw
+    for h in (0, 1):
+        s[0, h, 32:48] = low(16)
+    for h in heads_b:
+        s[1, h, 32:48] = low(16)
+    for h in range(H):
+        s[0, h, 16:32] = low(16)  # a block of sequence 0 alone, every head: unlinked
+    # keep = ceil(0.4 L): at least 32 evictions per head, so the low blocks go
+    _evict_case(fmt, N, H, L, D, 0.4, 4, s, bt=bt, seed=L + 7)
+    shared = int(bt[0, 2])
+    bt_d = to_dev(bt)
+    ibf_d = to_dev(np.zeros(N * M + 2, np.int32))
+    memopt_C.evict_tokens(to_dev(s), bt_d, ibf_d, 0.4, 4)
+    got_bt, got_ibf = bt_d.cpu().numpy(), ibf_d.cpu().numpy()
+    assert got_bt[0, 2] == shared and got_bt[1, 2] == shared and got_ibf[shared] == 0
+    assert got_bt[0, 1] == -1
 
 
 @pytest.mark.parametrize("D,N,H,L", [(128, 2, 3, 300), (192, 2, 3, 300), (1088, 2, 3, 300),

@@ -385,6 +385,36 @@ def test_evict_intended_unlinks_fully_evicted_blocks():
     assert bt.tolist() == [[0, -1, 2, 3]] and free.tolist() == [0, 2, 0, 0, 0, 0, 0, 0]
 
 
+@pytest.mark.parametrize("heads_b", [(0, 1), (2, 3), (0, 1, 2, 3)])
+def test_evict_intended_shared_page_gets_no_votes(heads_b):
+    """A page named by both sequences (prefix sharing, page 0): sequence 0
+    fully evicts it in heads 0 and 1, sequence 1 in `heads_b` (overlapping,
+    disjoint, all). Per-(sequence, head) votes would reach H = 4 in the
+    first two cases while heads still hold live rows; a shared page gets no
+    votes and stays linked in both tables. Pages of one sequence vote as
+    usual: page 1 (every head) is unlinked, the others collect partial
+    votes. keep = ceil(0.33 * 48) = 16, so each head keeps its 16 highest
+    scores and evicts the rest."""
+    N, H, L, bs = 2, 4, 48, 16
+    scores = np.ones((N, H, L), np.float32)
+    scores[0, :, 16:32] = 0.01                 # seq 0, page 1: lowest in every head
+    scores[0, [0, 1], 0:16] = 0.1              # heads 0, 1 keep block 2, evict blocks 0, 1
+    scores[0, [2, 3], 0:16] = 2.0              # heads 2, 3 keep block 0, evict blocks 1, 2
+    for h in range(H):                         # seq 1: evict block 0 in heads_b, blocks 1, 2 elsewhere
+        scores[1, h, 0:16] = 0.1 if h in heads_b else 2.0
+    pools = _pools("fp16", 5, bs, H, 64, np.random.default_rng(3))
+    bt = np.array([[0, 1, 3], [0, 2, 4]], np.int32)
+    free = np.zeros(5, np.int32)
+    ev = O.evict_tokens_intended(scores, bt, free, 0.33, 0, pools, bs)
+    other = H - len(heads_b)
+    assert bt.tolist() == [[0, -1, 3], [0, 2, 4]]
+    assert free.tolist() == [0, 4, other, 2, other]
+    for h in range(H):
+        assert ev[0, h, :16].all() == (h in (0, 1)) and ev[1, h, :16].all() == (h in heads_b)
+        # the union of both sequences' evictions is zeroed on the shared page
+        assert (pools["k"][0, :, h] == 0).all() == (h in (0, 1) or h in heads_b)
+
+
 def test_evict_literal_defects():
     rng = np.random.default_rng(9)
     scores = rng.lognormal(size=(2, 2, 256)).astype(np.float32)
