@@ -194,7 +194,7 @@ static int validate(const memopt_attn_desc &d) {
 static int decode_workspace(const memopt_attn_desc &d, int32_t *splits, int64_t *bytes) {
   // Splits are sized in the kernels' 16-token units.
   *splits = decode_splits(d.batch, d.num_heads, max_pages_visited(d) * (d.block_size / 16));
-  *bytes = (*splits > 1) ? (int64_t)d.batch * d.num_heads * (*splits) * (d.head_dim + 2) * 4 : 0;
+  *bytes = decode_workspace_bytes(d.batch, d.num_heads, *splits, d.head_dim);
   return MEMOPT_OK;
 }
 
@@ -330,7 +330,9 @@ static int paged_attention(const memopt_attn_desc &d, bool unsplit_ok, void *str
     p.bs = d.block_size;
     p.qk_scale_log2 = scale * 1.4426950408889634f;
     p.ws_o = (float *)d.workspace;
-    p.ws_ml = splits > 1 ? (float *)d.workspace + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
+    p.ws_ml = splits > 1 ? p.ws_o + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
+    p.ws_cnt = splits > 1 ? (unsigned long long *)(p.ws_ml + (int64_t)d.batch * d.num_heads * splits * 2) : nullptr;
+    p.tag = next_decode_tag();
     return launch_decode_int4(p, d.batch, d.head_dim, d.kv_format == MEMOPT_KV_INT4 ? MEMOPT_SCALE_F16 : d.scale_dtype, s);
   }
 
@@ -360,7 +362,9 @@ static int paged_attention(const memopt_attn_desc &d, bool unsplit_ok, void *str
     p.bs = d.block_size;
     p.qk_scale_log2 = scale * 1.4426950408889634f;
     p.ws_o = (float *)d.workspace;
-    p.ws_ml = splits > 1 ? (float *)d.workspace + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
+    p.ws_ml = splits > 1 ? p.ws_o + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
+    p.ws_cnt = splits > 1 ? (unsigned long long *)(p.ws_ml + (int64_t)d.batch * d.num_heads * splits * 2) : nullptr;
+    p.tag = next_decode_tag();
     return launch_decode_fp16(p, d.batch, d.head_dim, s);
   }
 

@@ -50,18 +50,96 @@ struct DecodeParams {
   float qk_scale_log2;  // (1/sqrt(D)) * log2(e)
   float *ws_o;          // [B, H, splits, D] (splits > 1)
   float *ws_ml;         // [B, H, splits, 2]
+  unsigned long long *ws_cnt;  // [B, H] arrival counters (splits > 1)
+  unsigned long long tag;      // this launch's id, 1 .. 2^56 - 1
 };
+
+// Bytes of a decode call's split-K workspace: partials (o[D], m, l) per
+// (b, h, split) and one arrival counter per (b, h).
+inline int64_t decode_workspace_bytes(int64_t batch, int64_t heads, int64_t splits, int64_t D) {
+  return splits > 1 ? batch * heads * (splits * (D + 2) * 4 + 8) : 0;
+}
+
+// Id of the next decode launch (for the arrival counters).
+unsigned long long next_decode_tag();
+
+// Epilogue of a decode workgroup of NW waves over (b, h, split): merges the
+// waves' (m, l, acc[D]) held in LDS. Unsplit: writes the output row. Split:
+// writes this split's partial to the workspace with agent-scope stores
+// (they bypass the per-XCD L2s, as the splits of one (b, h) run on
+// different XCDs), waits for them, and counts its arrival on (b, h) with a
+// compare-and-swap on (tag << 8 | count): a counter from another launch
+// (other tag, or any initial content) restarts at 1, so the workspace needs
+// no clearing. The split that brings the count to `splits` merges every
+// partial (log-sum-exp, agent-scope loads) into the output row. No
+// workgroup waits for another.
+template <int D, int NW>
+__device__ __forceinline__ void decode_epilogue(const DecodeParams &p, int64_t bh, int32_t split,
+                                                const float (*s_acc)[D], const float (*s_ml)[2]) {
+  for (int d = threadIdx.x; d < D; d += NW * 64) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_ml[w][0]);
+    float lt = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = (s_ml[w][0] == -INFINITY) ? 0.0f : fast_exp2(s_ml[w][0] - mx);
+      lt += s_ml[w][1] * f;
+      o += s_acc[w][d] * f;
+    }
+    if (p.splits == 1) {
+      p.out[bh * D + d] = (half_t)(lt > 0.0f ? o / lt : 0.0f);
+    } else {
+      const int64_t slot = bh * p.splits + split;
+      __hip_atomic_store(&p.ws_o[slot * D + d], o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(&p.ws_ml[slot * 2], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&p.ws_ml[slot * 2 + 1], lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (p.splits == 1) return;
+  __shared__ int s_last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long *cnt = p.ws_cnt + bh;
+    unsigned long long e = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), nv;
+    do {
+      nv = (e >> 8) == p.tag ? e + 1 : (p.tag << 8) | 1;
+    } while (!__hip_atomic_compare_exchange_strong(cnt, &e, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT));
+    s_last = (int)(nv & 0xFF) == p.splits;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const float *ml = p.ws_ml + bh * p.splits * 2;
+  for (int d = threadIdx.x; d < D; d += NW * 64) {
+    float mx = -INFINITY;
+    for (int s = 0; s < p.splits; ++s)
+      mx = fmaxf(mx, __hip_atomic_load(&ml[2 * s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float lt = 0.0f, o = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+      const float ms = __hip_atomic_load(&ml[2 * s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float ls = __hip_atomic_load(&ml[2 * s + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float os = __hip_atomic_load(&p.ws_o[(bh * p.splits + s) * D + d], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+      const float f = ms == -INFINITY ? 0.0f : fast_exp2(ms - mx);
+      lt += ls * f;
+      o += os * f;
+    }
+    p.out[bh * D + d] = (half_t)(lt > 0.0f ? o / lt : 0.0f);
+  }
+}
 
 // Split count used by the INT4 decode kernel for this launch shape.
 int decode_splits(int32_t batch, int32_t heads, int32_t max_pages_visited);
-// Launches the split-K INT4 decode kernel (+ combine when splits > 1).
+// Launches the split-K INT4 decode kernel (splits merged in-kernel).
 int launch_decode_int4(const DecodeParams &p, int32_t batch, int32_t D, int32_t scale_dtype,
                        hipStream_t stream);
 
-// Launches the split-K fp16-pool decode kernel (+ combine when splits > 1).
+// Launches the split-K fp16-pool decode kernel (splits merged in-kernel).
 int launch_decode_fp16(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream);
-// Log-sum-exp merge of the split partials in p.ws_o / p.ws_ml into p.out.
-int launch_decode_combine(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream);
 
 // Multi-query (q_len >= 2) MFMA kernel over INT4 page pools or contiguous
 // fp16 pools with 16-multiple pages and D in {64, 128}.

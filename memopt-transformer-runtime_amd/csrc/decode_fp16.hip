@@ -198,29 +198,7 @@ __global__ __launch_bounds__(NW * 64) void decode_fp16_kernel(const DecodeParams
     }
   }
   __syncthreads();
-  for (int dd = threadIdx.x; dd < D; dd += NW * 64) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_ml[w][0]);
-    float lt = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = (s_ml[w][0] == -INFINITY) ? 0.0f : fast_exp2(s_ml[w][0] - mx);
-      lt += s_ml[w][1] * f;
-      o += s_acc[w][dd] * f;
-    }
-    const int64_t bh = (int64_t)b * p.H + h;
-    if (p.splits == 1) {
-      p.out[bh * D + dd] = (half_t)(lt > 0.0f ? o / lt : 0.0f);
-    } else {
-      const int64_t slot = bh * p.splits + split;
-      p.ws_o[slot * D + dd] = o;
-      if (dd == 0) {
-        p.ws_ml[slot * 2] = mx;
-        p.ws_ml[slot * 2 + 1] = lt;
-      }
-    }
-  }
+  decode_epilogue<D, NW>(p, (int64_t)b * p.H + h, split, s_acc, s_ml);
 }
 
 int launch_decode_fp16(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream) {
@@ -229,9 +207,7 @@ int launch_decode_fp16(const DecodeParams &p, int32_t batch, int32_t D, hipStrea
     hipLaunchKernelGGL((decode_fp16_kernel<128, 4, 2>), grid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((decode_fp16_kernel<64, 4, 2>), grid, dim3(256), 0, stream, p);
-  int rc = check_launch("paged_attention(decode_fp16)");
-  if (rc != MEMOPT_OK || p.splits == 1) return rc;
-  return launch_decode_combine(p, batch, D, stream);
+  return check_launch("paged_attention(decode_fp16)");
 }
 
 }  // namespace memopt

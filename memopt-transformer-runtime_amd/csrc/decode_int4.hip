@@ -35,7 +35,9 @@
 //    moves (3 over the 8 lanes of a token pair in the page kernel);
 //  * only pages that intersect the sink range or the window are visited,
 //    block-table entries < 0 or >= num_kv_blocks are skipped, and split-K
-//    partials (m, l, o) are merged by a small log-sum-exp combine kernel.
+//    partials (m, l, o) are merged by the last split of each (b, h) to
+//    finish (decode_epilogue).
+#include <atomic>
 #include <cstdlib>
 
 #include "attention.hpp"
@@ -266,29 +268,7 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_kernel(const DecodeParams
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += NW * 64) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_ml[w][0]);
-    float lt = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = (s_ml[w][0] == -INFINITY) ? 0.0f : fast_exp2(s_ml[w][0] - mx);
-      lt += s_ml[w][1] * f;
-      o += s_acc[w][d] * f;
-    }
-    const int64_t bh = (int64_t)b * p.H + h;
-    if (p.splits == 1) {
-      p.out[bh * D + d] = (half_t)(lt > 0.0f ? o / lt : 0.0f);
-    } else {
-      const int64_t slot = bh * p.splits + split;
-      p.ws_o[slot * D + d] = o;
-      if (d == 0) {
-        p.ws_ml[slot * 2] = mx;
-        p.ws_ml[slot * 2 + 1] = lt;
-      }
-    }
-  }
+  decode_epilogue<D, NW>(p, (int64_t)b * p.H + h, split, s_acc, s_ml);
 }
 
 // Decode over this build's INT4 page format (page_format.hpp): lane l = 8p + c
@@ -502,49 +482,7 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += NW * 64) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_ml[w][0]);
-    float lt = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = (s_ml[w][0] == -INFINITY) ? 0.0f : fast_exp2(s_ml[w][0] - mx);
-      lt += s_ml[w][1] * f;
-      o += s_acc[w][d] * f;
-    }
-    const int64_t bh = (int64_t)b * p.H + h;
-    if (p.splits == 1) {
-      p.out[bh * D + d] = (half_t)(lt > 0.0f ? o / lt : 0.0f);
-    } else {
-      const int64_t slot = bh * p.splits + split;
-      p.ws_o[slot * D + d] = o;
-      if (d == 0) {
-        p.ws_ml[slot * 2] = mx;
-        p.ws_ml[slot * 2 + 1] = lt;
-      }
-    }
-  }
-}
-
-// Log-sum-exp merge of split partials: one workgroup per (b, h).
-__global__ __launch_bounds__(128) void decode_combine_kernel(const float *__restrict__ ws_o,
-                                                             const float *__restrict__ ws_ml,
-                                                             half_t *__restrict__ out, int32_t D,
-                                                             int32_t splits) {
-  const int64_t bh = blockIdx.x;
-  const float *ml = ws_ml + bh * splits * 2;
-  float mx = -INFINITY;
-  for (int s = 0; s < splits; ++s) mx = fmaxf(mx, ml[2 * s]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float lt = 0.0f, o = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-      const float f = (ml[2 * s] == -INFINITY) ? 0.0f : fast_exp2(ml[2 * s] - mx);
-      lt += ml[2 * s + 1] * f;
-      o += ws_o[(bh * splits + s) * D + d] * f;
-    }
-    out[bh * D + d] = (half_t)(lt > 0.0f ? o / lt : 0.0f);
-  }
+  decode_epilogue<D, NW>(p, (int64_t)b * p.H + h, split, s_acc, s_ml);
 }
 
 static int device_cus() {
@@ -632,15 +570,12 @@ int launch_decode_int4(const DecodeParams &p, int32_t batch, int32_t D, int32_t 
     launch_shape<64, half_t>(p, grid, sh, stream);
   else
     launch_shape<64, float>(p, grid, sh, stream);
-  int rc = check_launch("paged_attention(decode_int4)");
-  if (rc != MEMOPT_OK || p.splits == 1) return rc;
-  return launch_decode_combine(p, batch, D, stream);
+  return check_launch("paged_attention(decode_int4)");
 }
 
-int launch_decode_combine(const DecodeParams &p, int32_t batch, int32_t D, hipStream_t stream) {
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((int64_t)batch * p.H)), dim3(128), 0, stream,
-                     p.ws_o, p.ws_ml, p.out, D, p.splits);
-  return check_launch("paged_attention(decode_combine)");
+unsigned long long next_decode_tag() {
+  static std::atomic<unsigned long long> calls{0};
+  return (calls.fetch_add(1, std::memory_order_relaxed) % ((1ull << 56) - 1)) + 1;
 }
 
 }  // namespace memopt
