@@ -9,9 +9,10 @@ A "step" is one ``dynamic_sparse_attention`` call over the whole batch with
 inputs resident in HBM. ``value`` = effective KV bytes (codes + fp16 scales,
 285,212,672 B) / seconds per step, in GB/s.
 
-The pool holds two disjoint page sets and steps alternate between them, so a
-step never re-reads what the previous step left in the 256 MB last-level
-cache. The JSON line also carries the roofline of the decode kernel (timed
+The pool holds four disjoint page sets (1.14 GB) and steps rotate over
+them, so a step never re-reads what earlier steps left in the 256 MB
+last-level cache; the same launches rotating over two of the sets (570 MB)
+are timed as a control and reported beside the headline. The JSON line also carries the roofline of the decode kernel (timed
 with HIP events on the stream it runs on), a CPU baseline (the reference's
 torch CPU path, restated in oracle/, on a bounded sample), and secondary
 figures (prefill MFMA use, sparse and long-context decode with evict_tokens,
@@ -305,13 +306,14 @@ def fill_pages(torch, memopt_C, bt, cfg, gen):
         del kv
 
 
-def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, steps=20, warmup=3):
+def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, steps=20, warmup=3, control_copies=0):
     """evict_tokens (intended top-k, sinks kept) on LogNormal(0,1) scores, then
     INT4 decode over sinks U window. `copies` independent page sets (each
     filled and evicted on its own) are decoded in turn so that a working set
     smaller than the 256 MB last-level cache is not re-read from it. Returns
     the eviction time and the decode rate on the bytes of the pages the
-    decode actually visits."""
+    decode actually visits; with `control_copies`, also the rate when the
+    steps rotate over only that many of the sets."""
     B, H, D, ctx, bs = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
     dev = torch.device("cuda", 0)
     nbps = ctx // bs
@@ -354,11 +356,16 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
     nbytes //= copies  # bytes per step (copies are equal up to unlinked pages)
     ms, _ = time_steps(torch, calls, steps, warmup, pre_sleep_cycles=20_000_000)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"kernel": INT4_DECODE_KERNEL, "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
-            "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "evict_tokens_ms": round(evict_ms[0], 4), "pages_unlinked": unlinked,
-            "page_sets_rotated": copies,
-            "block_tables": "seeded FIFO alloc/free trace" if fifo_trace else "seeded random permutation"}
+    out = {"kernel": INT4_DECODE_KERNEL, "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
+           "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+           "evict_tokens_ms": round(evict_ms[0], 4), "pages_unlinked": unlinked,
+           "page_sets_rotated": copies,
+           "block_tables": "seeded FIFO alloc/free trace" if fifo_trace else "seeded random permutation"}
+    if control_copies:
+        cms, _ = time_steps(torch, calls[:control_copies], steps, warmup, pre_sleep_cycles=20_000_000)
+        out["rotation_control"] = {"page_sets_rotated": control_copies, "decode_ms": round(cms, 5),
+                                   "frac_of_hbm_peak": round(nbytes / (cms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def time_evict(torch, memopt_C, scores, bt, nb, cfg, reps=7):
@@ -482,7 +489,7 @@ def main():
     import memopt_C  # noqa: E402  (fails loudly if the HIP library is missing)
 
     cfg = CFG2
-    calls, tables, q, cl = setup_decode(torch, memopt_C, cfg)
+    calls, tables, q, cl = setup_decode(torch, memopt_C, cfg, copies=4)
     # The GPU starts from idle clocks: settle them with ~50 ms of device
     # copies before the W warm-up steps (nothing here is timed; a kernel other
     # than the decode kernel, so a profiler's decode average covers only the
@@ -494,6 +501,8 @@ def main():
     torch.cuda.synchronize()
     del settle_src, settle_dst
     region_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup, pre_sleep_cycles=20_000_000)
+    # control: the same launches rotating over two of the four page sets
+    control_ms, _ = time_steps(torch, calls[:2], args.steps, 20, pre_sleep_cycles=20_000_000)
     nbytes = effective_kv_bytes(cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"])
     value = nbytes / (region_ms * 1e-3) / 1e9
     achieved = value  # one decode launch per step
@@ -513,7 +522,10 @@ def main():
         "config": {"workload": "BASELINE configs[1] decode: batch 16, 32 heads, head_dim 128, context 4096, "
                                "INT4 16-token pages (group 64, fp16 scales), random-permutation block tables, "
                                "retain_ratio 1.0",
-                   "effective_kv_bytes": nbytes, "page_sets_rotated": len(calls)},
+                   "effective_kv_bytes": nbytes, "page_sets_rotated": len(calls),
+                   "rotation_control": {"page_sets_rotated": 2, "ms_per_step": round(control_ms, 5),
+                                        "frac_of_hbm_peak": round(nbytes / (control_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                                                  4)}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profile_traffic("decode_int4_config2_pmc.txt"),
@@ -527,7 +539,8 @@ def main():
         sec = {"prefill": bench_prefill(torch, memopt_C, CFG4)}
         sec["sparse_decode_config3"] = dict(
             workload="BASELINE configs[2]: B 16, ctx 8192, evict_tokens r 0.75 + 4 sinks, decode window 2048",
-            **bench_sparse_decode(torch, memopt_C, CFG3, CFG3["window"], fifo_trace=False, copies=3))
+            **bench_sparse_decode(torch, memopt_C, CFG3, CFG3["window"], fifo_trace=False, copies=6,
+                                  control_copies=3))
         sec["long_context_config5"] = dict(
             workload="BASELINE configs[4]: B 4, ctx 131072, 32768 pages, scheduler-forced INT4 + retain 0.75, "
                      "4 sinks, full window, through PolicyForward",
