@@ -2,8 +2,10 @@
 path: q_len >= 2 over fp16 pools and INT4 page pools, causal StreamingLLM
 masks (window + sinks), non-causal multi-query windows, unlinked pages,
 contexts shorter than the query block, against the CPU oracle; and the
-BASELINE config-4 shape at full size against an fp32 reference on sampled
-query rows."""
+BASELINE config-4 shape at full size against an fp32 reference: sampled
+query rows of every head, and every row of four heads."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -232,4 +234,47 @@ def test_config4_shape_int4_pages(S, H):
                         device=dev())
     ref = _fp32_rows_reference(q[0], kd, vd, rows, S, W, sinks)
     assert_close(out[0, rows.long()], ref, what=f"S={S} H={H}")
+    torch.cuda.synchronize()
+
+
+def _fp32_head_reference(qh, kh, vh, r0, r1, ctx, W, sinks):
+    """fp32 StreamingLLM causal attention of query rows [r0, r1) of one head
+    (qh [Lq, D], kh / vh [ctx, D] dequantized), with 2-D matmuls only."""
+    D = qh.shape[-1]
+    s = torch.matmul(qh[r0:r1].float(), kh.float().t().contiguous()) * (1.0 / math.sqrt(D))  # [n, ctx]
+    pos = (ctx - qh.shape[0] + torch.arange(r0, r1, device=qh.device))[:, None]
+    j = torch.arange(ctx, device=qh.device)[None, :]
+    vis = (j <= pos) & ((j < sinks) | (j >= pos - W + 1))
+    p = torch.softmax(s.masked_fill(~vis, float("-inf")), dim=-1)
+    return torch.matmul(p, vh.float())
+
+
+def test_config4_full_rows_int4_pages():
+    """BASELINE configs[3] at full size with its own inputs (Q/K/V ~ N(0, 0.5),
+    B 1, S 16384, H 32, D 128, causal W 4096, 4 sinks, K/V written through
+    write_cache into shuffled INT4 pages): every one of the 16384 output
+    rows of heads 0, 11, 22 and 31 against fp32 attention over the
+    dequantized pool, computed head by head on the GPU in 2048-row chunks."""
+    S, H, D, W, sinks, std = 16384, 32, 128, 4096, 4, 0.5
+    torch.manual_seed(11)
+    nb = S // 16 + 8
+    memopt_C.init_pool(nb, 16, H, D, kv_format="int4")
+    order = torch.randperm(nb)[: S // 16].to(torch.int32)
+    bt = order[None].to(dev())
+    slots = (order.to(dev()).long()[:, None] * 16 + torch.arange(16, device=dev())).reshape(-1).to(torch.int32)
+    k = (torch.randn(S, H, D, device=dev()) * std).half()
+    v = (torch.randn(S, H, D, device=dev()) * std).half()
+    memopt_C.write_cache(k, v, bt, slots)
+    del k, v
+    q = (torch.randn(1, S, H, D, device=dev()) * std).half()
+    ctx = torch.tensor([S], dtype=torch.int32, device=dev())
+    out = memopt_C.dynamic_sparse_attention(q, memopt_C.get_key_pool(), memopt_C.get_value_pool(), bt, ctx, S, W,
+                                            num_sink_tokens=sinks, causal=True)
+    pages = memopt_C.get_int4_pages()
+    kd, vd = O.dequant_pages_torch(pages[order.to(dev()).long()], D)
+    kd, vd = kd.reshape(S, H, D), vd.reshape(S, H, D)
+    for h in (0, 11, 22, 31):
+        for r0 in range(0, S, 2048):
+            ref = _fp32_head_reference(q[0, :, h], kd[:, h], vd[:, h], r0, r0 + 2048, S, W, sinks)
+            assert_close(out[0, r0:r0 + 2048, h], ref, what=f"config 4 head {h} rows {r0}..{r0 + 2047}")
     torch.cuda.synchronize()
