@@ -84,26 +84,82 @@ def setup_decode(torch, memopt_C, cfg, copies=2):
     return calls, tables, q, cl
 
 
-def time_steps(torch, fn_list, steps, warmup, pre_sleep_cycles=0):
+SETTLE_MS = 40.0
+
+
+def settle(torch, fn, settle_ms=SETTLE_MS):
+    """Runs `fn` (one launch or call per invocation) untimed until it has kept
+    the GPU busy for `settle_ms` of GPU time (HIP events, checked every 50
+    calls). Returns (host ms per call, GPU ms per call) over the settle.
+    On MI355X the first 20-40 ms of a sustained phase run 5-15 % slower than
+    the rest while the GPU's clocks adjust to it (config 5 decode: 405-416 us
+    per launch over the first 100, then 357 us; config 2: 55 us, then
+    47.5 us), and an idle GPU (a spin kernel holding the stream for 8 ms)
+    loses that state again, so every figure here is taken right after such a
+    settle, with the GPU kept busy in between: the sustained rate a serving
+    loop sees."""
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    t0, n = time.perf_counter(), 0
+    while True:
+        for _ in range(50):
+            fn()
+        n += 50
+        host_ms = (time.perf_counter() - t0) * 1e3 / n
+        e1.record(stream)
+        e1.synchronize()
+        gpu_ms = e0.elapsed_time(e1) / n
+        if gpu_ms * n >= settle_ms:
+            return host_ms, gpu_ms
+
+
+_BLOCK = {}
+
+
+def fill(torch, fn, steps, warmup, host_ms, gpu_ms):
+    """Untimed GPU work queued right before the timed calls, so that the host
+    enqueues the `steps` timed calls while the GPU is still busy and they
+    run back to back: `warmup` or more calls of `fn` when the host issues a
+    call in well under its GPU time, otherwise (calls that cost the host more
+    than the GPU) device copies covering 1.5x the host's enqueue time. Then
+    a one-cycle spin kernel, a marker that puts the timed dispatches right
+    after it in a kernel trace (the GPU idles a few microseconds, not the
+    milliseconds a spin that holds the stream costs)."""
+    if host_ms <= 0.7 * gpu_ms:
+        for _ in range(max(warmup, int(steps * host_ms / (gpu_ms - host_ms)) + 2)):
+            fn()
+    else:
+        for _ in range(warmup):
+            fn()
+        dev = torch.cuda.current_device()
+        if dev not in _BLOCK:
+            _BLOCK[dev] = (torch.empty(256 << 20, dtype=torch.uint8, device="cuda"),
+                           torch.empty(256 << 20, dtype=torch.uint8, device="cuda"))
+        src, dst = _BLOCK[dev]
+        for _ in range(int(1.5 * steps * host_ms / 0.045) + 2):  # a 256 MiB copy takes ~45 us
+            dst.copy_(src)
+    torch.cuda._sleep(1)
+
+
+def time_steps(torch, fn_list, steps, warmup, settle_ms=SETTLE_MS):
     """Returns (ms per step, host wall ms per step).
 
-    `steps` launches run back to back on the current stream between two HIP
-    events recorded on that stream, so the per-step time is the kernel's
-    average duration (plus sub-microsecond dispatch gaps); it matches the
-    AverageNs of `rocprofv3 --kernel-trace --stats` over the same command.
-    For kernels shorter than the host's per-call cost, `pre_sleep_cycles`
-    first parks the stream in a spin kernel (outside the timed region) so the
-    host queues every step before the first one starts.
+    After a settle of `settle_ms` of the same launches (see settle()) and
+    the untimed fill (see fill(); it includes the `warmup` steps), `steps`
+    launches run back to back on the current stream between two HIP events
+    recorded on that stream, so the per-step time is the kernel's average
+    duration (plus sub-microsecond dispatch gaps); it matches the AverageNs
+    of `rocprofv3 --kernel-trace --stats` over the same dispatches.
     """
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        fn_list[i % len(fn_list)]()
-    torch.cuda.synchronize()
+    it = iter(range(1 << 62))
+    nxt = lambda: fn_list[next(it) % len(fn_list)]()  # noqa: E731
+    host_ms, gpu_ms = settle(torch, nxt, settle_ms)
+    fill(torch, nxt, steps, warmup, host_ms, gpu_ms)
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    if pre_sleep_cycles:
-        torch.cuda._sleep(pre_sleep_cycles)
     t_start.record(stream)
     for i in range(steps):
         fn_list[i % len(fn_list)]()
@@ -207,7 +263,7 @@ def bench_fp16_decode(torch, memopt_C, cfg, steps=20):
     q = torch.randn(B, 1, H, D, device=dev, generator=g).half()
     cl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
     calls = [memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, ctx) for bt in tables]
-    ms, _ = time_steps(torch, calls, steps, 5, pre_sleep_cycles=20_000_000)
+    ms, _ = time_steps(torch, calls, steps, 5)
     nbytes = 2 * B * ctx * H * D * 2
     return {"workload": "config 2 decode shape over an fp16 page pool: batch 16, 32 heads, head_dim 128, "
                         "context 4096, 16-token pages, random-permutation block tables",
@@ -226,8 +282,7 @@ def bench_kv_quant(torch, memopt_C, cfg, steps=20):
     v = torch.randn(T, H, D, device=dev, generator=g).half()
     slots = torch.arange(T, dtype=torch.int32, device=dev)
     bt = torch.zeros(1, 1, dtype=torch.int32, device=dev)
-    launch_ms, _ = time_steps(torch, [lambda: memopt_C.write_cache(k, v, bt, slots, validate_slots=False)], steps, 3,
-                              pre_sleep_cycles=20_000_000)
+    launch_ms, _ = time_steps(torch, [lambda: memopt_C.write_cache(k, v, bt, slots, validate_slots=False)], steps, 3)
     elems = 2 * T * H * D
     nbytes = elems * 2.53125
     return {"workload": "write_cache fused quantize, 2 x [16384, 32, 128] fp16 -> INT4 pages",
@@ -354,7 +409,7 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
         calls.append(memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, window, num_sink_tokens=cfg["sinks"]))
         del scores
     nbytes //= copies  # bytes per step (copies are equal up to unlinked pages)
-    ms, _ = time_steps(torch, calls, steps, warmup, pre_sleep_cycles=20_000_000)
+    ms, _ = time_steps(torch, calls, steps, warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
     out = {"kernel": INT4_DECODE_KERNEL, "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
            "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
@@ -362,7 +417,7 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
            "page_sets_rotated": copies,
            "block_tables": "seeded FIFO alloc/free trace" if fifo_trace else "seeded random permutation"}
     if control_copies:
-        cms, _ = time_steps(torch, calls[:control_copies], steps, warmup, pre_sleep_cycles=20_000_000)
+        cms, _ = time_steps(torch, calls[:control_copies], steps, warmup)
         out["rotation_control"] = {"page_sets_rotated": control_copies, "decode_ms": round(cms, 5),
                                    "frac_of_hbm_peak": round(nbytes / (cms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return out
@@ -374,15 +429,17 @@ def time_evict(torch, memopt_C, scores, bt, nb, cfg, reps=7):
     and the work is that of the first call. Each call gets its own copy of the
     block tables (so unlinks do not accumulate) and a fresh vote counter, made
     before the timed region. The calls run back to back between two HIP
-    events, behind a spin kernel that keeps the stream busy while the host
-    enqueues them, like the other figures of this bench; timing each call
-    alone between its own events adds about 6 us of event overhead per call."""
+    events, after a settle and a fill (settle(), fill()) that keep the GPU
+    busy while the host enqueues them, like the other figures of this bench;
+    timing each call alone between its own events adds about 6 us of event
+    overhead per call."""
     btcs = [bt.clone() for _ in range(reps + 1)]
     ibfs = [torch.zeros(nb, dtype=torch.int32, device=bt.device) for _ in range(reps + 1)]
-    memopt_C.evict_tokens(scores, btcs[reps], ibfs[reps], cfg["retain"], cfg["sinks"])  # warm
-    torch.cuda.synchronize()
+    # settle and fill on one scratch copy (the same rows are zeroed again each call)
+    scratch = lambda: memopt_C.evict_tokens(scores, btcs[reps], ibfs[reps], cfg["retain"], cfg["sinks"])  # noqa: E731
+    host_ms, gpu_ms = settle(torch, scratch)
+    fill(torch, scratch, reps, 1, host_ms, gpu_ms)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(8_000_000)
     e0.record()
     for i in range(reps):
         memopt_C.evict_tokens(scores, btcs[i], ibfs[i], cfg["retain"], cfg["sinks"])
@@ -446,7 +503,7 @@ def bench_long_context_policy(torch, memopt_C, cfg, steps=20, warmup=3):
     cl = cache.context_lens(seqs)
     kc, vc = cache.key_value_pools()
     call = memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, ctx, num_sink_tokens=cfg["sinks"])
-    ms, _ = time_steps(torch, [call], steps, warmup, pre_sleep_cycles=20_000_000)
+    ms, _ = time_steps(torch, [call], steps, warmup)
     per_page = H * (2 * bs * (D // 2) + 2 * bs * 2 * (D // 64))
     linked = int((bt >= 0).sum())
     nbytes = linked * per_page
@@ -490,19 +547,9 @@ def main():
 
     cfg = CFG2
     calls, tables, q, cl = setup_decode(torch, memopt_C, cfg, copies=4)
-    # The GPU starts from idle clocks: settle them with ~50 ms of device
-    # copies before the W warm-up steps (nothing here is timed; a kernel other
-    # than the decode kernel, so a profiler's decode average covers only the
-    # warm-up and timed launches).
-    settle_src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
-    settle_dst = torch.empty_like(settle_src)
-    for _ in range(60):
-        settle_dst.copy_(settle_src)
-    torch.cuda.synchronize()
-    del settle_src, settle_dst
-    region_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup, pre_sleep_cycles=20_000_000)
+    region_ms, wall_ms = time_steps(torch, calls, args.steps, args.warmup)
     # control: the same launches rotating over two of the four page sets
-    control_ms, _ = time_steps(torch, calls[:2], args.steps, 20, pre_sleep_cycles=20_000_000)
+    control_ms, _ = time_steps(torch, calls[:2], args.steps, 20, settle_ms=10.0)
     nbytes = effective_kv_bytes(cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"])
     value = nbytes / (region_ms * 1e-3) / 1e9
     achieved = value  # one decode launch per step
