@@ -13,7 +13,8 @@
 //    can be streaming (non-temporal) without a line being fetched twice;
 //  * each wave keeps U chunks in flight (double-buffered batches) and a
 //    workgroup of NW waves interleaves the chunks of one (b, h); split-K
-//    partials (m, l, o) are merged by the shared combine kernel;
+//    partials (m, l, o) are merged by the last workgroup of each (b, h) to
+//    finish, in the shared decode epilogue;
 //  * q . k is v_dot2_f32_f16 over the lane's dims plus 3 DPP steps across
 //    the token's 8 lanes; the softmax running max is wave-uniform and raised
 //    lazily (only when a score exceeds it by more than 8 in log2 units);

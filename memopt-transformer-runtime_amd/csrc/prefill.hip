@@ -817,9 +817,11 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p) {
 //      PV(i) block 0 MFMAs    with exp2 / packing of S(i) block 1,
 //      PV(i) block 1 MFMAs,
 //    so the matrix pipe has independent work while the softmax runs.
-//  * K tiles are copied three tiles ahead (three buffers), V tiles one tile
-//    ahead (two buffers); iteration i reads K(i+1) and V(i) and refills the
+//  * K tiles are copied two tiles ahead and V tiles one tile ahead, two LDS
+//    buffers each; iteration i reads K(i+1) and V(i) and refills the
 //    buffers of K(i) and V(i-1), both last read in iteration i-1.
+//  * A wave computes only the tiles holding keys its own queries see; it
+//    still issues its share of every tile's copies and meets the barriers.
 //  * Workgroup IDs are remapped so that each XCD owns whole heads (a head's
 //    window stays in one L2), longest causal query tiles first.
 template <int D, int NW>
@@ -833,7 +835,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   constexpr int NKL = KBUF / (NT * 16), NVL = VBUF / (NT * 16);  // 16-byte copies per thread per tile
   using L = StageLayout<D>;
   constexpr uint32_t CS = (uint32_t)L::kBlock;  // bytes per staged chunk
-  // Three K buffers and two V buffers: 160 KiB for the two workgroups of a CU at D = 128.
+  // Two K buffers and two V buffers: 128 KiB for the two workgroups of a CU at D = 128.
   __shared__ __attribute__((aligned(16))) uint8_t lds_k0[KBUF], lds_k1[KBUF];
   __shared__ __attribute__((aligned(16))) uint8_t lds_v0[VBUF], lds_v1[VBUF];
 

@@ -113,7 +113,8 @@ def test_decode_int4_token_major_envelope(case):
 
 def test_decode_envelope_split_k():
     """The same large-V case with one sequence long enough for split-K: the
-    per-split reference points differ, and the combine must still agree."""
+    per-split reference points differ, and the in-kernel merge of the
+    split partials must still agree."""
     q, k, v, bt = _envelope_case(20, 2, 128, 16384, 1.0, 1.0, 2e3, 6e4, 7.5)
     cl = np.array([16384], np.int32)
     pages = O.to_int4_pages(k, v)
