@@ -518,6 +518,51 @@ def bench_long_context_policy(torch, memopt_C, cfg, steps=20, warmup=3):
             "block_tables": "fragmented FIFO free list (all pages allocated, freed in a seeded order)"}
 
 
+def decode_page_sweep(torch, memopt_C, cfg=CFG3, copies=4, steps=20):
+    """INT4 decode time against the pages each (b, h) visits, on config 3's
+    shape (B 16, H 32, ctx 8192, random-permutation block tables, `copies`
+    page sets rotated): windows of 1 to 256 pages (and 129 = config 3's
+    2048-token window + the sink page). A least-squares line over the cases
+    of 64 pages and more splits a launch into a fixed cost (intercept) and
+    a streaming rate (slope)."""
+    B, H, D, ctx, bs = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
+    dev = torch.device("cuda", 0)
+    nbps = ctx // bs
+    nb = copies * B * nbps
+    memopt_C.init_pool(1, bs, H, D, kv_format="int4")
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    pages = torch.randperm(nb, generator=torch.Generator().manual_seed(cfg["seed"])).to(torch.int32)
+    gen = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    kc, vc = memopt_C.get_pool_tensors()
+    cl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    bts, qs = [], []
+    for c in range(copies):
+        bt = pages[c * B * nbps:(c + 1) * B * nbps].reshape(B, nbps).to(dev)
+        fill_pages(torch, memopt_C, bt, cfg, gen)
+        bts.append(bt)
+        qs.append(torch.randn(B, 1, H, D, device=dev, generator=gen).half())
+    per_page = H * (2 * bs * (D // 2) + 2 * bs * 2 * (D // 64))
+    cases = []
+    for W, sinks in ((128, 0), (512, 0), (1024, 0), (2048, 0), (2048, 4), (4096, 0), (16, 0)):
+        calls = [memopt_C.PreparedAttention(qs[c], kc, vc, bts[c], cl, ctx, W, num_sink_tokens=sinks)
+                 for c in range(copies)]
+        npages = W // bs + (1 if sinks else 0)
+        ms, _ = time_steps(torch, calls, steps, 3)
+        cases.append({"window": W, "sinks": sinks, "pages_per_bh": npages, "us": round(ms * 1e3, 3),
+                      "frac_of_hbm_peak": round(B * npages * per_page / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    fit = [c for c in cases if c["pages_per_bh"] >= 64]
+    n = len(fit)
+    sx = sum(c["pages_per_bh"] for c in fit)
+    sy = sum(c["us"] for c in fit)
+    sxx = sum(c["pages_per_bh"] ** 2 for c in fit)
+    sxy = sum(c["pages_per_bh"] * c["us"] for c in fit)
+    slope = (n * sxy - sx * sy) / (n * sxx - sx * sx)
+    icpt = (sy - slope * sx) / n
+    return {"workload": "INT4 decode, B 16, H 32, D 128, ctx 8192, window swept", "cases": cases,
+            "fit_fixed_us": round(icpt, 3), "fit_us_per_page": round(slope, 4),
+            "fit_stream_frac_of_hbm_peak": round(B * per_page / (slope * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -527,6 +572,8 @@ def main():
     ap.add_argument("--no-secondary", action="store_true", help="skip secondary figures")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 plain 512 MiB device-to-device copies (scales rocprofv3 byte counters)")
+    ap.add_argument("--decode-sweep", action="store_true",
+                    help="only time INT4 decode against the pages per (b, h) (fixed cost and streaming rate)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the kernels run on one GPU's share of the "
@@ -544,6 +591,9 @@ def main():
         print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "launches": 5}))
         return
     import memopt_C  # noqa: E402  (fails loudly if the HIP library is missing)
+    if args.decode_sweep:
+        print(json.dumps(decode_page_sweep(torch, memopt_C)), flush=True)
+        return
 
     cfg = CFG2
     calls, tables, q, cl = setup_decode(torch, memopt_C, cfg, copies=4)

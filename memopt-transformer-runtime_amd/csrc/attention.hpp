@@ -34,6 +34,19 @@ inline int32_t effective_window(int32_t window, int32_t max_seq_len) {
   return (window <= 0 || window > max_seq_len) ? max_seq_len : window;
 }
 
+// Visible pages (or 16-token chunks) [begin, end) of split `split` of
+// `splits` over n of them, in 32-bit arithmetic: a 64-bit division expands
+// to a long scalar sequence that sits on every decode launch's critical path.
+struct SplitRange {
+  int32_t begin, end;
+};
+__device__ __forceinline__ SplitRange split_range(int32_t n, int32_t split, int32_t splits) {
+  if (splits <= 1) return {0, n};
+  const int32_t q = n / splits, r = n - q * splits;
+  const int32_t begin = split * q + (split < r ? split : r);
+  return {begin, begin + q + (split < r ? 1 : 0)};
+}
+
 struct DecodeParams {
   const half_t *q;
   half_t *out;

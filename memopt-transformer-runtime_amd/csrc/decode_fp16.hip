@@ -46,8 +46,8 @@ __global__ __launch_bounds__(NW * 64) void decode_fp16_kernel(const DecodeParams
   const int32_t sink_c = min((kr.sink_end + 15) >> 4, hi_c);
   const int32_t win_c0 = max(kr.win_lo >> 4, sink_c);
   const int64_t n_vis = (int64_t)sink_c + max(0, hi_c - win_c0);
-  const int32_t begin = (int32_t)((n_vis * split) / p.splits);
-  const int32_t end = (int32_t)((n_vis * (split + 1)) / p.splits);
+  const SplitRange sr = split_range((int32_t)n_vis, split, p.splits);
+  const int32_t begin = sr.begin, end = sr.end;
   const int32_t cpp_shift = __builtin_ctz((uint32_t)(p.bs >> 4));  // chunks per page = 2^shift
 
   // q over the lane's dims: 8 per line, dims 64 n + 8 c .. 64 n + 8 c + 7.

@@ -152,8 +152,8 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_kernel(const DecodeParams
   const int32_t win_page0 = max(kr.win_lo >> 4, sink_pages);
   const int32_t n_win = max(0, last_page - win_page0);
   const int64_t n_vis = (int64_t)sink_pages + n_win;
-  const int32_t begin = (int32_t)((n_vis * split) / p.splits);
-  const int32_t end = (int32_t)((n_vis * (split + 1)) / p.splits);
+  const SplitRange sr = split_range((int32_t)n_vis, split, p.splits);
+  const int32_t begin = sr.begin, end = sr.end;
 
   // q as fp16 pairs in unpack order + the bias sum q . (bias + 8).
   half2_t qp[NWORD][4];
@@ -300,8 +300,8 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
   const int32_t win_page0 = max(kr.win_lo >> 4, sink_pages);
   const int32_t n_win = max(0, last_page - win_page0);
   const int64_t n_vis = (int64_t)sink_pages + n_win;
-  const int32_t begin = (int32_t)((n_vis * split) / p.splits);
-  const int32_t end = (int32_t)((n_vis * (split + 1)) / p.splits);
+  const SplitRange sr = split_range((int32_t)n_vis, split, p.splits);
+  const int32_t begin = sr.begin, end = sr.end;
 
   // q for this lane's dims as fp16 pairs in unpack order; the dot products
   // start from -q . (bias + 8) so they end at q . (code - 8).
@@ -342,22 +342,22 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
   const int32_t nb32 = (int32_t)min(p.nb, (int64_t)INT32_MAX);
 
   // Page batches of U pages are double-buffered: the loads of batch n+1 are
-  // in flight while batch n is consumed. Slots past `end` (and unlinked
-  // pages) load page 0 of this head, which is always mapped and L2-resident
-  // after the first touch, and are masked out.
+  // in flight while batch n is consumed. Slots past their limit (and
+  // unlinked pages) load page 0 of this head, which is always mapped and
+  // L2-resident after the first touch, and are masked out.
   struct Batch {
     Chunk kw[U], vw[U];
     half2_t sk[U], sv[U];
     int32_t lp[U];
     bool ok[U];
   };
-  auto issue = [&](Batch &bt, int32_t base) {
+  auto issue_lim = [&](Batch &bt, int32_t base, int32_t lim) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int32_t i = base + u;
       bt.lp[u] = (i < sink_pages) ? i : win_page0 + (i - sink_pages);
-      const int32_t phys = btrow[(i < end) ? bt.lp[u] : 0];  // lp < M whenever i < end
-      bt.ok[u] = (i < end) && phys >= 0 && phys < nb32;
+      const int32_t phys = btrow[(i < lim) ? bt.lp[u] : 0];  // lp < M whenever i < lim <= end
+      bt.ok[u] = (i < lim) && phys >= 0 && phys < nb32;
       const int64_t pg = bt.ok[u] ? (int64_t)phys : 0;
       const __amdgpu_buffer_rsrc_t r = block_rsrc(uniform_ptr(hbase + pg * p.kv_ps));
       bt.kw[u].load(r, koff);
@@ -366,6 +366,7 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
       bt.sv[u] = as_half2(__builtin_amdgcn_raw_buffer_load_b32(r, (int)vsoff, 0, kStreamLoad));
     }
   };
+  auto issue = [&](Batch &bt, int32_t base) { issue_lim(bt, base, end); };
   auto consume = [&](const Batch &bt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -447,10 +448,18 @@ __global__ __launch_bounds__(NW * 64) void decode_int4_pages_kernel(const Decode
     }
   };
 
+  // The (end - begin) % kStep pages left over by whole steps come first,
+  // one batch to each of the first waves, issued together with that wave's
+  // first regular batch: every wave then runs the same number of steps, and
+  // a leftover page does not cost the workgroup a last step of its own.
   constexpr int32_t kStep = NW * U;
+  const int32_t rem = (end - begin) % kStep, rbeg = begin + rem;
+  const bool extra = wave * U < rem;  // wave-uniform
   Batch ba, bb;
-  int32_t base = begin + wave * U;
+  int32_t base = rbeg + wave * U;
+  if (extra) issue_lim(bb, begin + wave * U, rbeg);
   issue(ba, base);
+  if (extra) consume(bb);
   while (base < end) {
     issue(bb, base + kStep);
     consume(ba);
