@@ -18,7 +18,8 @@ torch CPU path, restated in oracle/, on a bounded sample), and secondary
 figures (prefill MFMA use, sparse and long-context decode with evict_tokens,
 the KV-quant write path, and config 2's decode shape over an fp16 page pool).
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 200] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 200] [--no-cpu] [--no-secondary]
+       python bench.py --calibrate-copy | --decode-sweep
 """
 from __future__ import annotations
 

@@ -29,6 +29,9 @@
 //    exceed 2^8); scores stay unscaled fp32 q . k and exp2 takes
 //    log2(e) / sqrt(D) (score - m), so no scaled copy of Q is rounded.
 #include "attention.hpp"
+#include <algorithm>
+#include <atomic>
+#include <cstdlib>
 #include "page_format.hpp"
 
 namespace memopt {
@@ -604,129 +607,175 @@ struct StageLayout {
   static constexpr int64_t kVPart = 16 * D * 2;      // byte offset of V^T in a block
 };
 
-// One wave per (sequence b, head h, chunk lc); lane l = 8p + c owns tokens
-// (p, p + 8) x dims [c*D/8, (c+1)*D/8), as in the INT4 page format.
-template <int D, bool INT4>
-__global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams p, uint8_t *__restrict__ ws,
-                                                            int32_t MC, int32_t units) {
+// Stages the workspace blocks of slots slot0 + i * sstride, i < n <= N, of
+// (sequence, head) bh with one wave: the blocks' page lookups (scalar
+// loads), then every block's page loads, are issued before anything waits
+// for them, so the N blocks cost one chain of memory round trips. Block
+// = bh * MC + slot; lane l = 8p + c owns tokens (p, p + 8) x dims
+// [c*D/8, (c+1)*D/8), as in the INT4 page format. vl: the wave's 32 * D
+// bytes of LDS (the V^T transpose). all_flags: write each slot's link flag
+// from every head (else head 0's wave writes it).
+template <int D, bool INT4, int N>
+__device__ __forceinline__ void stage_blocks(const PrefillParams &p, uint8_t *__restrict__ ws, int32_t MC,
+                                             int32_t units, int32_t bh, int32_t slot0, int32_t sstride, int32_t n,
+                                             uint8_t *vl, bool all_flags) {
   constexpr int DPL = D / 8;
   using L = StageLayout<D>;
   const int lane = threadIdx.x & 63;
-  const int32_t unit = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (unit >= units) return;  // wave-uniform
-  const int32_t slot = unit % MC, bh = unit / MC, h = bh % p.H, b = bh / p.H;
   const int pp = lane >> 3, c = lane & 7;
-  const int32_t ctx = p.ctx[b];
-  const int32_t kv_lim = min(ctx, p.M * p.bs);
+  bh = __builtin_amdgcn_readfirstlane(bh);
+  slot0 = __builtin_amdgcn_readfirstlane(slot0);
+  const int32_t b = bh / p.H, h = bh % p.H;
+  const int32_t ctx = __builtin_amdgcn_readfirstlane(p.ctx[b]);
+  const int32_t kvl = min(ctx, p.M * p.bs);
   const StageMap sm = stage_map(ctx, p.M * p.bs, p.Lq, p.W, p.sinks, p.causal != 0);
-  if (slot >= sm.hi - sm.off) return;  // wave-uniform: no chunk maps here
-  const int32_t lc = slot < sm.sc ? slot : slot + sm.off;
-  const int32_t key0 = lc * 16;
-  int32_t pg = -1;
-  if (key0 < kv_lim) {
-    const int32_t e = p.bt[(int64_t)b * p.M + key0 / p.bs];
-    pg = (e >= 0 && e < p.nb) ? e : -1;
+  int32_t key0[N], pg[N], slot[N];
+  bool live[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    slot[i] = slot0 + i * sstride;
+    live[i] = i < n && slot[i] < sm.hi - sm.off;  // wave-uniform: a slot past the map holds no chunk
+    const int32_t lc = slot[i] < sm.sc ? slot[i] : slot[i] + sm.off;
+    key0[i] = lc * 16;
+    const bool in = live[i] && key0[i] < kvl;
+    const int32_t e = p.bt[(int64_t)b * p.M + (in ? key0[i] / p.bs : 0)];  // loaded unconditionally
+    pg[i] = (in && e >= 0 && e < p.nb) ? e : -1;
   }
-  uint8_t *blk = ws + (int64_t)unit * L::kBlock;
-  uint32_t kw0[DPL / 2], kw1[DPL / 2];  // K halves of tokens pp, pp + 8 (unpack order), as packed pairs
-  uint32_t vw[DPL];                     // V: dim d -> {token pp, token pp + 8}
-  if (pg < 0) {
-#pragma unroll
-    for (int i = 0; i < DPL / 2; ++i) kw0[i] = kw1[i] = 0;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) vw[i] = 0;
-  } else if constexpr (INT4) {
+  // raw page words (INT4): K codes of tokens pp, pp + 8, V codes, the scale pairs
+  uint32_t kraw[INT4 ? N : 1][DPL / 4], vraw[INT4 ? N : 1][DPL / 4], skr[N], svr[N];
+  if constexpr (INT4) {
+    // (unconditional loads: a block with no page reads page 0, which is
+    // mapped, and its values are not used)
     const Int4Page f(D);
-    const uint8_t *src = p.pool + ((int64_t)pg * p.H + h) * f.block;
-    const int slot = 8 * pp + c, g = (c * DPL) / 64;
-    const half2_t sk = as_half2(*reinterpret_cast<const uint32_t *>(src + f.kscales + 2 * (g * 16 + 2 * pp)));
-    const half2_t sv = as_half2(*reinterpret_cast<const uint32_t *>(src + f.vscales + 2 * (g * 16 + 2 * pp)));
-    const half2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f}, b72 = {(half_t)72.0f, (half_t)72.0f};
-    const uint32_t *kc32 = reinterpret_cast<const uint32_t *>(src + f.kcodes + slot * f.BPL);
-    const uint32_t *vc32 = reinterpret_cast<const uint32_t *>(src + f.vcodes + slot * f.BPL);
+    const int sl = 8 * pp + c, g = (c * DPL) / 64;
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      const half2_t s2 = t2 ? half2_t{sk.y, sk.y} : half2_t{sk.x, sk.x};
-      uint32_t *dst = t2 ? kw1 : kw0;
+    for (int i = 0; i < N; ++i) {
+      const uint8_t *src = p.pool + ((int64_t)(pg[i] >= 0 ? pg[i] : 0) * p.H + h) * f.block;
+      const uint32_t *kc32 = reinterpret_cast<const uint32_t *>(src + f.kcodes + sl * f.BPL);
+      const uint32_t *vc32 = reinterpret_cast<const uint32_t *>(src + f.vcodes + sl * f.BPL);
 #pragma unroll
-      for (int wi = 0; wi < DPL / 8; ++wi) {
-        const uint32_t w = kc32[t2 * (DPL / 8) + wi], w8 = w >> 8;
-        dst[4 * wi + 0] = as_u32((as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * s2);
-        dst[4 * wi + 1] = as_u32((as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * s2);
-        dst[4 * wi + 2] = as_u32((as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * s2);
-        dst[4 * wi + 3] = as_u32((as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * s2);
+      for (int w = 0; w < DPL / 4; ++w) {
+        kraw[i][w] = kc32[w];
+        vraw[i][w] = vc32[w];
+      }
+      skr[i] = *reinterpret_cast<const uint32_t *>(src + f.kscales + 2 * (g * 16 + 2 * pp));
+      svr[i] = *reinterpret_cast<const uint32_t *>(src + f.vscales + 2 * (g * 16 + 2 * pp));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (!live[i]) continue;  // wave-uniform
+    uint8_t *blk = ws + ((int64_t)bh * MC + slot[i]) * L::kBlock;
+    uint32_t kw0[DPL / 2], kw1[DPL / 2];  // K halves of tokens pp, pp + 8 (unpack order), as packed pairs
+    uint32_t vw[DPL];                     // V: dim d -> {token pp, token pp + 8}
+    if (pg[i] < 0) {
+#pragma unroll
+      for (int k = 0; k < DPL / 2; ++k) kw0[k] = kw1[k] = 0;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) vw[k] = 0;
+    } else if constexpr (INT4) {
+      const half2_t sk = as_half2(skr[i]), sv = as_half2(svr[i]);
+      const half2_t b1032 = {(half_t)1032.0f, (half_t)1032.0f}, b72 = {(half_t)72.0f, (half_t)72.0f};
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const half2_t s2 = t2 ? half2_t{sk.y, sk.y} : half2_t{sk.x, sk.x};
+        uint32_t *dst = t2 ? kw1 : kw0;
+#pragma unroll
+        for (int wi = 0; wi < DPL / 8; ++wi) {
+          const uint32_t w = kraw[i][t2 * (DPL / 8) + wi], w8 = w >> 8;
+          dst[4 * wi + 0] = as_u32((as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * s2);
+          dst[4 * wi + 1] = as_u32((as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * s2);
+          dst[4 * wi + 2] = as_u32((as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * s2);
+          dst[4 * wi + 3] = as_u32((as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * s2);
+        }
+      }
+#pragma unroll
+      for (int wi = 0; wi < DPL / 4; ++wi) {
+        const uint32_t w = vraw[i][wi], w8 = w >> 8;
+        vw[4 * wi + 0] = as_u32((as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * sv);
+        vw[4 * wi + 1] = as_u32((as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * sv);
+        vw[4 * wi + 2] = as_u32((as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * sv);
+        vw[4 * wi + 3] = as_u32((as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * sv);
+      }
+    } else {
+      const half_t *kp = reinterpret_cast<const half_t *>(p.pool);
+      const half_t *vp = reinterpret_cast<const half_t *>(p.vpool);
+      const int32_t pos0 = key0[i] % p.bs;  // a 16-token chunk lies in one page (bs % 16 == 0)
+      const int64_t r0 = (((int64_t)pg[i] * p.bs + pos0 + pp) * p.H + h) * D + c * DPL;
+      const int64_t r1 = r0 + 8LL * p.H * D;
+#pragma unroll
+      for (int k = 0; k < DPL / 8; ++k) {
+        const half8_t k0 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(kp + r0 + 8 * k));
+        const half8_t k1 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(kp + r1 + 8 * k));
+        const half8_t v0 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(vp + r0 + 8 * k));
+        const half8_t v1 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(vp + r1 + 8 * k));
+        // K in unpack order (0,4,1,5,2,6,3,7) within each 8-dim group
+        kw0[4 * k + 0] = as_u32(half2_t{k0[0], k0[4]}); kw0[4 * k + 1] = as_u32(half2_t{k0[1], k0[5]});
+        kw0[4 * k + 2] = as_u32(half2_t{k0[2], k0[6]}); kw0[4 * k + 3] = as_u32(half2_t{k0[3], k0[7]});
+        kw1[4 * k + 0] = as_u32(half2_t{k1[0], k1[4]}); kw1[4 * k + 1] = as_u32(half2_t{k1[1], k1[5]});
+        kw1[4 * k + 2] = as_u32(half2_t{k1[2], k1[6]}); kw1[4 * k + 3] = as_u32(half2_t{k1[3], k1[7]});
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vw[8 * k + e] = as_u32(half2_t{v0[e], v1[e]});
       }
     }
+    // Tokens at or past the context length stage as zeros: a page's unused
+    // tail may hold any bits (NaN included), and P = 0 must not meet them in PV.
+    if (key0[i] + pp >= kvl) {
 #pragma unroll
-    for (int wi = 0; wi < DPL / 4; ++wi) {
-      const uint32_t w = vc32[wi], w8 = w >> 8;
-      vw[4 * wi + 0] = as_u32((as_half2(bfi(0x000F000Fu, w, 0x64006400u)) - b1032) * sv);
-      vw[4 * wi + 1] = as_u32((as_half2(bfi(0x00F000F0u, w, 0x54005400u)) - b72) * sv);
-      vw[4 * wi + 2] = as_u32((as_half2(bfi(0x000F000Fu, w8, 0x64006400u)) - b1032) * sv);
-      vw[4 * wi + 3] = as_u32((as_half2(bfi(0x00F000F0u, w8, 0x54005400u)) - b72) * sv);
+      for (int k = 0; k < DPL / 2; ++k) kw0[k] = 0;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) vw[k] &= 0xFFFF0000u;
     }
-  } else {
-    const half_t *kp = reinterpret_cast<const half_t *>(p.pool);
-    const half_t *vp = reinterpret_cast<const half_t *>(p.vpool);
-    const int32_t pos0 = key0 % p.bs;  // a 16-token chunk lies in one page (bs % 16 == 0)
-    const int64_t r0 = (((int64_t)pg * p.bs + pos0 + pp) * p.H + h) * D + c * DPL;
-    const int64_t r1 = r0 + 8LL * p.H * D;
+    if (key0[i] + pp + 8 >= kvl) {
 #pragma unroll
-    for (int i = 0; i < DPL / 8; ++i) {
-      const half8_t k0 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(kp + r0 + 8 * i));
-      const half8_t k1 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(kp + r1 + 8 * i));
-      const half8_t v0 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(vp + r0 + 8 * i));
-      const half8_t v1 = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(vp + r1 + 8 * i));
-      // K in unpack order (0,4,1,5,2,6,3,7) within each 8-dim group
-      kw0[4 * i + 0] = as_u32(half2_t{k0[0], k0[4]}); kw0[4 * i + 1] = as_u32(half2_t{k0[1], k0[5]});
-      kw0[4 * i + 2] = as_u32(half2_t{k0[2], k0[6]}); kw0[4 * i + 3] = as_u32(half2_t{k0[3], k0[7]});
-      kw1[4 * i + 0] = as_u32(half2_t{k1[0], k1[4]}); kw1[4 * i + 1] = as_u32(half2_t{k1[1], k1[5]});
-      kw1[4 * i + 2] = as_u32(half2_t{k1[2], k1[6]}); kw1[4 * i + 3] = as_u32(half2_t{k1[3], k1[7]});
+      for (int k = 0; k < DPL / 2; ++k) kw1[k] = 0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vw[8 * i + e] = as_u32(half2_t{v0[e], v1[e]});
+      for (int k = 0; k < DPL; ++k) vw[k] &= 0x0000FFFFu;
     }
+    // V dims come out of the INT4 unpack in order d, d+1, d+2, d+3 per word;
+    // K words are already in unpack order for both sources.
+    uint8_t *krow0 = blk + (2 * pp) * (2 * D) + c * DPL * 2;
+#pragma unroll
+    for (int k = 0; k < DPL / 8; ++k) {
+      *reinterpret_cast<u32x4 *>(krow0 + 16 * k) = u32x4{kw0[4 * k], kw0[4 * k + 1], kw0[4 * k + 2], kw0[4 * k + 3]};
+      *reinterpret_cast<u32x4 *>(krow0 + 2 * D + 16 * k) =
+          u32x4{kw1[4 * k], kw1[4 * k + 1], kw1[4 * k + 2], kw1[4 * k + 3]};
+    }
+    // V^T goes through LDS: the 4-byte pieces of a lane (two tokens of one
+    // dim) land in the block's layout there, and the wave then writes the
+    // block as contiguous 16-byte stores; written directly, the scattered
+    // 4-byte stores cost twice the K stores for the same bytes.
+    const int vc = chunk_vcol(pp);
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) *reinterpret_cast<uint32_t *>(vl + (c * DPL + d) * 32 + vc * 2) = vw[d];
+    // One wave's LDS accesses complete in order; the clobber keeps the
+    // compiler from moving the reads above the writes.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < 32 * D / 1024; ++k)
+      *reinterpret_cast<u32x4 *>(blk + L::kVPart + k * 1024 + lane * 16) =
+          *reinterpret_cast<const u32x4 *>(vl + k * 1024 + lane * 16);
+    if ((all_flags || h == 0) && lane == 0)
+      reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + slot[i]] = pg[i] >= 0 ? 1 : 0;
+    // The LDS reads above are complete before the next block (or the
+    // caller) reuses vl.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
-  // Tokens at or past the context length stage as zeros: a page's unused
-  // tail may hold any bits (NaN included), and P = 0 must not meet them in PV.
-  if (key0 + pp >= kv_lim) {
-#pragma unroll
-    for (int i = 0; i < DPL / 2; ++i) kw0[i] = 0;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) vw[i] &= 0xFFFF0000u;
-  }
-  if (key0 + pp + 8 >= kv_lim) {
-#pragma unroll
-    for (int i = 0; i < DPL / 2; ++i) kw1[i] = 0;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) vw[i] &= 0x0000FFFFu;
-  }
-  // V dims come out of the INT4 unpack in order d, d+1, d+2, d+3 per word; K
-  // words are already in unpack order for both sources.
-  uint8_t *krow0 = blk + (2 * pp) * (2 * D) + c * DPL * 2;
-#pragma unroll
-  for (int i = 0; i < DPL / 8; ++i) {
-    *reinterpret_cast<u32x4 *>(krow0 + 16 * i) = u32x4{kw0[4 * i], kw0[4 * i + 1], kw0[4 * i + 2], kw0[4 * i + 3]};
-    *reinterpret_cast<u32x4 *>(krow0 + 2 * D + 16 * i) =
-        u32x4{kw1[4 * i], kw1[4 * i + 1], kw1[4 * i + 2], kw1[4 * i + 3]};
-  }
-  // V^T goes through LDS: the 4-byte pieces of a lane (two tokens of one
-  // dim) land in the block's layout there, and the wave then writes the
-  // block as contiguous 16-byte stores; written directly, the scattered
-  // 4-byte stores cost twice the K stores for the same bytes.
-  const int vc = chunk_vcol(pp);
+}
+
+// One wave per workspace block: block q * MC + slot, q < nblocks / MC, of
+// (sequence, head) q * ustride (ustride 1: every block of the workspace,
+// head 0's writing the link flags; otherwise every head writes them, as
+// the staged units need not include head 0 of each sequence).
+template <int D, bool INT4>
+__global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams p, uint8_t *__restrict__ ws,
+                                                            int32_t MC, int32_t units, int32_t ustride,
+                                                            int32_t nblocks) {
+  const int32_t idx = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (idx >= nblocks) return;  // wave-uniform
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[4][32 * D];
-  uint8_t *vl = vt_lds[threadIdx.x >> 6];
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) *reinterpret_cast<uint32_t *>(vl + (c * DPL + d) * 32 + vc * 2) = vw[d];
-  // One wave's LDS accesses complete in order; the clobber keeps the compiler
-  // from moving the reads above the writes.
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-  for (int k = 0; k < 32 * D / 1024; ++k)
-    *reinterpret_cast<u32x4 *>(blk + L::kVPart + k * 1024 + lane * 16) =
-        *reinterpret_cast<const u32x4 *>(vl + k * 1024 + lane * 16);
-  if (h == 0 && lane == 0)
-    reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + slot] = pg >= 0 ? 1 : 0;
+  stage_blocks<D, INT4, 1>(p, ws, MC, units, (idx / MC) * ustride, idx % MC, 1, 1, vt_lds[threadIdx.x >> 6],
+                           ustride != 1);
 }
 
 template <int N>
@@ -824,10 +873,25 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p) {
 //    still issues its share of every tile's copies and meets the barriers.
 //  * Workgroup IDs are remapped so that each XCD owns whole heads (a head's
 //    window stays in one L2), longest causal query tiles first.
-template <int D, int NW>
+//  * STAGE: the workspace is staged by this kernel instead of a staging
+//    launch before it (StageSched), except for the first (sequence, head)
+//    unit of each XCD, which a staging launch of those units only stages:
+//    each XCD runs whole units one after another, and the first S
+//    workgroups of a unit stage 1/S of the next unit's blocks at their
+//    start, so the staging rides on memory bandwidth the MFMA-bound pass
+//    leaves idle.
+struct StageSched {
+  uint32_t *flags;  // [sequence * H + head][64]: the call's tag once stager j's blocks are stored
+  uint32_t tag;     // this call's id (nonzero)
+  int32_t S;        // stagers per unit (<= 64)
+  int32_t spin;     // wait bound (polls); past it a workgroup stages its unit itself (< 0: always)
+};
+
+template <int D, int NW, bool STAGE, bool INT4>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(const PrefillParams p,
-                                                                                const uint8_t *__restrict__ ws,
-                                                                                int32_t MC, int32_t units) {
+                                                                                uint8_t *__restrict__ ws,
+                                                                                int32_t MC, int32_t units,
+                                                                                const StageSched ss) {
   constexpr int TK = 64, NT = NW * 64;
   constexpr int KRB = 2 * D, KC = KRB / 16, VRB = TK * 2;
   constexpr int KBUF = TK * KRB, VBUF = D * VRB;
@@ -849,6 +913,46 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   if (wg < n8) wg = (wg & 7) * (n8 >> 3) + (wg >> 3);
   const int32_t qt = nqt - 1 - wg % nqt;
   const int32_t h = (wg / nqt) % p.H, b = wg / (nqt * p.H);
+  uint32_t stage_flag = 0;
+  bool stage_wait = false;
+  int32_t stage_unit = 0;
+  if constexpr (STAGE) {
+    // Position on this XCD: unit k of its sequence of units, workgroup j of
+    // that unit (the host launches this form only when every XCD owns whole
+    // units: gridDim.x % 8 == 0 and (gridDim.x / 8) % nqt == 0). A stager
+    // and the workgroups reading what it staged run on one XCD and share its
+    // L2: the GPU places workgroup i on XCD i % (XCDs in the partition), and
+    // every MI355X partition has 8, 4, 2 or 1 XCDs, so workgroups with equal
+    // i % 8 share an XCD.
+    const int32_t P = (int32_t)(gridDim.x >> 3), i = wg % P, k = i / nqt, j = i % nqt, U = wg / nqt;
+    uint8_t *vl = lds_k0 + wave * 32 * D;  // free until the first tile copy
+    // Share j of S of unit u, slots [s0, s1): wave w takes s0 + w, s0 + w +
+    // NW, ..., eight blocks per stage_blocks call (INT4; one for fp16
+    // pools). Then the
+    // workgroup's flag for unit u, flags[u * 64 + j] = tag, once its stores
+    // are complete.
+    auto stage_share = [&](int32_t u, int32_t S) {
+      const int32_t s0 = (int32_t)((int64_t)j * MC / S), s1 = (int32_t)((int64_t)(j + 1) * MC / S);
+      constexpr int NB = INT4 ? 8 : 1;
+      for (int32_t sl = s0 + wave; sl < s1; sl += NB * NW)
+        stage_blocks<D, INT4, NB>(p, ws, MC, units, u, sl, NW, min(NB, (s1 - sl + NW - 1) / NW), vl, true);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores are complete
+      __syncthreads();
+      if (threadIdx.x == 0)
+        __hip_atomic_store(ss.flags + (int64_t)u * 64 + j, ss.tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if (k + 1 < P / nqt && j < ss.S) stage_share(U + 1, ss.S);
+    // The first poll of this unit's stagers' flags (wave 0, lane l < S polls
+    // stager l) is issued now and checked before the first read of the
+    // workspace, so its round trip overlaps the setup below. The XCD's
+    // first unit was staged by the launch before this one.
+    if (k > 0 && wave == 0)
+      stage_flag = lane < ss.S ? __hip_atomic_load(ss.flags + (int64_t)U * 64 + lane, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : ss.tag;
+    stage_wait = k > 0;
+    stage_unit = U;
+  }
   const int32_t ctx = p.ctx[b];
   const int32_t kv_lim = min(ctx, p.M * p.bs);
   const int32_t q0 = qt * 32 * NW;
@@ -921,6 +1025,34 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   // for every chunk the workgroup visits. In a workgroup with an unlinked
   // chunk every tile takes the mask, which loads the link flags itself, so
   // the common path carries no flag loads.
+  if constexpr (STAGE) {
+    // Wait for this unit's stagers: workgroups dispatched a unit earlier,
+    // which stage before they wait for anything. Past the bound (stagers not
+    // resident) the workgroup stages its whole unit itself: the same bytes,
+    // so a concurrent stager's writes agree.
+    __shared__ int s_ok;
+    if (stage_wait) {  // workgroup-uniform
+      if (wave == 0) {
+        bool ok = ss.spin >= 0 && __all(stage_flag == ss.tag);
+        for (int32_t n = 0; n < ss.spin && !ok; ++n) {
+          __builtin_amdgcn_s_sleep(4);
+          const uint32_t v = lane < ss.S ? __hip_atomic_load(ss.flags + (int64_t)stage_unit * 64 + lane,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                         : ss.tag;
+          ok = __all(v == ss.tag);
+        }
+        if (lane == 0) s_ok = ok;
+      }
+      __syncthreads();
+      if (!s_ok) {
+        uint8_t *vl = lds_k0 + wave * 32 * D;  // free until the first tile copy
+        for (int32_t sl = wave; sl < MC; sl += NW)
+          stage_blocks<D, INT4, 1>(p, ws, MC, units, stage_unit, sl, NW, 1, vl, true);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
+    }
+  }
   int32_t it_full = 0, n_full = 0;
   {
     bool first = true;
@@ -1350,12 +1482,37 @@ static int64_t staged_chunks(const memopt_attn_desc &d) {
   return bound < full ? bound : full;
 }
 
+// Workspace: the staged blocks, one link flag per (sequence, slot), then
+// 64 in-kernel staging flags per (sequence, head), 8-byte aligned.
+static int64_t stage_counters_offset(const memopt_attn_desc &d, int64_t mc) {
+  const int64_t units = (int64_t)d.batch * mc * d.num_heads;
+  return (units * (64LL * d.head_dim) + (int64_t)d.batch * mc * 4 + 7) / 8 * 8;
+}
+
 int64_t prefill_workspace_bytes(const memopt_attn_desc &d) {
   const int64_t mc = staged_chunks(d);
   const int64_t units = (int64_t)d.batch * mc * d.num_heads;
   // one sequence's chunks must stay inside a 31-bit buffer range
   if (units <= 0 || units >= (1LL << 31) || mc * d.num_heads * 64LL * d.head_dim >= (1LL << 31)) return 0;
-  return units * (64LL * d.head_dim) + (int64_t)d.batch * mc * 4;
+  return stage_counters_offset(d, mc) + (int64_t)d.batch * d.num_heads * 64 * 4;
+}
+
+static int prefill_device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+      cus = prop.multiProcessorCount;
+    if (cus <= 0) cus = 256;
+  }
+  return cus;
+}
+
+// Id of a prefill call for the in-kernel staging flags: 1 .. 2^32 - 1.
+static uint32_t next_prefill_tag() {
+  static std::atomic<unsigned long long> n{0};
+  return (uint32_t)(n.fetch_add(1, std::memory_order_relaxed) % 0xFFFFFFFFull + 1);
 }
 
 int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hipStream_t stream) {
@@ -1386,14 +1543,65 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
     uint8_t *ws = (uint8_t *)d.workspace;
     const dim3 sgrid((unsigned)((units + 3) / 4)), grid((unsigned)n_wg);
     const bool int4 = d.kv_format == MEMOPT_KV_INT4;
+    // In-kernel staging when every XCD owns whole (sequence, head) units of
+    // at least 32 query tiles: a staging launch stages each XCD's first
+    // unit, and the first S = min(nqt / 4, 32) workgroups of every unit the
+    // next one (fewer, larger shares cost less waiting in all).
+    const int64_t nqt = (d.q_len + 32 * NW - 1) / (32 * NW);
+    const int64_t per_xcd = n_wg / 8;
+    StageSched ss{};
+    ss.S = (int32_t)std::min<int64_t>(nqt / 4, 32);
+    // (MEMOPT_PREFILL_STAGE_LAUNCH selects the staging launch for every
+    // call, so that tests can compare the two paths.)
+    const bool in_kernel = n_wg % 8 == 0 && nqt >= 32 && per_xcd % nqt == 0 &&
+                           std::getenv("MEMOPT_PREFILL_STAGE_LAUNCH") == nullptr;
+    if (in_kernel) {
+      ss.flags = reinterpret_cast<uint32_t *>(ws + stage_counters_offset(d, mc));
+      ss.tag = next_prefill_tag();
+      // MEMOPT_PREFILL_STAGE_SPIN overrides the wait bound (a negative value
+      // makes every waiting workgroup stage its unit itself: a test hook for
+      // that path).
+      const char *spin = std::getenv("MEMOPT_PREFILL_STAGE_SPIN");
+      ss.spin = spin ? std::atoi(spin) : 200000;
+      const int32_t upx = (int32_t)(per_xcd / nqt), first = 8 * mc;
+      const dim3 fgrid((unsigned)((first + 3) / 4));
+      if (d.head_dim == 128) {
+        if (int4) {
+          hipLaunchKernelGGL((prefill_stage_kernel<128, true>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
+                             first);
+          hipLaunchKernelGGL((prefill_pipe_kernel<128, NW, true, true>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
+                             units, ss);
+        } else {
+          hipLaunchKernelGGL((prefill_stage_kernel<128, false>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
+                             first);
+          hipLaunchKernelGGL((prefill_pipe_kernel<128, NW, true, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
+                             units, ss);
+        }
+      } else {
+        if (int4) {
+          hipLaunchKernelGGL((prefill_stage_kernel<64, true>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
+                             first);
+          hipLaunchKernelGGL((prefill_pipe_kernel<64, NW, true, true>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
+                             units, ss);
+        } else {
+          hipLaunchKernelGGL((prefill_stage_kernel<64, false>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
+                             first);
+          hipLaunchKernelGGL((prefill_pipe_kernel<64, NW, true, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
+                             units, ss);
+        }
+      }
+      return check_launch("paged_attention(prefill, staged in kernel)");
+    }
     if (d.head_dim == 128) {
-      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<128, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      else hipLaunchKernelGGL((prefill_stage_kernel<128, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      hipLaunchKernelGGL((prefill_pipe_kernel<128, NW>), grid, dim3(NW * 64), 0, stream, p, ws, mc, units);
+      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<128, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
+      else hipLaunchKernelGGL((prefill_stage_kernel<128, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
+      hipLaunchKernelGGL((prefill_pipe_kernel<128, NW, false, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
+                         units, ss);
     } else {
-      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<64, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      else hipLaunchKernelGGL((prefill_stage_kernel<64, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units);
-      hipLaunchKernelGGL((prefill_pipe_kernel<64, NW>), grid, dim3(NW * 64), 0, stream, p, ws, mc, units);
+      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<64, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
+      else hipLaunchKernelGGL((prefill_stage_kernel<64, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
+      hipLaunchKernelGGL((prefill_pipe_kernel<64, NW, false, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
+                         units, ss);
     }
     return check_launch("paged_attention(prefill, staged)");
   }

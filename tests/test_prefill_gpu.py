@@ -278,3 +278,62 @@ def test_config4_full_rows_int4_pages():
             ref = _fp32_head_reference(q[0, :, h], kd[:, h], vd[:, h], r0, r0 + 2048, S, W, sinks)
             assert_close(out[0, r0:r0 + 2048, h], ref, what=f"config 4 head {h} rows {r0}..{r0 + 2047}")
     torch.cuda.synchronize()
+
+
+def _prefill_with_env(env, *args, **kw):
+    """One attention call with the given environment overrides in place."""
+    import os
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        out = memopt_C.dynamic_sparse_attention(*args, **kw)
+        torch.cuda.synchronize()
+        return out
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def test_in_kernel_staging_paths_agree():
+    """Long causal prefill (q_len 4096, so the attention kernel stages the
+    workspace itself: each XCD's first (sequence, head) unit by a staging
+    launch, every later unit by the first workgroups of the unit before it)
+    over three sequences whose first units on the XCDs include no head 0 of
+    sequences 1 and 2, with unlinked pages in both: the in-kernel path, the
+    staging-launch path (MEMOPT_PREFILL_STAGE_LAUNCH) and the path where every
+    waiting workgroup stages its unit itself (MEMOPT_PREFILL_STAGE_SPIN=-1)
+    agree, and sequence 0 matches fp32 attention over the dequantized pool
+    on every row of two heads."""
+    B, S, H, D, W, sinks = 3, 4096, 8, 128, 1024, 4
+    torch.manual_seed(13)
+    nbps = S // 16
+    nb = B * nbps + 8
+    memopt_C.init_pool(nb, 16, H, D, kv_format="int4")
+    order = torch.randperm(nb)[:B * nbps].to(torch.int32).reshape(B, nbps)
+    bt = order.to(dev())
+    for b in range(B):
+        slots = (bt[b].long()[:, None] * 16 + torch.arange(16, device=dev())).reshape(-1).to(torch.int32)
+        k = torch.randn(S, H, D, device=dev(), dtype=torch.float16)
+        v = torch.randn(S, H, D, device=dev(), dtype=torch.float16)
+        memopt_C.write_cache(k, v, bt, slots)
+    bt[1, 5] = -1
+    bt[2, 100] = -1
+    q = torch.randn(B, S, H, D, device=dev(), dtype=torch.float16)
+    ctx = torch.full((B,), S, dtype=torch.int32, device=dev())
+    args = (q, memopt_C.get_key_pool(), memopt_C.get_value_pool(), bt, ctx, S, W)
+    kw = dict(num_sink_tokens=sinks, causal=True)
+    ink = _prefill_with_env({}, *args, **kw)
+    launch = _prefill_with_env({"MEMOPT_PREFILL_STAGE_LAUNCH": "1"}, *args, **kw)
+    self_staged = _prefill_with_env({"MEMOPT_PREFILL_STAGE_SPIN": "-1"}, *args, **kw)
+    assert torch.isfinite(ink).all()
+    assert_close(ink, launch.float().cpu().numpy(), what="in-kernel vs staging launch")
+    assert_close(self_staged, launch.float().cpu().numpy(), what="self-staged vs staging launch")
+    pages = memopt_C.get_int4_pages()
+    kd, vd = O.dequant_pages_torch(pages[order[0].to(dev()).long()], D)
+    kd, vd = kd.reshape(S, H, D), vd.reshape(S, H, D)
+    for h in (0, 5):
+        ref = _fp32_head_reference(q[0, :, h], kd[:, h], vd[:, h], 0, S, S, W, sinks)
+        assert_close(ink[0, :, h], ref, what=f"sequence 0 head {h}")

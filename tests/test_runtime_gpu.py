@@ -261,8 +261,8 @@ def test_chunk_call_workspace_is_bounded_by_the_window():
     win = memopt_C.PreparedAttention(q, kp, vp, bt, ctx, S, W, num_sink_tokens=sinks, causal=True)
     full = memopt_C.PreparedAttention(q, kp, vp, bt, ctx, S, -1, num_sink_tokens=sinks, causal=True)
     slots = 4 * ((Lq + W - 1 + 63) // 64 + 1) + 4  # window tiles + alignment + one sink tile
-    assert win.workspace_bytes == slots * H * 64 * D + slots * 4
-    assert full.workspace_bytes == (S // 16) * H * 64 * D + (S // 16) * 4
+    assert win.workspace_bytes == (slots * H * 64 * D + slots * 4 + 7) // 8 * 8 + H * 256
+    assert full.workspace_bytes == ((S // 16) * H * 64 * D + (S // 16) * 4 + 7) // 8 * 8 + H * 256
     chunk_bytes = R.chunk_call_bytes(Lq, S, H, D, W)
     assert win.workspace_bytes <= chunk_bytes
     # and the call is right: same rows as the whole-window reference on the dequantized pool
