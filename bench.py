@@ -334,7 +334,8 @@ def bench_prefill(torch, memopt_C, cfg, steps=10, warmup=25):
     tflops = flops / (launch_ms * 1e-3) / 1e12
     return {"workload": "BASELINE configs[3]: B 1, seq 16384, 32 heads, head_dim 128, INT4 16-token pages, "
                         "causal window 4096 + 4 sinks, all 16384 queries",
-            "kernel": "prefill_stage_kernel<128, true> + prefill_pipe_kernel<128>", "kernel_ms": round(launch_ms, 4),
+            "kernel": "prefill_stage_kernel<128, true> (first head per XCD) + prefill_pipe_kernel<128, 4, true, true> "
+                      "(stages the other heads)", "kernel_ms": round(launch_ms, 4),
             "flops": flops, "TFLOP/s": round(tflops, 1), "peak_TFLOP/s": MFMA_F16_PEAK_TFLOPS,
             "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
             "write_cache_ms": round(write_ms, 4)}
@@ -405,6 +406,7 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
         memopt_C.evict_tokens(scores, bt, ibf, cfg["retain"], cfg["sinks"])
         if c == copies - 1:
             evict_ms.append(time_evict(torch, memopt_C, scores, bt, nb, cfg))
+            evict_ms.append(time_evict_cold(torch, memopt_C, scores, bt, nb, cfg))
         unlinked += int((bt == -1).sum())
         nbytes += int(((bt.cpu() >= 0) & vis[None]).sum()) * per_page
         calls.append(memopt_C.PreparedAttention(q, kc, vc, bt, cl, ctx, window, num_sink_tokens=cfg["sinks"]))
@@ -414,7 +416,8 @@ def bench_sparse_decode(torch, memopt_C, cfg, window, fifo_trace, copies=1, step
     gbs = nbytes / (ms * 1e-3) / 1e9
     out = {"kernel": INT4_DECODE_KERNEL, "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
            "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-           "evict_tokens_ms": round(evict_ms[0], 4), "pages_unlinked": unlinked,
+           "evict_tokens_ms": round(evict_ms[0], 4), "evict_tokens_cold_ms": round(evict_ms[1], 4),
+           "pages_unlinked": unlinked,
            "page_sets_rotated": copies,
            "block_tables": "seeded FIFO alloc/free trace" if fifo_trace else "seeded random permutation"}
     if control_copies:
@@ -447,6 +450,27 @@ def time_evict(torch, memopt_C, scores, bt, nb, cfg, reps=7):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def time_evict_cold(torch, memopt_C, scores, bt, nb, cfg, reps=7):
+    """evict_tokens as time_evict() does it, but each call timed alone right
+    after a 1 GiB device copy, so that no scale run, score or bitmask word of
+    the previous call is still in the last-level cache (back-to-back calls
+    find the scale runs the previous call rewrote there). Each call between
+    its own HIP events, which adds about 1.5 us of event overhead per call."""
+    btcs = [bt.clone() for _ in range(reps)]
+    ibfs = [torch.zeros(nb, dtype=torch.int32, device=bt.device) for _ in range(reps)]
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=bt.device)
+    dst = torch.empty_like(src)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i in range(reps):
+        dst.copy_(src)
+        ev[i][0].record()
+        memopt_C.evict_tokens(scores, btcs[i], ibfs[i], cfg["retain"], cfg["sinks"])
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    del src, dst
+    return sum(a.elapsed_time(b) for a, b in ev) / reps
 
 
 def bench_long_context_policy(torch, memopt_C, cfg, steps=20, warmup=3):
@@ -510,9 +534,11 @@ def bench_long_context_policy(torch, memopt_C, cfg, steps=20, warmup=3):
     nbytes = linked * per_page
     gbs = nbytes / (ms * 1e-3) / 1e9
     evict_ms = time_evict(torch, memopt_C, scores, bt, nb, cfg)
+    evict_cold_ms = time_evict_cold(torch, memopt_C, scores, bt, nb, cfg)
     return {"kernel": INT4_DECODE_KERNEL, "decode_ms": round(ms, 5), "bytes_streamed": nbytes,
             "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "evict_tokens_ms": round(evict_ms, 4), "pages_unlinked": B * nbps - linked,
+            "evict_tokens_ms": round(evict_ms, 4), "evict_tokens_cold_ms": round(evict_cold_ms, 4),
+            "pages_unlinked": B * nbps - linked,
             "policy": {"use_int4": pf.last_policy.use_int4, "retain_ratio": pf.last_policy.retain_ratio},
             "policy_step_ms": round(step_ms, 2),
             "policy_step": "fp16 -> INT4 pool conversion, 1-token append, decode, evict_tokens, free sweep",
