@@ -608,14 +608,16 @@ struct StageLayout {
 };
 
 // Stages the workspace blocks of slots slot0 + i * sstride, i < n <= N, of
-// (sequence, head) bh with one wave: the blocks' page lookups (scalar
-// loads), then every block's page loads, are issued before anything waits
-// for them, so the N blocks cost one chain of memory round trips. Block
-// = bh * MC + slot; lane l = 8p + c owns tokens (p, p + 8) x dims
-// [c*D/8, (c+1)*D/8), as in the INT4 page format. vl: the wave's 32 * D
-// bytes of LDS (the V^T transpose). all_flags: write each slot's link flag
-// from every head (else head 0's wave writes it).
-template <int D, bool INT4, int N>
+// (sequence, head) bh with one wave: the blocks' page lookups, then every
+// block's page loads, are issued before anything waits for them, so the N
+// blocks cost one chain of memory round trips. Block = bh * MC + slot;
+// lane l = 8p + c owns tokens (p, p + 8) x dims [c*D/8, (c+1)*D/8), as in
+// the INT4 page format. vl: the wave's 32 * D + (D / 16) * PADG bytes of
+// LDS (the V^T transpose; each 16-row group PADG bytes further on, so the
+// 8 lanes writing one row offset of 8 groups hit different banks).
+// all_flags: write each slot's link flag from every head (else head 0's
+// wave writes it).
+template <int D, bool INT4, int N, int PADG = 0>
 __device__ __forceinline__ void stage_blocks(const PrefillParams &p, uint8_t *__restrict__ ws, int32_t MC,
                                              int32_t units, int32_t bh, int32_t slot0, int32_t sstride, int32_t n,
                                              uint8_t *vl, bool all_flags) {
@@ -747,14 +749,15 @@ __device__ __forceinline__ void stage_blocks(const PrefillParams &p, uint8_t *__
     // 4-byte stores cost twice the K stores for the same bytes.
     const int vc = chunk_vcol(pp);
 #pragma unroll
-    for (int d = 0; d < DPL; ++d) *reinterpret_cast<uint32_t *>(vl + (c * DPL + d) * 32 + vc * 2) = vw[d];
+    for (int d = 0; d < DPL; ++d)
+      *reinterpret_cast<uint32_t *>(vl + (c * DPL + d) * 32 + ((c * DPL + d) >> 4) * PADG + vc * 2) = vw[d];
     // One wave's LDS accesses complete in order; the clobber keeps the
     // compiler from moving the reads above the writes.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int k = 0; k < 32 * D / 1024; ++k)
       *reinterpret_cast<u32x4 *>(blk + L::kVPart + k * 1024 + lane * 16) =
-          *reinterpret_cast<const u32x4 *>(vl + k * 1024 + lane * 16);
+          *reinterpret_cast<const u32x4 *>(vl + k * 1024 + lane * 16 + ((k * 1024 + lane * 16) >> 9) * PADG);
     if ((all_flags || h == 0) && lane == 0)
       reinterpret_cast<int32_t *>(ws + (int64_t)units * L::kBlock)[(int64_t)b * MC + slot[i]] = pg[i] >= 0 ? 1 : 0;
     // The LDS reads above are complete before the next block (or the
@@ -763,19 +766,20 @@ __device__ __forceinline__ void stage_blocks(const PrefillParams &p, uint8_t *__
   }
 }
 
-// One wave per workspace block: block q * MC + slot, q < nblocks / MC, of
-// (sequence, head) q * ustride (ustride 1: every block of the workspace,
+// Four consecutive workspace blocks per wave: block q * MC + slot, q <
+// nblocks / MC, of (sequence, head) q * ustride (ustride 1: every block of
+// the workspace,
 // head 0's writing the link flags; otherwise every head writes them, as
 // the staged units need not include head 0 of each sequence).
 template <int D, bool INT4>
 __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams p, uint8_t *__restrict__ ws,
                                                             int32_t MC, int32_t units, int32_t ustride,
                                                             int32_t nblocks) {
-  const int32_t idx = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int32_t idx = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;  // 4 consecutive slots per wave (MC % 4 == 0)
   if (idx >= nblocks) return;  // wave-uniform
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[4][32 * D];
-  stage_blocks<D, INT4, 1>(p, ws, MC, units, (idx / MC) * ustride, idx % MC, 1, 1, vt_lds[threadIdx.x >> 6],
-                           ustride != 1);
+  stage_blocks<D, INT4, 4>(p, ws, MC, units, (idx / MC) * ustride, idx % MC, 1, min(4, nblocks - idx),
+                           vt_lds[threadIdx.x >> 6], ustride != 1);
 }
 
 template <int N>
@@ -925,7 +929,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     // every MI355X partition has 8, 4, 2 or 1 XCDs, so workgroups with equal
     // i % 8 share an XCD.
     const int32_t P = (int32_t)(gridDim.x >> 3), i = wg % P, k = i / nqt, j = i % nqt, U = wg / nqt;
-    uint8_t *vl = lds_k0 + wave * 32 * D;  // free until the first tile copy
+    // (LDS scratch of the V^T transposes, free until the first tile copy)
+    uint8_t *vl = (wave < 2 ? lds_k0 : lds_k1) + (wave & 1) * (32 * D + (D / 16) * 16);
     // Share j of S of unit u, slots [s0, s1): wave w takes s0 + w, s0 + w +
     // NW, ..., eight blocks per stage_blocks call (INT4; one for fp16
     // pools). Then the
@@ -935,7 +940,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       const int32_t s0 = (int32_t)((int64_t)j * MC / S), s1 = (int32_t)((int64_t)(j + 1) * MC / S);
       constexpr int NB = INT4 ? 8 : 1;
       for (int32_t sl = s0 + wave; sl < s1; sl += NB * NW)
-        stage_blocks<D, INT4, NB>(p, ws, MC, units, u, sl, NW, min(NB, (s1 - sl + NW - 1) / NW), vl, true);
+        stage_blocks<D, INT4, NB, 16>(p, ws, MC, units, u, sl, NW, min(NB, (s1 - sl + NW - 1) / NW), vl, true);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores are complete
       __syncthreads();
       if (threadIdx.x == 0)
@@ -1541,7 +1546,7 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
     const int64_t n_wg = (int64_t)((d.q_len + 32 * NW - 1) / (32 * NW)) * d.num_heads * d.batch;
     MEMOPT_REQUIRE(n_wg < (1LL << 31), MEMOPT_ERR_UNSUPPORTED, "paged_attention: too many query tiles");
     uint8_t *ws = (uint8_t *)d.workspace;
-    const dim3 sgrid((unsigned)((units + 3) / 4)), grid((unsigned)n_wg);
+    const dim3 sgrid((unsigned)((units + 15) / 16)), grid((unsigned)n_wg);
     const bool int4 = d.kv_format == MEMOPT_KV_INT4;
     // In-kernel staging when every XCD owns whole (sequence, head) units of
     // at least 32 query tiles: a staging launch stages each XCD's first
@@ -1564,7 +1569,7 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
       const char *spin = std::getenv("MEMOPT_PREFILL_STAGE_SPIN");
       ss.spin = spin ? std::atoi(spin) : 200000;
       const int32_t upx = (int32_t)(per_xcd / nqt), first = 8 * mc;
-      const dim3 fgrid((unsigned)((first + 3) / 4));
+      const dim3 fgrid((unsigned)((first + 15) / 16));
       if (d.head_dim == 128) {
         if (int4) {
           hipLaunchKernelGGL((prefill_stage_kernel<128, true>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
