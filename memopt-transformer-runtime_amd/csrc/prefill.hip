@@ -1550,12 +1550,13 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
     const bool int4 = d.kv_format == MEMOPT_KV_INT4;
     // In-kernel staging when every XCD owns whole (sequence, head) units of
     // at least 32 query tiles: a staging launch stages each XCD's first
-    // unit, and the first S = min(nqt / 4, 32) workgroups of every unit the
-    // next one (fewer, larger shares cost less waiting in all).
+    // unit, and the first S = min(nqt / 8, 16) workgroups of every unit the
+    // next one (config 4: 8 to 16 stagers measured 0.5 % faster than 32,
+    // 64 slower: fewer, larger shares cost less waiting in all).
     const int64_t nqt = (d.q_len + 32 * NW - 1) / (32 * NW);
     const int64_t per_xcd = n_wg / 8;
     StageSched ss{};
-    ss.S = (int32_t)std::min<int64_t>(nqt / 4, 32);
+    ss.S = (int32_t)std::min<int64_t>(nqt / 8, 16);
     // (MEMOPT_PREFILL_STAGE_LAUNCH selects the staging launch for every
     // call, so that tests can compare the two paths.)
     const bool in_kernel = n_wg % 8 == 0 && nqt >= 32 && per_xcd % nqt == 0 &&
