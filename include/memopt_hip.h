@@ -216,8 +216,10 @@ int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_
  *     j <= pos && (j < sinks || j >= pos-W+1), scripts/bench_accuracy.py:253-280).
  * With num_sink_tokens == 0, causal == 0 and an fp16 cache it computes the
  * same function as memopt_dynamic_sparse_attention.
- * `workspace` (device, >= memopt_attention_workspace_size bytes) holds
- * split-K partials; it may be NULL when that size is 0. */
+ * `workspace` (device, >= memopt_attention_workspace_size bytes) holds the
+ * decode's split-K partials and arrival counters, or the prefill's staged
+ * K/V and staging flags (any content: counters and flags carry a per-call
+ * id); it may be NULL when that size is 0. */
 typedef struct memopt_attn_desc {
   const void *query;          /* fp16 [batch, q_len, H, D] contiguous        */
   void *out;                  /* fp16 [batch, q_len, H, D] contiguous        */
