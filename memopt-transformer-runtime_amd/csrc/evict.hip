@@ -1408,13 +1408,32 @@ __global__ __launch_bounds__(256) void evict_cache_kernel(const float *__restric
   if (nv) atomicAdd(&s_valid, nv);
   __syncthreads();
   const bool enough = s_valid >= keep;
+  // Pages of more than 256 tokens: tau = the key of the keep-th largest
+  // score above -1e38 (a radix select over the block's scores in LDS), and a
+  // score above -1e38 is evicted when its key is below tau, the same set as
+  // the count below, in O(bs) instead of O(bs^2) per (block, head).
+  __shared__ SelectShared<256> sh;
+  uint32_t tau = 0;
+  if (bs > 256 && enough)  // workgroup-uniform
+    tau = radix_select<256, false>(
+        [&](auto f) {
+          for (int32_t i = threadIdx.x; i < bs; i += 256)
+            if (ssc[i] > -1e38f) f(order_key(ssc[i]));
+        },
+        (uint32_t)keep, sh);
   for (int32_t i = threadIdx.x; i < bs; i += 256) {
     const float si = ssc[i];
     bool evict;
     if (enough) {
-      int32_t greater = 0;
-      for (int32_t j = 0; j < bs; ++j) greater += (ssc[j] > -1e38f && ssc[j] > si) ? 1 : 0;
-      evict = greater >= keep;
+      if (bs > 256) {
+        // a NaN score has no key order: no score exceeds it (not evicted);
+        // one at or below -1e38 is exceeded by every score above -1e38
+        evict = !(si != si) && (si > -1e38f ? order_key(si) < tau : true);
+      } else {
+        int32_t greater = 0;
+        for (int32_t j = 0; j < bs; ++j) greater += (ssc[j] > -1e38f && ssc[j] > si) ? 1 : 0;
+        evict = greater >= keep;
+      }
     } else {
       evict = si < -1e38f;
     }

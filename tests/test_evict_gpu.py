@@ -313,10 +313,13 @@ def test_evict_then_free_sweep():
     assert memopt_C.free_evicted_blocks(ibf) == [1] and memopt_C.free_blocks_count() == 5
 
 
-@pytest.mark.parametrize("fmt,bs", [("fp16", 16), ("int4", 16), ("fp16", 128), ("fp16", 256), ("fp16", 8)])
+@pytest.mark.parametrize("fmt,bs", [("fp16", 16), ("int4", 16), ("fp16", 128), ("fp16", 256), ("fp16", 8),
+                                    ("fp16", 512), ("fp16", 2048), ("fp16", 8192)])
 def test_evict_cache_vs_oracle(fmt, bs):
     """evict_cache for pages of any size (the reference strides over
-    block_size, src/csrc/kv_cache.cu:409, :454)."""
+    block_size, src/csrc/kv_cache.cu:409, :454); pages over 256 tokens take
+    the radix-select path, with the same ties and sentinel cases, and a NaN
+    score (never exceeded, so never evicted) in one of them."""
     rng = np.random.default_rng(5 + bs)
     nb, H, D = 6, 4, 64
     memopt_C.init_pool(nb, bs, H, D, kv_format=fmt)
@@ -327,6 +330,9 @@ def test_evict_cache_vs_oracle(fmt, bs):
     scores = rng.standard_normal((nb, bs, H)).astype(np.float32)
     scores[0, : bs // 2, 0] = 0.25                     # ties
     scores[1, :, 1] = -np.inf                          # nothing above the reference's -1e38 sentinel
+    scores[2, 3, 2] = np.nan
+    scores[2, 5, 2] = np.float32(-1e38)                # at the sentinel: exceeded by every valid score
+    scores[3, :, 3] = np.where(np.arange(bs) % 2 == 0, 0.0, -0.0)  # -0 and +0 tie: none evicted
     memopt_C.evict_cache(to_dev(np.zeros((1, 1), np.int32)), to_dev(scores), 0.4)
     if fmt == "fp16":
         kp = k.reshape(nb, bs, H, D).copy()
