@@ -393,12 +393,24 @@ def evict_cache(block_tables: torch.Tensor, attention_scores: torch.Tensor, reta
         _check(_c_evict_cache(scores.data_ptr(), nb, float(retain_ratio), int(num_sink_tokens), _stream(scores)))
 
 
+def evict_workspace_bytes(num_seqs: int, num_heads: int, seq_len: int, max_blocks_per_seq: int,
+                          total_pool_blocks: int) -> int:
+    """Device workspace bytes an ``evict_tokens`` call of this shape needs
+    (``memopt_evict_workspace_size``)."""
+    need = _i64(0)
+    _check(_c_evict_ws(num_seqs, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, ctypes.byref(need)))
+    return need.value
+
+
 def evict_tokens(attention_scores: torch.Tensor, block_tables: torch.Tensor, is_block_free: torch.Tensor,
-                 retain_ratio: float, num_sink_tokens: int = 4) -> None:
+                 retain_ratio: float, num_sink_tokens: int = 4, workspace: Optional[torch.Tensor] = None) -> None:
     """Sequence-centric Ada-KV eviction; mutates the pool, ``block_tables`` and ``is_block_free``.
 
     ``block_tables`` and ``is_block_free`` must be contiguous int32 CUDA
     tensors (the reference silently drops mutations of non-contiguous ones).
+    ``workspace``: a contiguous uint8 tensor on the scores' device of at
+    least ``evict_workspace_bytes`` bytes, any content (default: one from
+    torch's caching allocator per call).
     """
     p = _pool_or_raise("evict_tokens")
     _require(0.0 < retain_ratio <= 1.0, "evict_tokens: retain_ratio must be in (0, 1]")
@@ -423,15 +435,21 @@ def evict_tokens(attention_scores: torch.Tensor, block_tables: torch.Tensor, is_
         return
     scores = attention_scores.contiguous()
     M, nb = block_tables.shape[1], is_block_free.shape[0]
-    need = _i64(0)
-    _check(_c_evict_ws(N, H, L, M, nb, ctypes.byref(need)))
+    need = evict_workspace_bytes(N, H, L, M, nb)
     with torch.cuda.device(scores.device):
-        # scratch from torch's caching allocator on the current stream (page
-        # marks and long-row selection state; nothing is kept between calls)
-        ws = torch.empty(need.value, dtype=torch.uint8, device=scores.device)
+        if workspace is None:
+            # scratch from torch's caching allocator on the current stream (page
+            # marks and long-row selection state; nothing is kept between calls)
+            ws = torch.empty(need, dtype=torch.uint8, device=scores.device)
+        else:
+            _require(workspace.dtype == torch.uint8 and workspace.is_contiguous() and
+                     workspace.device == scores.device and workspace.numel() >= need,
+                     f"evict_tokens: workspace must be a contiguous uint8 tensor of >= {need} bytes on the "
+                     "scores' device")
+            ws = workspace
         _check(_c_evict_tokens(scores.data_ptr(), N, H, L, block_tables.data_ptr(), M,
                                is_block_free.data_ptr(), nb, float(retain_ratio),
-                               int(num_sink_tokens), ws.data_ptr(), need.value, _stream(scores)))
+                               int(num_sink_tokens), ws.data_ptr(), ws.numel(), _stream(scores)))
 
 
 def free_evicted_blocks(is_block_free: torch.Tensor) -> List[int]:

@@ -347,6 +347,38 @@ def test_evict_cache_vs_oracle(fmt, bs):
         assert np.array_equal(np.all(kd == 0, axis=-1), zero) and np.array_equal(np.all(vd == 0, axis=-1), zero)
 
 
+def test_evict_tokens_caller_workspace():
+    """evict_tokens with a workspace the caller keeps, starting filled with
+    0x5A bytes, over back-to-back calls (short and long rows): a call
+    depends on nothing the workspace holds (page marks, span slots, lists,
+    bitmasks and the alias flag are all overwritten or tag-checked)."""
+    rng = np.random.default_rng(61)
+    N, H, bs, D = 2, 4, 16, 64
+    for L in (3000, 70000):
+        M = (L + bs - 1) // bs
+        nb = N * M + 2
+        memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+        T = nb * bs
+        k = rng.standard_normal((T, H, D)).astype(np.float16)
+        memopt_C.write_cache(to_dev(k), to_dev(k), to_dev(np.zeros((1, 1), np.int32)),
+                             to_dev(np.arange(T, dtype=np.int32)))
+        bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
+        bt[1, ::5] = bt[0, ::5]  # shared pages: the alias path
+        ws = torch.full((memopt_C.evict_workspace_bytes(N, H, L, M, nb),), 0x5A, dtype=torch.uint8, device=dev())
+        state = _pool_state("int4")
+        bt_d, ibf = to_dev(bt), np.zeros(nb, np.int32)
+        ibf_d = to_dev(ibf)
+        for _ in range(3):
+            s = rng.lognormal(size=(N, H, L)).astype(np.float32)
+            memopt_C.evict_tokens(to_dev(s), bt_d, ibf_d, 0.9, 4, workspace=ws)
+            O.evict_tokens_intended(s, bt, ibf, 0.9, 4, state, bs)
+            same_bits(_pool_state("int4")["pages"], state["pages"])
+            same_bits(bt_d, bt)
+            same_bits(ibf_d, ibf)
+    with pytest.raises(RuntimeError, match="workspace"):
+        memopt_C.evict_tokens(to_dev(s), bt_d, ibf_d, 0.9, 4, workspace=ws[:16])
+
+
 def test_evict_errors():
     memopt_C.init_pool(4, 16, 2, 64)
     s = torch.ones(1, 2, 64, device=dev())
