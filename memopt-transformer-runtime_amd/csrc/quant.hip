@@ -19,6 +19,11 @@ static constexpr int kThreads = 256;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
+// Workgroups for work_items (one per thread) up to `cap`. The surface
+// quantize, dequantize and fp16 scatter launch one item (or, dequantize, four)
+// per thread with no practical cap: a grid-stride loop capped at 16384
+// workgroups kept one 16-byte load per thread in flight at a time (config 2's
+// pool tensor: quantize 0.67 -> 0.72 of HBM, dequantize 0.77 -> 0.85).
 static inline unsigned grid_for(int64_t work_items, int64_t cap = 16384) {
   int64_t g = (work_items + kThreads - 1) / kThreads;
   if (g < 1) g = 1;
@@ -45,7 +50,13 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(const half_t *__rest
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
     float v[8];
-    load8<VEC>(in + i * 8, v);
+    if (VEC) {  // read once: non-temporal (1 % faster)
+      typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+      const u4v x = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(in + i * 8));
+      unpack_half8(make_uint4(x.x, x.y, x.z, x.w), v);
+    } else {
+      load8<VEC>(in + i * 8, v);
+    }
     float s;
     const uint32_t w = quantize8(v, s);
     if (VEC) {
@@ -113,6 +124,24 @@ __global__ __launch_bounds__(kThreads) void write_fp16_kernel(
     uint4 *__restrict__ vpool, const int32_t *__restrict__ slots, int64_t n_chunks, int64_t cpr,
     int64_t n_slots) {
   const int64_t stride = (int64_t)gridDim.x * kThreads;
+  // 32-bit token index when it fits (a 64-bit division expands to a long
+  // sequence); the pool rows are written with non-temporal stores (nothing
+  // reads them back soon): 0.48 -> 0.59 of HBM on 16384 tokens x 32 x 128
+  // (non-temporal loads as well: 0.49).
+  if (n_chunks < (1LL << 31) && cpr < (1LL << 31)) {
+    const uint32_t cp = (uint32_t)cpr;
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
+      const uint32_t t = (uint32_t)i / cp, c = (uint32_t)i - t * cp;
+      const int64_t slot = slots[t];
+      if (slot < 0 || slot >= n_slots) continue;
+      const u4v kx = *reinterpret_cast<const u4v *>(keys + i);
+      const u4v vx = *reinterpret_cast<const u4v *>(values + i);
+      __builtin_nontemporal_store(kx, reinterpret_cast<u4v *>(kpool + slot * cpr + c));
+      __builtin_nontemporal_store(vx, reinterpret_cast<u4v *>(vpool + slot * cpr + c));
+    }
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_chunks; i += stride) {
     const int64_t t = i / cpr, c = i - t * cpr;
     const int64_t slot = slots[t];
@@ -368,7 +397,7 @@ int memopt_quantize_kv_cache_int4(const void *cache, int64_t numel, int64_t last
   hipStream_t s = (hipStream_t)stream;
   const bool vec = aligned(cache, 16) && aligned(packed_out, 4);
   if (vec)
-    hipLaunchKernelGGL(quantize_kernel<true>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL(quantize_kernel<true>, dim3(grid_for(n_chunks, 1LL << 30)), dim3(kThreads), 0, s,
                        (const half_t *)cache, packed_out, scales_out, n_chunks);
   else
     hipLaunchKernelGGL(quantize_kernel<false>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s,
@@ -390,8 +419,8 @@ int memopt_dequantize_kv_cache_int4(const uint8_t *packed, int64_t packed_numel,
   hipStream_t s = (hipStream_t)stream;
   const bool vec = aligned(packed, 4) && aligned(out, 16);
   if (vec)
-    hipLaunchKernelGGL(dequantize_kernel<true>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s, packed,
-                       scales, (half_t *)out, n_chunks);
+    hipLaunchKernelGGL(dequantize_kernel<true>, dim3(grid_for((n_chunks + 3) / 4, 1LL << 30)), dim3(kThreads), 0,
+                       s, packed, scales, (half_t *)out, n_chunks);
   else
     hipLaunchKernelGGL(dequantize_kernel<false>, dim3(grid_for(n_chunks)), dim3(kThreads), 0, s, packed,
                        scales, (half_t *)out, n_chunks);
@@ -414,9 +443,9 @@ int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
                      aligned(p.value, 16);
     if (vec) {
       const int64_t cpr = row / 8, n = num_tokens * cpr;
-      hipLaunchKernelGGL(write_fp16_kernel, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint4 *)keys,
-                         (const uint4 *)values, (uint4 *)p.key, (uint4 *)p.value, slot_mapping, n, cpr,
-                         n_slots);
+      hipLaunchKernelGGL(write_fp16_kernel, dim3(grid_for(n, 1LL << 30)), dim3(kThreads), 0, s,
+                         (const uint4 *)keys, (const uint4 *)values, (uint4 *)p.key, (uint4 *)p.value, slot_mapping,
+                         n, cpr, n_slots);
     } else {
       const int64_t n = num_tokens * row;
       hipLaunchKernelGGL(write_fp16_scalar_kernel, dim3(grid_for(n)), dim3(kThreads), 0, s,
