@@ -1581,10 +1581,11 @@ int memopt_evict_tokens(const float *attention_scores, int32_t num_seqs, int32_t
   }
   const size_t lds = (size_t)words * sizeof(uint32_t);
   const dim3 grid(num_seqs, num_heads);
-  // Rows up to 8192 (32768) tokens keep their keys in registers with 256
-  // (1024) threads.
-  if (seq_len <= 256 * 32)
-    hipLaunchKernelGGL((evict_tokens_kernel<256, 32>), grid, dim3(256), lds, st, attention_scores, block_tables,
+  // Rows up to 8192 (32768) tokens keep their keys in registers with 512
+  // (1024) threads (config 3, 8192 tokens: 512 threads x 16 keys 28.8-29.0
+  // us per call, 256 x 32 32.7, 1024 x 8 36.4).
+  if (seq_len <= 512 * 16)
+    hipLaunchKernelGGL((evict_tokens_kernel<512, 16>), grid, dim3(512), lds, st, attention_scores, block_tables,
                        is_block_free, num_heads, seq_len, max_blocks_per_seq, total_pool_blocks, keep, sinks, z);
   else
     hipLaunchKernelGGL((evict_tokens_kernel<1024, 32>), grid, dim3(1024), lds, st, attention_scores, block_tables,
