@@ -325,8 +325,17 @@ def test_config5_through_policy_forward():
 
     q = torch.randn(B, 1, H, D, device=dev(), generator=g).half()
     k1, v1 = kv(1)
+    # 256 full pages sampled before the conversion (2.4e9 elements per pool,
+    # converted in one page-writer launch): their INT4 pages must equal the
+    # oracle's quantization of their fp16 rows, byte for byte
+    pick = cache.block_tables(seqs)[:, :8000:125].reshape(-1).long()
+    kf, vf = memopt_C.get_pool_tensors()
+    k_s, v_s = kf[pick].cpu().numpy(), vf[pick].cpu().numpy()
+    del kf, vf
     out1 = pf.step(seqs, q, k1, v1)                      # no scores: convert, append, decode
     assert pf.conversions == 1 and cache.kv_format == "int4" and pf.last_policy == R.Policy(0.75, True)
+    assert np.array_equal(memopt_C.get_int4_pages()[pick].cpu().numpy(), O.to_int4_pages(k_s, v_s))
+    del k_s, v_s
     check_decode(out1, 0)
     k2, v2 = kv(1)
     scores = torch.exp(torch.randn(B, H, L, device=dev(), generator=g))
