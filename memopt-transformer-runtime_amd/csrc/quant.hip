@@ -455,10 +455,11 @@ int memopt_write_cache(const void *keys, const void *values, int64_t num_tokens,
   } else {
     const int64_t n = num_tokens * row / 8;
     const bool vec = aligned(keys, 16) && aligned(values, 16);
-    // (64-bit element offsets; 32-bit wave ids: a whole fp16 pool of config 5,
-    // 2.4e9 elements per K, converts through this kernel too)
+    // (64-bit element offsets, 32-bit token indices and wave ids: a whole
+    // fp16 pool of config 5, 2.4e9 elements per K, converts through this
+    // kernel too)
     const int64_t waves = (num_tokens + 15) / 16 * num_heads * 2;
-    if (vec && waves < (1LL << 32) && (head_dim == 64 || head_dim == 128)) {
+    if (vec && waves < (1LL << 32) && num_tokens < (1LL << 31) && (head_dim == 64 || head_dim == 128)) {
       const unsigned grid = (unsigned)((waves + kThreads / 64 - 1) / (kThreads / 64));
       if (head_dim == 128)
         hipLaunchKernelGGL(write_int4_pages_kernel<128>, dim3(grid), dim3(kThreads), 0, s, (const half_t *)keys,
