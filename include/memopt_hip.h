@@ -218,8 +218,11 @@ int memopt_dynamic_sparse_attention(const void *query, int32_t batch, int32_t q_
  * same function as memopt_dynamic_sparse_attention.
  * `workspace` (device, >= memopt_attention_workspace_size bytes) holds the
  * decode's split-K partials and arrival counters, or the prefill's staged
- * K/V and staging flags (any content: counters and flags carry a per-call
- * id); it may be NULL when that size is 0. */
+ * K/V and staging flags; it may be NULL when that size is 0. A decode
+ * (q_len == 1) workspace must be zero before its first use; later calls may
+ * reuse it without clearing (each call's counters carry the call's id, so
+ * what an earlier call left is never taken for its own). A multi-query
+ * workspace may hold anything (the call clears its flags itself). */
 typedef struct memopt_attn_desc {
   const void *query;          /* fp16 [batch, q_len, H, D] contiguous        */
   void *out;                  /* fp16 [batch, q_len, H, D] contiguous        */
@@ -260,11 +263,13 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream);
  * the same descriptor (desc->workspace is ignored) and allocates nothing: the
  * decode kernels' split-K partials, and the staged K/V of a multi-query call
  * when they fit, live in a static device array of
- * MEMOPT_NOALLOC_SCRATCH_BYTES (4 MiB) per GPU, held until the process ends.
+ * MEMOPT_NOALLOC_SCRATCH_BYTES (4 MiB) per GPU, held until the process ends;
+ * its last 64 KiB hold the decode's arrival counters (zero at load, then
+ * only ever counters) and the rest the partials or staged K/V.
  * Multi-query calls whose staging does not fit run the in-kernel staging
- * kernel, which needs no scratch. A decode whose partials exceed the array
- * (B * H * splits * (head_dim + 2) * 4 bytes; splits grow only while B * H
- * is below two workgroups per CU) returns MEMOPT_ERR_INVALID. Every call on
+ * kernel, which needs no scratch. A decode whose partials exceed the rest
+ * (B * H * splits * (head_dim + 2) * 4 + 8 * B * H bytes; splits grow only
+ * while B * H is below two workgroups per CU) returns MEMOPT_ERR_INVALID. Every call on
  * a GPU shares that GPU's array, so calls that overlap on one GPU (other
  * streams or host threads) race: the caller serializes them. The first call
  * on each device resolves the array's device address there. */

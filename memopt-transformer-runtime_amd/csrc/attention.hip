@@ -221,7 +221,13 @@ static int decode_plan(const memopt_attn_desc &d, bool unsplit_ok, int32_t *spli
 // shares it. Host code never passes `scratch` itself to a kernel (on the host
 // it names a stand-in, not device memory): it resolves the device address
 // once per device with hipGetSymbolAddress and passes that.
+// Its last kNoallocCounterBytes hold the split-K arrival counters and
+// nothing else: zero when the program loads, afterwards only ever holding a
+// decode call's (tag, count), so a later call's tag never meets a stale
+// match (staged K/V and partials stay below them).
 static __device__ __align__(256) uint8_t scratch[MEMOPT_NOALLOC_SCRATCH_BYTES];
+static constexpr int64_t kNoallocCounterBytes = 64 << 10;
+static constexpr int64_t kNoallocDataBytes = MEMOPT_NOALLOC_SCRATCH_BYTES - kNoallocCounterBytes;
 
 static constexpr int kMaxDevices = 64;
 
@@ -274,7 +280,10 @@ int memopt_attention_workspace_size(const memopt_attn_desc *desc, int64_t *bytes
 
 namespace memopt {
 
-static int paged_attention(const memopt_attn_desc &d, bool unsplit_ok, void *stream) {
+// `cnt`: the split-K arrival counters (one per (b, h)); nullptr places
+// them after the partials in d.workspace.
+static int paged_attention(const memopt_attn_desc &d, bool unsplit_ok, void *stream,
+                           unsigned long long *cnt = nullptr) {
   int rc = validate(d);
   if (rc != MEMOPT_OK) return rc;
   if (d.batch == 0 || d.q_len == 0 || d.num_heads == 0 || d.head_dim == 0) return MEMOPT_OK;
@@ -331,7 +340,9 @@ static int paged_attention(const memopt_attn_desc &d, bool unsplit_ok, void *str
     p.qk_scale_log2 = scale * 1.4426950408889634f;
     p.ws_o = (float *)d.workspace;
     p.ws_ml = splits > 1 ? p.ws_o + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
-    p.ws_cnt = splits > 1 ? (unsigned long long *)(p.ws_ml + (int64_t)d.batch * d.num_heads * splits * 2) : nullptr;
+    p.ws_cnt = splits <= 1 ? nullptr
+               : cnt       ? cnt
+                           : (unsigned long long *)(p.ws_ml + (int64_t)d.batch * d.num_heads * splits * 2);
     p.tag = next_decode_tag();
     return launch_decode_int4(p, d.batch, d.head_dim, d.kv_format == MEMOPT_KV_INT4 ? MEMOPT_SCALE_F16 : d.scale_dtype, s);
   }
@@ -363,7 +374,9 @@ static int paged_attention(const memopt_attn_desc &d, bool unsplit_ok, void *str
     p.qk_scale_log2 = scale * 1.4426950408889634f;
     p.ws_o = (float *)d.workspace;
     p.ws_ml = splits > 1 ? p.ws_o + (int64_t)d.batch * d.num_heads * splits * d.head_dim : nullptr;
-    p.ws_cnt = splits > 1 ? (unsigned long long *)(p.ws_ml + (int64_t)d.batch * d.num_heads * splits * 2) : nullptr;
+    p.ws_cnt = splits <= 1 ? nullptr
+               : cnt       ? cnt
+                           : (unsigned long long *)(p.ws_ml + (int64_t)d.batch * d.num_heads * splits * 2);
     p.tag = next_decode_tag();
     return launch_decode_fp16(p, d.batch, d.head_dim, s);
   }
@@ -422,22 +435,26 @@ int memopt_paged_attention_noalloc(const memopt_attn_desc *desc, void *stream) {
   if (rc != MEMOPT_OK) return rc;
   if (d.batch == 0 || d.q_len == 0 || d.num_heads == 0 || d.head_dim == 0) return MEMOPT_OK;
   int64_t need = 0;
-  if (use_decode_int4(d) || use_decode_fp16(d)) {
+  const bool decode = use_decode_int4(d) || use_decode_fp16(d);
+  if (decode) {
     int32_t splits;
     decode_workspace(d, &splits, &need);
-    MEMOPT_REQUIRE(need <= MEMOPT_NOALLOC_SCRATCH_BYTES, MEMOPT_ERR_INVALID,
+    const int64_t units = (int64_t)d.batch * d.num_heads;
+    MEMOPT_REQUIRE(need <= kNoallocDataBytes && (need == 0 || units * 8 <= kNoallocCounterBytes),
+                   MEMOPT_ERR_INVALID,
                    "paged_attention_noalloc: the split-K partials need " + std::to_string(need) +
-                       " bytes, more than the " + std::to_string((long long)MEMOPT_NOALLOC_SCRATCH_BYTES) +
-                       "-byte static scratch");
+                       " bytes, more than the " + std::to_string((long long)kNoallocDataBytes) +
+                       " bytes of the static scratch they may use");
   } else if (prefill_supported(d)) {
     need = prefill_workspace_bytes(d);
-    if (need > MEMOPT_NOALLOC_SCRATCH_BYTES) need = 0;  // in-kernel staging: no scratch
+    if (need > kNoallocDataBytes) need = 0;  // in-kernel staging: no scratch
   }
   if (need > 0) {
-    void *ws = scratch_address();
+    uint8_t *ws = (uint8_t *)scratch_address();
     if (ws == nullptr) return MEMOPT_ERR_HIP;
     d.workspace = ws;
-    d.workspace_bytes = MEMOPT_NOALLOC_SCRATCH_BYTES;
+    d.workspace_bytes = kNoallocDataBytes;
+    if (decode) return paged_attention(d, false, stream, (unsigned long long *)(ws + kNoallocDataBytes));
   }
   return memopt_paged_attention(&d, stream);
 }

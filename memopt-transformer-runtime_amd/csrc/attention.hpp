@@ -81,9 +81,11 @@ unsigned long long next_decode_tag();
 // writes this split's partial to the workspace with agent-scope stores
 // (they bypass the per-XCD L2s, as the splits of one (b, h) run on
 // different XCDs), waits for them, and counts its arrival on (b, h) with a
-// compare-and-swap on (tag << 8 | count): a counter from another launch
-// (other tag, or any initial content) restarts at 1, so the workspace needs
-// no clearing. The split that brings the count to `splits` merges every
+// compare-and-swap on (tag << 8 | count): a counter left by an earlier
+// launch (other tag) or zero restarts at 1, so a workspace zeroed once needs
+// no clearing between launches (a fresh one must be zero: a stale word equal
+// to this launch's (tag << 8 | count) would stop the merge). The split that
+// brings the count to `splits` merges every
 // partial (log-sum-exp, agent-scope loads) into the output row. No
 // workgroup waits for another.
 template <int D, int NW>

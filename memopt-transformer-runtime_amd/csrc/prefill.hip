@@ -770,11 +770,16 @@ __device__ __forceinline__ void stage_blocks(const PrefillParams &p, uint8_t *__
 // nblocks / MC, of (sequence, head) q * ustride (ustride 1: every block of
 // the workspace,
 // head 0's writing the link flags; otherwise every head writes them, as
-// the staged units need not include head 0 of each sequence).
+// the staged units need not include head 0 of each sequence). The launch
+// also clears the call's `nflags` in-kernel staging flags: the attention
+// pass after it compares them with the call's tag, and a stale word equal to
+// that tag would let a workgroup read blocks before they are staged.
 template <int D, bool INT4>
 __global__ __launch_bounds__(256) void prefill_stage_kernel(const PrefillParams p, uint8_t *__restrict__ ws,
                                                             int32_t MC, int32_t units, int32_t ustride,
-                                                            int32_t nblocks) {
+                                                            int32_t nblocks, uint32_t *__restrict__ flags,
+                                                            int32_t nflags) {
+  for (int32_t i = blockIdx.x * 256 + threadIdx.x; i < nflags; i += gridDim.x * 256) flags[i] = 0u;
   const int32_t idx = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;  // 4 consecutive slots per wave (MC % 4 == 0)
   if (idx >= nblocks) return;  // wave-uniform
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[4][32 * D];
@@ -1570,28 +1575,29 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
       const char *spin = std::getenv("MEMOPT_PREFILL_STAGE_SPIN");
       ss.spin = spin ? std::atoi(spin) : 200000;
       const int32_t upx = (int32_t)(per_xcd / nqt), first = 8 * mc;
+      const int32_t nflags = d.batch * d.num_heads * 64;
       const dim3 fgrid((unsigned)((first + 15) / 16));
       if (d.head_dim == 128) {
         if (int4) {
           hipLaunchKernelGGL((prefill_stage_kernel<128, true>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
-                             first);
+                             first, ss.flags, nflags);
           hipLaunchKernelGGL((prefill_pipe_kernel<128, NW, true, true>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
                              units, ss);
         } else {
           hipLaunchKernelGGL((prefill_stage_kernel<128, false>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
-                             first);
+                             first, ss.flags, nflags);
           hipLaunchKernelGGL((prefill_pipe_kernel<128, NW, true, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
                              units, ss);
         }
       } else {
         if (int4) {
           hipLaunchKernelGGL((prefill_stage_kernel<64, true>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
-                             first);
+                             first, ss.flags, nflags);
           hipLaunchKernelGGL((prefill_pipe_kernel<64, NW, true, true>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
                              units, ss);
         } else {
           hipLaunchKernelGGL((prefill_stage_kernel<64, false>), fgrid, dim3(256), 0, stream, p, ws, mc, units, upx,
-                             first);
+                             first, ss.flags, nflags);
           hipLaunchKernelGGL((prefill_pipe_kernel<64, NW, true, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
                              units, ss);
         }
@@ -1599,13 +1605,17 @@ int launch_prefill(const memopt_attn_desc &d, int32_t W, float qk_scale_log2, hi
       return check_launch("paged_attention(prefill, staged in kernel)");
     }
     if (d.head_dim == 128) {
-      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<128, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
-      else hipLaunchKernelGGL((prefill_stage_kernel<128, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
+      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<128, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units,
+                                   nullptr, 0);
+      else hipLaunchKernelGGL((prefill_stage_kernel<128, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units,
+                                   nullptr, 0);
       hipLaunchKernelGGL((prefill_pipe_kernel<128, NW, false, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
                          units, ss);
     } else {
-      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<64, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
-      else hipLaunchKernelGGL((prefill_stage_kernel<64, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units);
+      if (int4) hipLaunchKernelGGL((prefill_stage_kernel<64, true>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units,
+                                   nullptr, 0);
+      else hipLaunchKernelGGL((prefill_stage_kernel<64, false>), sgrid, dim3(256), 0, stream, p, ws, mc, units, 1, units,
+                                   nullptr, 0);
       hipLaunchKernelGGL((prefill_pipe_kernel<64, NW, false, false>), grid, dim3(NW * 64), 0, stream, p, ws, mc,
                          units, ss);
     }

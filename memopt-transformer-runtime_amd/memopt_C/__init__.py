@@ -634,7 +634,11 @@ def _attention_desc(query, key_cache, value_cache, block_tables, context_lens, m
     _check(_c_ws(ctypes.byref(d), ctypes.byref(need)))
     ws = None
     if need.value > 0 and alloc_workspace:
-        ws = torch.empty(need.value, dtype=torch.uint8, device=query.device)
+        # A decode workspace holds split-K arrival counters, which must start
+        # from zero (later calls may reuse it without clearing); a
+        # multi-query workspace may hold anything.
+        alloc = torch.zeros if Lq == 1 else torch.empty
+        ws = alloc(need.value, dtype=torch.uint8, device=query.device)
         d.workspace, d.workspace_bytes = ws.data_ptr(), need.value
     return d, out, ws, keep
 

@@ -204,3 +204,46 @@ def test_config1_slice_golden_fixture():
     out = memopt_C.dynamic_sparse_attention(to_dev(f["q"]), kc, vc, to_dev(f["block_tables"]),
                                             to_dev(f["context_lens"]), 64, 24, num_sink_tokens=4)
     assert_close(out, f["out_pages_window24_sinks4"], what="config1 slice fixture")
+
+
+def _split_case(seed):
+    """4 (b, h) units over 2048 tokens: the decode splits each into 4."""
+    rng = np.random.default_rng(seed)
+    nb, H, D = 130, 4, 128
+    k = rng.standard_normal((nb, 16, H, D)).astype(np.float16)
+    v = rng.standard_normal((nb, 16, H, D)).astype(np.float16)
+    q = rng.standard_normal((1, 1, H, D)).astype(np.float16)
+    bt = rng.permutation(nb)[:128][None].astype(np.int32)
+    return q, O.to_int4_pages(k, v), bt, np.array([2048], np.int32)
+
+
+def test_split_decode_workspace_counters():
+    """The split-K arrival counters live in the workspace as (call id << 8 |
+    count). A call reusing a workspace finds only earlier calls' counters
+    there and needs no clearing; a fresh workspace is zeroed by the shim, so
+    memory that held a word equal to (next call's id << 8 | count) cannot
+    stop the merge. That memory is planted here: every freed block of the
+    workspace's size holds the next call's id with count 1 in every word,
+    and the call after it must still match the oracle (before the shim
+    zeroed decode workspaces, the merge never ran and the output kept
+    whatever its memory held)."""
+    q, pages, bt, cl = _split_case(21)
+    want = O.paged_attention_int4(q, pages, bt, cl, 2048, 2048)
+    pg, dq, dbt, dcl = to_dev(pages), to_dev(q), to_dev(bt), to_dev(cl)
+    call = memopt_C.PreparedAttention(dq, pg, pg, dbt, dcl, 2048, 2048)
+    nbytes = call.workspace_bytes
+    assert nbytes > 0                                   # split-K: partials and counters
+    for _ in range(3):                                  # one workspace, no clearing between calls
+        assert_close(call().clone(), want, what="reused workspace")
+    torch.cuda.synchronize()
+    cnt = call._ws[nbytes - 8 * 4:].view(torch.int64).cpu()
+    assert (cnt & 0xFF).tolist() == [4] * 4             # each (b, h): 4 splits arrived
+    nxt = int(cnt[0]) >> 8
+    assert (cnt >> 8).tolist() == [nxt] * 4
+    nxt += 1                                            # the next decode launch's id
+    poison = [torch.full((nbytes // 8,), (nxt << 8) | 1, dtype=torch.int64, device=dev()) for _ in range(32)]
+    torch.cuda.synchronize()
+    del poison
+    got = memopt_C.dynamic_sparse_attention(dq, pg, pg, dbt, dcl, 2048, 2048)
+    assert torch.isfinite(got).all()
+    assert_close(got, want, what="fresh workspace over stale memory")
