@@ -990,14 +990,16 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   for (int i = 0; i < NDB; ++i) o[i] = (float16_t){};
   // Row sums of the probabilities, one per 32-key block: two independent
   // chains of 8 dependent v_dot2 per tile instead of one chain of 16.
-  // The S accumulators hold raw scores q.k; the running max m enters each
-  // exp2 argument through one fma, cs s + ncm with ncm = -cs m (0 while m is
-  // -inf), so raising m touches no held score and no registers carry a -m
-  // splat for the MFMA chains to start from.
-  float m = -INFINITY, ncm = 0.0f, lsum = 0.0f, lsum1 = 0.0f;
-  // Raise threshold in raw score units, m + 8 / cs (-inf until the first
-  // visible key), so the per-tile test is one compare.
-  const float thr_off = 8.0f / cs;
+  // The QK chains start from zero and produce raw scores s = q.k; the block's
+  // producer then turns them into exp2 arguments x = cs s + ncm with one fma
+  // (ncm = -cs m for the running max m, 0 while no key of the lane is
+  // visible), and the S blocks held between iterations are those x. In the
+  // pipelined body the fmas run under the PV MFMAs of the iteration's last
+  // segment, which has issue slots to spare, so the two segments that run
+  // the exp2s carry no fma. Raising m shifts the held x by the same amount.
+  float ncm = 0.0f, lsum = 0.0f, lsum1 = 0.0f;
+  // Raise threshold in x units: 8 (a probability would exceed 2^8), -inf
+  // until the lane's first visible key, so the per-tile test is one compare.
   float thr = -INFINITY;
 
   const int32_t qlast = min(q0 + 32 * NW, p.Lq) - 1;
@@ -1201,34 +1203,45 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     for (int r = 0; r < 16; ++r) t = fmaxf(t, s[1][r]);
     return half_max(t);
   };
-  // Lazy running max (raw score units): rescale only when cs (score - m)
-  // exceeds 8, i.e. a probability would exceed 2^8; the first visible key
-  // always raises.
-  auto raise_max = [&](float tmax) __attribute__((always_inline)) {
+  // Raw scores of an S block to exp2 arguments.
+  auto to_x = [&](float16_t &s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = fmaf(s[r], cs, ncm);
+  };
+  // Lazy running max (x units, tmax = the lane's largest x of the tile):
+  // rescale only when tmax exceeds 8; the lane's first visible key always
+  // raises (its x becomes the reference, with o and the sums still 0; a
+  // NaN or -inf tmax leaves the lane waiting). The held blocks sc shift
+  // with the reference.
+  auto raise_max = [&](float tmax, float16_t (&sc)[2]) __attribute__((always_inline)) {
     if (__any(tmax > thr)) {
-      const float mn = fmaxf(m, tmax);
-      const float alpha = (mn == m) ? 1.0f : fast_exp2((m - mn) * cs);
+      const bool first = thr == -INFINITY, found = tmax > -INFINITY;
+      const float shift = first ? (found ? tmax : 0.0f) : fmaxf(tmax, 0.0f);
+      const float alpha = first ? (found ? 0.0f : 1.0f) : (shift > 0.0f ? fast_exp2(-shift) : 1.0f);
       lsum *= alpha;
       lsum1 *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      m = mn;
-      ncm = (mn == -INFINITY) ? 0.0f : -mn * cs;
-      thr = mn + thr_off;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[blk][r] -= shift;
+      ncm -= shift;
+      thr = (first && !found) ? thr : 8.0f;
     }
   };
   const half2_t ones = {(half_t)1.0f, (half_t)1.0f};
-  // exp2 of one S block, packed to fp16 in PV B-operand order; adds the
-  // probabilities to the running sum from the packed words themselves (the
-  // same pairs rebuilt from the half8 operands cost 12 conversions a tile).
+  // exp2 of one S block (exp2 arguments), packed to fp16 in PV B-operand
+  // order; adds the probabilities to the running sum from the packed words
+  // themselves (the same pairs rebuilt from the half8 operands cost 12
+  // conversions a tile).
   auto probs = [&](const float16_t &s, half8_t (&pb)[2], float &ls) __attribute__((always_inline)) {
     uint32_t w[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      w[i] = as_u32(half2_t{(half_t)fast_exp2(fmaf(s[2 * i], cs, ncm)),
-                            (half_t)fast_exp2(fmaf(s[2 * i + 1], cs, ncm))});
+      w[i] = as_u32(half2_t{(half_t)fast_exp2(s[2 * i]), (half_t)fast_exp2(s[2 * i + 1])});
 #pragma unroll
     for (int i = 0; i < 8; ++i) ls = __builtin_amdgcn_fdot2(as_half2(w[i]), ones, ls, false);
     pb[0] = __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
@@ -1271,6 +1284,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     if (wave_vis(0)) {
       qk_block(lds_k0, 0, sx[0], IntC<0>{}, none);
       if (!sink_half) qk_block(lds_k0, 1, sx[1], IntC<0>{}, none);
+      to_x(sx[0]);
+      to_x(sx[1]);
     }
     __syncthreads();  // K(0)'s buffer is refilled by the first iteration
   }
@@ -1312,7 +1327,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
         PIPE_SGB(0x002, 2, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      raise_max(tmax);
+      raise_max(tmax, sc);
       if (k_ahead) load_k(it + 2, IntC<P>{}, IntC<NKL / 2>{}, IntC<NKL>{});
       // Seg 2: QK(i+1) block 1 | probabilities of S(i) block 0
       half8_t pa[2], pb[2];
@@ -1324,7 +1339,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       for (int c = 0; c < NCH; ++c) {
         PIPE_SGB(0x008, 1, 0);
         PIPE_SGB(0x100, 1, 0);
-        PIPE_SGB(0x002, 32 / NCH, 0);  // per exp2: a scale fma, half a pack, half a row-sum dot
+        PIPE_SGB(0x002, 16 / NCH, 0);  // per exp2: half a pack, half a row-sum dot
         PIPE_SGB(0x400, 16 / NCH, 0);
       }
       // The probabilities must be complete here: without this use the
@@ -1342,18 +1357,21 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       for (int c = 0; c < 2 * NDB; ++c) {
         PIPE_SGB(0x008, 1, 0);
         PIPE_SGB(0x100, 1, 0);
-        PIPE_SGB(0x002, 32 / (2 * NDB), 0);
+        PIPE_SGB(0x002, 16 / (2 * NDB), 0);
         PIPE_SGB(0x400, 16 / (2 * NDB), 0);
       }
       asm volatile("" ::"v"(pb[0]), "v"(pb[1]));
       __builtin_amdgcn_sched_barrier(0);
       if (v_ahead) load_v(it + 1, IntC<P ^ 1>{}, IntC<NVL / 2>{}, IntC<NVL>{});
-      // Seg 4: PV(i) block 1
+      // Seg 4: PV(i) block 1 | S(i+1) to exp2 arguments
       pv_block(IntC<P>{}, 1, pb, pre_b);
+      to_x(sn[0]);
+      to_x(sn[1]);
 #pragma unroll
       for (int c = 0; c < 2 * NDB; ++c) {
         PIPE_SGB(0x008, 1, 0);
         if (c < 4) PIPE_SGB(0x100, 1, 0);
+        PIPE_SGB(0x002, 32 / (2 * NDB), 0);
       }
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(0);
@@ -1385,7 +1403,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       } else {
         tmax = row_max(sc);
       }
-      raise_max(tmax);
+      raise_max(tmax, sc);
       half8_t pa[2], pre[4];
       probs(sc[0], pa, lsum);
       if (one && sink_quarter) {
@@ -1411,6 +1429,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     if (nxt) {
       qk_block(kt, 0, sn[0], IntC<0>{}, none);
       qk_block(kt, 1, sn[1], IntC<0>{}, none);
+      to_x(sn[0]);
+      to_x(sn[1]);
     } else {
       sn[0] = (float16_t){};
       sn[1] = (float16_t){};
@@ -1454,7 +1474,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   const float l = half_sum(lsum + lsum1);
   if (!q_ok) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  half_t *orow = p.out + (((int64_t)b * p.Lq + qi) * p.H + h) * D;
+  // The row's offset is rebuilt here from the lane id, not taken from the Q
+  // load's address: that 64-bit value, live across the tile loops, spills
+  // at 256 VGPRs.
+  int32_t qo = qw0 + (int32_t)(__lane_id() & 31);
+  asm volatile("" : "+v"(qo));
+  half_t *orow = p.out + (((int64_t)b * p.Lq + qo) * p.H + h) * D;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
