@@ -1146,6 +1146,17 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     const uint32_t m0v = buf ? mv1 : mv0, soff = tile_slot(it) * CS;
     lds_dma_range<C0, C1>(rs, m0v, vvo, soff);
   };
+  // The same for a window tile (it >= sink_tiles), whose slot needs no select.
+  auto load_kw = [&](int32_t it, auto bufc, auto c0c, auto c1c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value, C0 = decltype(c0c)::value, C1 = decltype(c1c)::value;
+    const uint32_t m0v = buf ? mk1 : mk0, soff = (uint32_t)(4 * it + slot_w) * CS;
+    lds_dma_range<C0, C1>(rs, m0v, kvo, soff);
+  };
+  auto load_vw = [&](int32_t it, auto bufc, auto c0c, auto c1c) __attribute__((always_inline)) {
+    constexpr int buf = decltype(bufc)::value, C0 = decltype(c0c)::value, C1 = decltype(c1c)::value;
+    const uint32_t m0v = buf ? mv1 : mv0, soff = (uint32_t)(4 * it + slot_w) * CS;
+    lds_dma_range<C0, C1>(rs, m0v, vvo, soff);
+  };
   // End of a tile: wait for this thread's tile copies except the newest
   // `keep` (the K prefetch, which has another tile of time) and for its LDS
   // reads (the next copies overwrite buffers read in this tile); then the
@@ -1300,7 +1311,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
     const uint8_t *const kt = P ? lds_k0 : lds_k1;
     const int32_t tb = tile_base(it);
     const bool v_ahead = it + 1 < n_tiles, k_ahead = it + 2 < n_tiles;
-    if (k_ahead) load_k(it + 2, IntC<P>{}, IntC<0>{}, IntC<NKL / 2>{});
+    if (k_ahead) load_kw(it + 2, IntC<P>{}, IntC<0>{}, IntC<NKL / 2>{});
     // Tiles that are not fully visible go through the mask.
     if ((uint32_t)(it - it_full) >= (uint32_t)n_full) apply_mask(sc, tb, it);
     {
@@ -1328,7 +1339,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       raise_max(tmax, sc);
-      if (k_ahead) load_k(it + 2, IntC<P>{}, IntC<NKL / 2>{}, IntC<NKL>{});
+      if (k_ahead) load_kw(it + 2, IntC<P>{}, IntC<NKL / 2>{}, IntC<NKL>{});
       // Seg 2: QK(i+1) block 1 | probabilities of S(i) block 0
       half8_t pa[2], pb[2];
       qk_block(kt, 1, sn[1], IntC<1>{}, pre_k);
@@ -1347,7 +1358,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       // segment 3, ahead of the PV MFMAs that need them.
       asm volatile("" ::"v"(pa[0]), "v"(pa[1]));
       __builtin_amdgcn_sched_barrier(0);
-      if (v_ahead) load_v(it + 1, IntC<P ^ 1>{}, IntC<0>{}, IntC<NVL / 2>{});
+      if (v_ahead) load_vw(it + 1, IntC<P ^ 1>{}, IntC<0>{}, IntC<NVL / 2>{});
       // Seg 3: PV(i) block 0 | probabilities of S(i) block 1
       pv_block(IntC<P>{}, 0, pa, pre_a);
       probs(sc[1], pb, lsum1);
@@ -1362,7 +1373,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
       }
       asm volatile("" ::"v"(pb[0]), "v"(pb[1]));
       __builtin_amdgcn_sched_barrier(0);
-      if (v_ahead) load_v(it + 1, IntC<P ^ 1>{}, IntC<NVL / 2>{}, IntC<NVL>{});
+      if (v_ahead) load_vw(it + 1, IntC<P ^ 1>{}, IntC<NVL / 2>{}, IntC<NVL>{});
       // Seg 4: PV(i) block 1 | S(i+1) to exp2 arguments
       pv_block(IntC<P>{}, 1, pb, pre_b);
       to_x(sn[0]);
@@ -1442,7 +1453,10 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void prefill_pipe_kernel(
   // iterations per trip, so buffer indices and score registers stay
   // compile-time constants (a parity branch per iteration instead made the
   // compiler spill).
-  const int32_t m0 = min(n_tiles, c0 + (c0 & 1)), m1 = max(m0, c1);
+  // (The pipelined body copies tiles it + 1 and it + 2 as window tiles, so
+  // it starts no earlier than sink_tiles - 1.)
+  const int32_t mp = max(c0, sink_tiles - 1);
+  const int32_t m0 = min(n_tiles, mp + (mp & 1)), m1 = max(m0, c1);
   int32_t it = 0;
   for (; it < m0; it += 2) {
     iter_edge(it, sx, sy, IntC<0>{});

@@ -36,6 +36,8 @@ PREFILL_CASES = [
     (1, 1, 128, 16, [1100], 1100, 2048, 1024, 4, True, False),  # window just under the sequence
     (1, 2, 64, 16, [257], 17, 512, 33, 5, True, True),          # ragged sizes, sinks not tile-aligned
     (1, 2, 128, 16, [640], 16, 640, 640, 0, False, False),      # smallest q_len on this path
+    (1, 2, 128, 16, [1500], 700, 2048, 256, 150, True, False),  # 150 sinks: three sink tiles before the window
+    (2, 2, 64, 16, [900, 650], 128, 1024, 200, 100, False, True),  # non-causal, two sink tiles
 ]
 
 
