@@ -273,6 +273,31 @@ def bench_fp16_decode(torch, memopt_C, cfg, steps=20):
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_fp16_write(torch, memopt_C, cfg, steps=20):
+    """write_cache into the fp16 page pool bench_fp16_decode leaves: 4 x ctx
+    tokens of config 2's K and V (2 x [16384, 32, 128]) into slots drawn at
+    random from the pool (each token's H x D row lands on its own 8 KB), with
+    validate_slots=False so the call is the scatter launch alone (the default
+    check is a device min/max and one host read per call). GB/s on the bytes
+    read and written."""
+    H, D, ctx = cfg["heads"], cfg["head_dim"], cfg["ctx"]
+    dev = torch.device("cuda", 0)
+    T = 4 * ctx
+    g = torch.Generator(device=dev).manual_seed(2)
+    k = torch.randn(T, H, D, device=dev, generator=g).half()
+    v = torch.randn(T, H, D, device=dev, generator=g).half()
+    kc, _ = memopt_C.get_pool_tensors()
+    nslots = kc.shape[0] * kc.shape[1]
+    slots = torch.randperm(nslots, generator=torch.Generator().manual_seed(2))[:T].to(torch.int32).to(dev)
+    bt = torch.zeros(1, 1, dtype=torch.int32, device=dev)
+    ms, _ = time_steps(torch, [lambda: memopt_C.write_cache(k, v, bt, slots, validate_slots=False)], steps, 3)
+    nbytes = 4 * T * H * D * 2
+    return {"workload": "write_cache fp16 scatter, 2 x [16384, 32, 128] into random slots of an fp16 page pool",
+            "kernel": "write_fp16_kernel", "kernel_ms": round(ms, 5), "bytes_moved": nbytes,
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def bench_kv_quant(torch, memopt_C, cfg, steps=20):
     """Fused write + quantize of config 2's K and V into INT4 pages (write_cache), GB/s."""
     B, H, D, ctx, bs = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["ctx"], cfg["block"]
@@ -671,6 +696,7 @@ def main():
             **bench_long_context_policy(torch, memopt_C, CFG5))
         sec["kv_quant"] = bench_kv_quant(torch, memopt_C, cfg)
         sec["fp16_pool_decode"] = bench_fp16_decode(torch, memopt_C, cfg)
+        sec["fp16_write_cache"] = bench_fp16_write(torch, memopt_C, cfg)
         line["secondary"] = sec
     print(json.dumps(line), flush=True)
 
