@@ -256,6 +256,19 @@ __global__ __launch_bounds__(kThreads) void write_int4_pages_kernel(
   const half_t *__restrict__ src = is_v ? values : keys;
   const int64_t codes_off = is_v ? f.vcodes : f.kcodes, scales_off = is_v ? f.vscales : f.kscales;
 
+  // The full-page path's loads do not depend on the slots, so they are issued
+  // before the slot check (rows clamped to T - 1; unused when the group
+  // scatters) and overlap its round trip: 2 x [16384, 32, 128] went from
+  // 0.80 to 0.84-0.86 of HBM.
+  const int p = lane >> 3, c = lane & 7;
+  uint4 raw[2][KW];
+#pragma unroll
+  for (int tk = 0; tk < 2; ++tk) {
+    const uint32_t row = min(t0 + p + 8 * tk, T - 1);
+    const size_t o = (size_t)row * rowstride + (size_t)h * D + c * DPL;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) raw[tk][k] = *reinterpret_cast<const uint4 *>(src + o + 8 * k);
+  }
   int32_t sl = -1;
   if (lane < 16 && t0 + lane < T) sl = slots[t0 + lane];
   const int32_t s0 = __builtin_amdgcn_readfirstlane(sl);
@@ -263,15 +276,11 @@ __global__ __launch_bounds__(kThreads) void write_int4_pages_kernel(
   const bool full = __all(mine) && s0 >= 0 && (s0 & 15) == 0 && (int64_t)s0 + 16 <= n_slots;
 
   if (full) {
-    const int p = lane >> 3, c = lane & 7;
-    const size_t off = (size_t)t0 * rowstride + (size_t)h * D + c * DPL;
     float x[2][DPL];
 #pragma unroll
-    for (int tk = 0; tk < 2; ++tk) {
-      const size_t o = off + (size_t)(p + 8 * tk) * rowstride;
+    for (int tk = 0; tk < 2; ++tk)
 #pragma unroll
-      for (int k = 0; k < KW; ++k) unpack_half8(*reinterpret_cast<const uint4 *>(src + o + 8 * k), &x[tk][8 * k]);
-    }
+      for (int k = 0; k < KW; ++k) unpack_half8(raw[tk][k], &x[tk][8 * k]);
     float am[2];
 #pragma unroll
     for (int tk = 0; tk < 2; ++tk) {
