@@ -299,7 +299,8 @@ def _prefill_with_env(env, *args, **kw):
                 os.environ[k] = v
 
 
-def test_in_kernel_staging_paths_agree():
+@pytest.mark.parametrize("D,fmt", [(128, "int4"), (64, "int4"), (128, "fp16")])
+def test_in_kernel_staging_paths_agree(D, fmt):
     """Long causal prefill (q_len 4096, so the attention kernel stages the
     workspace itself: each XCD's first (sequence, head) unit by a staging
     launch, every later unit by the first workgroups of the unit before it)
@@ -309,11 +310,11 @@ def test_in_kernel_staging_paths_agree():
     waiting workgroup stages its unit itself (MEMOPT_PREFILL_STAGE_SPIN=-1)
     agree, and sequence 0 matches fp32 attention over the dequantized pool
     on every row of two heads."""
-    B, S, H, D, W, sinks = 3, 4096, 8, 128, 1024, 4
+    B, S, H, W, sinks = 3, 4096, 8, 1024, 4
     torch.manual_seed(13)
     nbps = S // 16
     nb = B * nbps + 8
-    memopt_C.init_pool(nb, 16, H, D, kv_format="int4")
+    memopt_C.init_pool(nb, 16, H, D, kv_format=fmt)
     order = torch.randperm(nb)[:B * nbps].to(torch.int32).reshape(B, nbps)
     bt = order.to(dev())
     for b in range(B):
@@ -333,8 +334,11 @@ def test_in_kernel_staging_paths_agree():
     assert torch.isfinite(ink).all()
     assert_close(ink, launch.float().cpu().numpy(), what="in-kernel vs staging launch")
     assert_close(self_staged, launch.float().cpu().numpy(), what="self-staged vs staging launch")
-    pages = memopt_C.get_int4_pages()
-    kd, vd = O.dequant_pages_torch(pages[order[0].to(dev()).long()], D)
+    if fmt == "int4":
+        kd, vd = O.dequant_pages_torch(memopt_C.get_int4_pages()[order[0].to(dev()).long()], D)
+    else:
+        kc, vc = memopt_C.get_pool_tensors()
+        kd, vd = kc[order[0].to(dev()).long()].float(), vc[order[0].to(dev()).long()].float()
     kd, vd = kd.reshape(S, H, D), vd.reshape(S, H, D)
     for h in (0, 5):
         ref = _fp32_head_reference(q[0, :, h], kd[:, h], vd[:, h], 0, S, S, W, sinks)
