@@ -85,6 +85,23 @@ def test_noalloc_staged_prefill_two_calls():
                      what="noalloc prefill")
 
 
+def test_noalloc_decode_after_staged_prefill():
+    """A staged multi-query call writes its K/V over the scratch the split-K
+    partials use; the decode after it must still merge its splits (its
+    arrival counters live in the scratch's last 64 KiB, which nothing else
+    writes)."""
+    pre = _pages_case(7, 1, 2, 128, [512], 128)
+    dec = _pages_case(8, 1, 4, 128, [8192], 1)
+    for _ in range(2):
+        got, want, _ = _run_both(pre, 1 << 20, 256, 4, True)
+        assert torch.equal(got, want)
+        got, want, ws_bytes = _run_both(dec, 1 << 20, 8192, 4, False)
+        assert ws_bytes > 0 and torch.equal(got, want)
+        q, pages, bt, cl = dec
+        assert_close(got, O.paged_attention_int4(q, pages, bt, cl, 1 << 20, 8192, num_sink_tokens=4),
+                     what="noalloc decode after a staged prefill")
+
+
 def test_noalloc_prepared_attention_and_limit():
     """PreparedAttention(no_alloc=True) holds no workspace and matches the
     regular call; partials past the scratch (forced splits) are refused."""
