@@ -28,10 +28,16 @@ struct IntC {
 // Order-preserving uint32 key of a float: negative values have every bit
 // flipped, others the sign bit set; -0 takes the key of +0 (f + 0 turns -0
 // into +0 and leaves every other value as it is), since the two compare
-// equal: a -0 score ties with a +0 tau, as in float compares.
+// equal: a -0 score ties with a +0 tau, as in float compares. A NaN of
+// either sign gets key 0, which no other float has (-inf's key is
+// 0x007FFFFF): the reference's selection counts and evicts by float
+// compares, which a NaN never passes, so a NaN ranks below every score and
+// is never evicted (kNanKey is excluded wherever a key < tau evicts).
+static constexpr uint32_t kNanKey = 0u;
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t u = __builtin_bit_cast(uint32_t, f + 0.0f);
-  return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+  const uint32_t k = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+  return f != f ? kNanKey : k;
 }
 
 // Set in a page mark when two or more live block-table entries of one call
@@ -314,7 +320,7 @@ __device__ __forceinline__ uint32_t token_key(const float *row, int32_t t, int32
 // Thread tid owns tokens t = tid + i NT, i < R; their keys stay in registers,
 // so the row is read once (rows up to R NT tokens).
 //  A. tau = key of the keep-th largest sink-boosted score, by radix_select.
-//  B. evicted-token bitmask in LDS (key < tau, sinks excluded), then zero the
+//  B. evicted-token bitmask in LDS (key < tau, sinks and NaN excluded), then zero the
 //     evicted (token, head) rows.
 //  C. block votes: a full logical block whose every token is evicted votes
 //     is_block_free[phys] += 1; the vote that reaches H unlinks it. A head
@@ -362,7 +368,7 @@ __global__ __launch_bounds__(NT) void evict_tokens_kernel(
   for (int i = tid; i < nwords; i += NT) evbits[i] = 0;
   __syncthreads();
   for_keys([&](int32_t t, uint32_t key) {
-    const uint64_t m = __ballot(t >= sinks && key < tau);
+    const uint64_t m = __ballot(t >= sinks && key < tau && key != kNanKey);
     if (lane == 0 && m) {
       evbits[t / 32] = (uint32_t)m;
       evbits[t / 32 + 1] = (uint32_t)(m >> 32);
@@ -1032,7 +1038,7 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
     // The spans' candidate lists. The classify launch places a token by
     // float compares with the floats of lo and hi; a score the compares
     // cannot place (a NaN) is listed whatever its key: listed keys above
-    // hi count as kept, keys below lo are evicted, and the select runs over
+    // hi count as kept, keys below lo are evicted (a NaN's never is), and the select runs over
     // the keys in [lo, hi], whose first-pass histogram is built here.
     uint32_t xa = 0, xi = 0;
     auto take = [&](uint32_t e, uint2 c) {
@@ -1125,7 +1131,8 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
       }
       for (uint32_t i = tid; i < nc; i += NT) {
         const int32_t t = (int32_t)sm.lpos[i], w = (t >> 5) - w0;
-        if (sm.lkey[i] < tau && t >= lr.sinks && w >= 0 && w < kLdsWords) atomicOr(&sm.lbits[w], 1u << (t & 31));
+        const uint32_t k = sm.lkey[i];
+        if (k < tau && k != kNanKey && t >= lr.sinks && w >= 0 && w < kLdsWords) atomicOr(&sm.lbits[w], 1u << (t & 31));
       }
       __syncthreads();
       uint32_t lb[PW], gw[PW];
@@ -1161,7 +1168,8 @@ __global__ __launch_bounds__(kResNT) void evict_resolve_long_kernel(const LongRo
   const int32_t nw64 = (L + 63) / 64;
   for (int32_t w = wave; w < nw64; w += NW) {
     const int32_t t = w * 64 + lane;
-    const bool e = t < L && t >= lr.sinks && token_key(row, min(t, L - 1), lr.sinks) < tau;
+    const uint32_t key = token_key(row, min(t, L - 1), lr.sinks);
+    const bool e = t < L && t >= lr.sinks && key < tau && key != kNanKey;
     const uint64_t b = __ballot(e);
     if (lane == 0) {
       bits[2 * w] = (uint32_t)b;

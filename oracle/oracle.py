@@ -442,7 +442,9 @@ def evict_tokens_intended(scores, block_tables, is_block_free, retain_ratio,
 
     Per (seq, head): sink scores := 1e38 (:722-726); keep = keep_count;
     tau = keep-th largest boosted score; tokens with boosted score < tau are
-    evicted (ties at tau kept); every evicted (token, head) row is zeroed
+    evicted (ties at tau kept; a NaN score, of either sign, is sorted after
+    every number and fails s < tau: it takes no rank and is never evicted,
+    as under the reference's float compares, :757-803, :814-868); every evicted (token, head) row is zeroed
     (fp16: zeros; INT4 pages: its scales set to 0, see _zero_row); pools = {"format": "fp16", "k", "v"} or
     {"format": "int4", "pages", "D"}. A logical block whose block_size positions are all
     evicted in this head votes is_block_free[phys] += 1; the vote that

@@ -176,6 +176,25 @@ def test_evict_tokens_signed_zero_ties(L):
     _evict_case("int4", N, H, L, 64, 0.5, 4, s)
 
 
+@pytest.mark.parametrize("kind", ["scattered", "mostly_nan"])
+@pytest.mark.parametrize("fmt,L", [("int4", 5000), ("fp16", 5000), ("int4", 70000), ("fp16", 40000)])
+def test_evict_tokens_nan_scores(fmt, L, kind):
+    """NaN scores of both signs, with +-0 and +-inf beside them: a NaN is
+    never evicted and takes no place in the ranking, as under the
+    reference's float compares (scattered: 1 % NaN, keep 75 %). mostly_nan:
+    40 % NaN and keep 70 %, fewer non-NaN scores than keep, so nothing is
+    evicted. Short rows (one workgroup) and long rows (a NaN becomes a
+    candidate; the resolve and its whole-row select leave it in place)."""
+    rng = np.random.default_rng(L + (7 if kind == "scattered" else 9))
+    N, H = 1, 2
+    s = rng.standard_normal((N, H, L)).astype(np.float32)
+    nan = rng.random((N, H, L)) < (0.01 if kind == "scattered" else 0.4)
+    neg_nan = np.frombuffer(np.uint32(0xFFC00000).tobytes(), np.float32)[0]
+    s[nan] = np.where(rng.random(int(nan.sum())) < 0.5, np.float32(np.nan), neg_nan)
+    s[0, 0, 100:104] = [np.inf, -np.inf, 0.0, -0.0]
+    _evict_case(fmt, N, H, L, 64, 0.75 if kind == "scattered" else 0.7, 4, s)
+
+
 @pytest.mark.parametrize("kind", ["wide", "cluster", "wide_cluster"])
 def test_evict_tokens_long_rows_select_passes(kind):
     """The resolve's exact select over the candidates in [lo, hi], a 12-bit

@@ -374,6 +374,38 @@ def test_evict_intended_brute_force(fmt, r, sinks):
     assert ((bt == -1) == (free[np.clip(bt0, 0, None)] == H)).all()
 
 
+@pytest.mark.parametrize("nan_frac,r", [(0.1, 0.5), (0.6, 0.75)])
+def test_evict_intended_nan_scores(nan_frac, r):
+    """NaN scores (both signs) next to +-0 and +-inf. The reference selects
+    and evicts by float compares (src/csrc/kv_cache.cu:757-803, :814-868),
+    which a NaN never passes, so a NaN is never evicted and takes no place in
+    the ranking: tau = the keep-th largest non-NaN boosted score, and nothing
+    is evicted when fewer than keep scores are non-NaN (nan_frac 0.6,
+    keep 75 %). Brute force over Python floats, NaN filtered by math.isnan."""
+    rng = np.random.default_rng(11)
+    N, H, L, D, bs, sinks = 1, 2, 64, 64, 16, 3
+    scores = rng.standard_normal((N, H, L)).astype(np.float32)
+    neg_nan = np.frombuffer(np.uint32(0xFFC00000).tobytes(), np.float32)[0]
+    nan = rng.random((N, H, L)) < nan_frac
+    scores[nan] = np.where(rng.random(int(nan.sum())) < 0.5, np.float32(np.nan), neg_nan)
+    scores[0, 0, 40:44] = [np.inf, -np.inf, 0.0, -0.0]
+    pools = _pools("int4", 6, bs, H, D, rng)
+    bt = rng.permutation(6)[:4].reshape(1, 4).astype(np.int32)
+    ev = O.evict_tokens_intended(scores, bt, np.zeros(6, np.int32), r, sinks, pools, bs)
+    keep = max(1, min(L, math.ceil(np.float32(r) * np.float32(L))))
+    for h in range(H):
+        boosted = [1e38 if t < sinks else float(scores[0, h, t]) for t in range(L)]
+        ranked = sorted((x for x in boosted if not math.isnan(x)), reverse=True)
+        want = [False] * L
+        if len(ranked) >= keep:
+            tau = ranked[keep - 1]
+            want = [t >= sinks and not math.isnan(boosted[t]) and boosted[t] < tau for t in range(L)]
+        assert ev[0, h].tolist() == want
+        assert not any(ev[0, h, t] for t in range(L) if math.isnan(boosted[t]))
+    if nan_frac > 0.5:
+        assert not ev.any()
+
+
 def test_evict_intended_unlinks_fully_evicted_blocks():
     N, H, L, bs = 1, 2, 16, 4
     scores = np.ones((N, H, L), np.float32)
