@@ -125,7 +125,8 @@ def dequantize_int4(packed: np.ndarray, scales: np.ndarray, group_size: int = GR
     assert group_size == GROUP
     codes = unpack_codes(packed).astype(np.float32) - np.float32(8.0)
     s = np.asarray(scales).astype(np.float32).reshape(-1)
-    vals = (codes.reshape(-1, GROUP) * s[:, None]).astype(np.float32)
+    with np.errstate(invalid="ignore"):  # code 8 under an inf scale: 0 * inf = NaN, as on the device
+        vals = (codes.reshape(-1, GROUP) * s[:, None]).astype(np.float32)
     shape = tuple(packed.shape[:-1]) + (packed.shape[-1] * 2,)
     return vals.astype(np.float16).reshape(shape)
 

@@ -78,3 +78,29 @@ def reference_decode_dev(q, kpool, vpool, bt, ctx, W, sinks):
         p = torch.softmax(s, dim=-1)
         out[b] = (p[:, None, :] @ v).squeeze(1)
     return out.half()[:, None]
+
+
+def special_fp16(shape, seed):
+    """fp16 data with NaN of both signs, +-inf, -0, subnormals and +-65504
+    scattered through normal values (3 %), and whole 64-element groups of
+    them: all NaN, all -NaN, all inf, all subnormal, all -0, 65504 in every
+    other element, one inf, one NaN (the first 8 groups of the flattened
+    tensor, which must hold at least 8)."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(shape).astype(np.float16)
+    neg_nan = np.frombuffer(np.uint16(0xFE00).tobytes(), np.float16)[0]
+    vals = np.array([np.nan, neg_nan, np.inf, -np.inf, -0.0, 6e-8, -6e-8, 1e-5, 65504, -65504], np.float16)
+    flat = x.reshape(-1)
+    m = rng.random(flat.size) < 0.03
+    flat[m] = vals[rng.integers(0, vals.size, int(m.sum()))]
+    g = flat.reshape(-1, 64)
+    assert g.shape[0] >= 8
+    g[0] = np.nan
+    g[1] = neg_nan
+    g[2] = np.inf
+    g[3] = np.float16(6e-8)
+    g[4] = np.float16(-0.0)
+    g[5, ::2] = np.float16(65504)
+    g[6, 0] = np.inf
+    g[7, 0] = np.nan
+    return x

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_helpers import dev, memopt_C, same_bits, to_dev
+from gpu_helpers import dev, memopt_C, same_bits, special_fp16, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -90,6 +90,24 @@ def test_write_cache_int4_scatter_orders_bit_exact(D, order):
         slots = rng.permutation(nb * bs)[:T].astype(np.int32)
     else:
         slots = (np.arange(T) + 1).astype(np.int32)  # every group straddles two pages
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)), to_dev(slots))
+    wk, wv = np.zeros((nb, bs, H, D), np.float16), np.zeros((nb, bs, H, D), np.float16)
+    O.write_cache(wk, k, slots)
+    O.write_cache(wv, v, slots)
+    same_bits(memopt_C.get_int4_pages(), O.to_int4_pages(wk, wv))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("order", ["pages", "shifted"])
+def test_write_cache_int4_special_values_bit_exact(D, order):
+    """write_cache into INT4 pages of K and V holding NaN of both signs,
+    +-inf, -0, subnormals and +-65504 (aligned pages take the page path,
+    slots shifted by one the chunk scatter): the pool's bytes equal the
+    oracle's."""
+    nb, bs, H, T = 12, 16, 3, 160
+    memopt_C.init_pool(nb, bs, H, D, kv_format="int4")
+    k, v = special_fp16((T, H, D), 6), special_fp16((T, H, D), 7)
+    slots = (np.arange(T) + (order == "shifted")).astype(np.int32)
     memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)), to_dev(slots))
     wk, wv = np.zeros((nb, bs, H, D), np.float16), np.zeros((nb, bs, H, D), np.float16)
     O.write_cache(wk, k, slots)

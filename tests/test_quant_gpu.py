@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_helpers import dev, memopt_C, same_bits, to_dev
+from gpu_helpers import dev, memopt_C, same_bits, special_fp16, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -59,6 +59,15 @@ def test_shapes_and_dtypes(shape):
 @pytest.mark.parametrize("shape", [(4, 128), (2, 8, 64), (129, 64), (64, 16, 8, 64)])
 def test_bit_exact_vs_oracle(shape, dist):
     check_exact(make(shape, dist))
+
+
+@pytest.mark.parametrize("shape", [(4, 128), (64, 16, 8, 64)])
+def test_special_values_bit_exact(shape):
+    """NaN of both signs, +-inf, -0, subnormals and +-65504, scattered and as
+    whole groups: codes, scales and the dequantized values bit-exact with the
+    oracle (the reference's fmaxf leaves a NaN out of the absmax; an inf
+    absmax gives scale inf)."""
+    check_exact(torch.from_numpy(special_fp16(shape, 5)))
 
 
 @pytest.mark.parametrize("num_groups,dist,bound,relative", [
