@@ -202,6 +202,71 @@ def test_evict_tokens_sweep(seed):
     same_bits(ibf_d, ibf)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_evict_tokens_long_rows_sweep(seed):
+    """Long rows (L > 32768: classify, resolve, apply) with a different score
+    distribution per seed (lognormal, normal, few distinct integers, two
+    tight modes, ascending, normal with many +-0 and some NaN of both signs)
+    and block tables that share pages between sequences, hold unlinked
+    entries and entries past the pool, against the oracle bit for bit."""
+    rng = np.random.default_rng(9500 + seed)
+    fmt = "fp16" if seed % 3 == 2 else "int4"
+    N, H = 2, int(rng.integers(1, 3))
+    L = int(rng.integers(32769, 90000))
+    r = float(rng.choice([0.05, 0.25, 0.5, 0.75, 0.95]))
+    sinks = int(rng.integers(0, 100))
+    bs, D = 16, 64
+    M = (L + bs - 1) // bs
+    nb = N * M + 2
+    memopt_C.reset_pool()
+    memopt_C.init_pool(nb, bs, H, D, kv_format=fmt)
+    k, v = _kv(rng, (nb * bs, H, D))
+    memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)),
+                         to_dev(np.arange(nb * bs, dtype=np.int32)))
+    shape = (N, H, L)
+    dist = seed % 6
+    if dist == 0:
+        s = rng.lognormal(size=shape)
+    elif dist == 1:
+        s = rng.standard_normal(shape)
+    elif dist == 2:
+        s = rng.integers(0, 50, size=shape).astype(np.float64)
+    elif dist == 3:
+        s = np.where(rng.random(shape) < 0.5, rng.normal(-5, 0.01, shape), rng.normal(5, 0.01, shape))
+    elif dist == 4:
+        s = np.broadcast_to(np.arange(L, dtype=np.float64) * 1e-3, shape).copy()
+    else:
+        s = rng.standard_normal(shape)
+        s[rng.random(shape) < 0.2] = 0.0
+        s[rng.random(shape) < 0.1] = -0.0
+        s[rng.random(shape) < 0.001] = np.nan
+        s[rng.random(shape) < 0.001] = -np.nan
+    scores = s.astype(np.float32)
+    scores[0, :, 32:48] = -1e30  # a logical block evicted in every head
+    bt = rng.permutation(nb)[:N * M].reshape(N, M).astype(np.int32)
+    idx = rng.choice(M, M // 30, replace=False)
+    bt[1, idx] = bt[0, rng.permutation(idx)]  # pages shared by the two sequences
+    bt[rng.random(bt.shape) < 0.01] = -1
+    bt[rng.random(bt.shape) < 0.005] = nb + 5
+    ibf = np.zeros(nb, np.int32)
+    if fmt == "fp16":
+        kk, vv = memopt_C.get_pool_tensors()
+        before = {"format": fmt, "k": kk.cpu().numpy(), "v": vv.cpu().numpy()}
+    else:
+        before = {"format": fmt, "pages": memopt_C.get_int4_pages().cpu().numpy(), "D": D}
+    bt_d, ibf_d = to_dev(bt), to_dev(ibf)
+    memopt_C.evict_tokens(to_dev(scores), bt_d, ibf_d, r, sinks)
+    O.evict_tokens_intended(scores, bt, ibf, r, sinks, before, bs)
+    if fmt == "fp16":
+        kk, vv = memopt_C.get_pool_tensors()
+        same_bits(kk, before["k"])
+        same_bits(vv, before["v"])
+    else:
+        same_bits(memopt_C.get_int4_pages(), before["pages"])
+    same_bits(bt_d, bt)
+    same_bits(ibf_d, ibf)
+
+
 @pytest.mark.parametrize("seed", range(24))
 def test_decode_fp16_pool_sweep(seed):
     """Random decode shapes over fp16 page pools (16-, 32- and 64-token
