@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_helpers import assert_close, dev, memopt_C, same_bits, to_dev
+from gpu_helpers import assert_close, dev, memopt_C, same_bits, special_fp16, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -26,12 +26,18 @@ def _rows(rng, T, H, D, outlier=0.01):
     return x.astype(np.float16)
 
 
+@pytest.mark.parametrize("data", ["normal", "special"])
 @pytest.mark.parametrize("D", [64, 128])
-def test_dequantize_int4_pages_bit_exact(D):
+def test_dequantize_int4_pages_bit_exact(D, data):
+    """special: NaN of both signs, +-inf, -0, subnormals and +-65504."""
     rng = np.random.default_rng(D)
     nb, H = 7, 3
-    k = _rows(rng, nb * 16, H, D).reshape(nb, 16, H, D)
-    v = _rows(rng, nb * 16, H, D).reshape(nb, 16, H, D)
+    if data == "special":
+        k = special_fp16((nb * 16, H, D), 1).reshape(nb, 16, H, D)
+        v = special_fp16((nb * 16, H, D), 2).reshape(nb, 16, H, D)
+    else:
+        k = _rows(rng, nb * 16, H, D).reshape(nb, 16, H, D)
+        v = _rows(rng, nb * 16, H, D).reshape(nb, 16, H, D)
     pages = O.to_int4_pages(k, v)
     memopt_C.init_pool(nb, 16, H, D, kv_format="int4")
     kd, vd = memopt_C.dequantize_int4_pages(to_dev(pages))
@@ -40,15 +46,21 @@ def test_dequantize_int4_pages_bit_exact(D):
     same_bits(vd, wv)
 
 
-def test_convert_pool_round_trip_keeps_free_list():
+@pytest.mark.parametrize("data", ["normal", "special"])
+def test_convert_pool_round_trip_keeps_free_list(data):
+    """special: rows holding NaN of both signs, +-inf, -0, subnormals and
+    +-65504."""
     rng = np.random.default_rng(3)
     nb, H, D = 12, 2, 128
     memopt_C.init_pool(nb, 16, H, D, kv_format="fp16")
     taken = [memopt_C.allocate_block() for _ in range(5)]
     memopt_C.free_block(taken[1])
     before_free = memopt_C.free_blocks_count()
-    k = _rows(rng, nb * 16, H, D)
-    v = _rows(rng, nb * 16, H, D)
+    if data == "special":
+        k, v = special_fp16((nb * 16, H, D), 3), special_fp16((nb * 16, H, D), 4)
+    else:
+        k = _rows(rng, nb * 16, H, D)
+        v = _rows(rng, nb * 16, H, D)
     slots = torch.arange(nb * 16, dtype=torch.int32, device=dev())
     memopt_C.write_cache(to_dev(k), to_dev(v), to_dev(np.zeros((1, 1), np.int32)), slots)
     kp, vp = (t.cpu().numpy() for t in memopt_C.get_pool_tensors())
