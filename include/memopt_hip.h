@@ -259,15 +259,17 @@ int memopt_paged_attention(const memopt_attn_desc *desc, void *stream);
 
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory: code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc. Computes exactly what memopt_paged_attention computes for
- * the same descriptor (desc->workspace is ignored) and allocates nothing: the
+ * forbid hipMalloc. Computes what memopt_paged_attention computes for the
+ * same descriptor (desc->workspace is ignored) and allocates nothing: the
  * decode kernels' split-K partials, and the staged K/V of a multi-query call
  * when they fit, live in a static device array of
  * MEMOPT_NOALLOC_SCRATCH_BYTES (4 MiB) per GPU, held until the process ends;
  * its last 64 KiB hold the decode's arrival counters (zero at load, then
  * only ever counters) and the rest the partials or staged K/V.
- * Multi-query calls whose staging does not fit run the in-kernel staging
- * kernel, which needs no scratch. A decode whose partials exceed the rest
+ * Results are bit-identical to memopt_paged_attention's except for
+ * multi-query calls whose staging does not fit: those run the in-kernel
+ * staging kernel, which needs no scratch and agrees with the staged one to
+ * within fp16 attention tolerance, not bit for bit. A decode whose partials exceed the rest
  * (B * H * splits * (head_dim + 2) * 4 + 8 * B * H bytes; splits grow only
  * while B * H is below two workgroups per CU) returns MEMOPT_ERR_INVALID. Every call on
  * a GPU shares that GPU's array, so calls that overlap on one GPU (other

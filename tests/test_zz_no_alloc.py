@@ -102,6 +102,22 @@ def test_noalloc_decode_after_staged_prefill():
                      what="noalloc decode after a staged prefill")
 
 
+@pytest.mark.parametrize("B,H,D,ctx,Lq,causal", [(2, 4, 128, [3835, 696], 2, False),
+                                                 (3, 2, 64, [5243, 266, 2961], 120, True)])
+def test_noalloc_large_prefill_runs_unstaged(B, H, D, ctx, Lq, causal):
+    """A multi-query call whose staged K/V would not fit the static scratch
+    runs the kernel that dequantizes into LDS itself (no scratch): its output
+    and the regular entry point's (staged) are both within the tests'
+    tolerance of the oracle; they need not be bit-identical."""
+    case = _pages_case(11 + B, B, H, D, ctx, Lq)
+    got, want, ws_bytes = _run_both(case, 1 << 20, 1 << 20, 16, causal)
+    assert ws_bytes > (4 << 20)  # the staged workspace exceeds the scratch
+    q, pages, bt, cl = case
+    ref = O.paged_attention_int4(q, pages, bt, cl, 1 << 20, 1 << 20, num_sink_tokens=16, causal=causal)
+    assert_close(got, ref, what="noalloc (unstaged) prefill")
+    assert_close(want, ref, what="regular (staged) prefill")
+
+
 def test_noalloc_prepared_attention_and_limit():
     """PreparedAttention(no_alloc=True) holds no workspace and matches the
     regular call; partials past the scratch (forced splits) are refused."""
